@@ -1,0 +1,183 @@
+"""Benchmark of the Loopback depth-attention read on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--mode scores] [--no-cpu-baseline]
+
+A step is one pass of the read path over one batch: the K x R chain of BASELINE.json's configuration (default
+config 4: d=2048, K=4, R=8 -> N=32 updates, 31 reads, T = 8 x 2048 tokens, bf16 updates, fp32 scores), forward and
+backward -- N writes (with the read-query scores), N-1 reads, their backwards, the updates' gradients -- with the
+synthetic blocks x -> x + D_s and the caller's torch glue included. Inputs are resident in HBM before timing.
+
+Prints ONE JSON line (rank 0): the metric of BASELINE.json (read tokens/s = T * steps / wall time), plus
+  roofline      the dominant kernel: algorithmic bytes per launch (the traffic formula of the stacked dataflow, per
+                kernel family) / its mean launch duration, from HIP events on the launch stream, against 8 TB/s;
+  chain         the same over every library kernel of the pass (formula bytes * T / summed kernel time);
+  cpu_baseline  the CPU oracle (the restated reference read, fp32/bf16 torch on the host cores) on a bounded sample
+                of the same chain (T reduced), fwd+bwd, tokens/s.
+"""
+from __future__ import annotations
+
+import argparse
+import contextlib
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c4", choices=["c2", "c3", "c4"])
+    ap.add_argument("--mode", default="scores", choices=["scores", "stack", "list"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the CPU baseline sample")
+    return ap.parse_args()
+
+
+class KernelTimer:
+    """HIP events around every library call, on the current (launch) stream; summed per kernel family."""
+
+    def __init__(self):
+        self.events = []
+
+    @contextlib.contextmanager
+    def __call__(self, name):
+        import torch
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        yield
+        b.record()
+        self.events.append((name, a, b))
+
+    def summary(self):
+        import torch
+        torch.cuda.synchronize()
+        out = {}
+        for name, a, b in self.events:
+            ms = a.elapsed_time(b)
+            t = out.setdefault(name, [0, 0.0])
+            t[0] += 1
+            t[1] += ms
+        return {k: {"launches": v[0], "total_ms": v[1], "mean_us": 1e3 * v[1] / v[0]} for k, v in out.items()}
+
+
+def family_bytes(cfg, mode):
+    """Algorithmic bytes per pass (T tokens) of each kernel family, from the per-token formula."""
+    from loopback_amd.chain import algorithmic_bytes_per_token
+    e = 2 if str(cfg.dtype).endswith("bfloat16") else 4
+    parts = algorithmic_bytes_per_token(cfg.N, cfg.d, e, backward=cfg.backward, dots=(mode == "scores"))
+    T = cfg.n_tok
+    fam = {"write_dots": parts["write"] * T, "read_fwd": parts["read_fwd"] * T}
+    if cfg.backward:
+        fam["read_bwd1"] = parts["bwd1"] * T
+        fam["dv_assemble"] = (parts["bwd2"] + parts["rstd_bwd"]) * T   # this build forms dV once per update
+    return fam, parts["total"] * T
+
+
+def cpu_baseline(cfg, tokens):
+    """The oracle chain on the host cores, fwd(+bwd), on `tokens` tokens of the same configuration."""
+    import torch
+    from oracle.reference_read import run_chain
+    from loopback_amd.chain import make_inputs
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    h0, D, Q, G = make_inputs(cfg, "cpu", n_tok=tokens)
+    run_chain(cfg.K, cfg.R, h0, D, Q, G, beta=cfg.beta, eps=cfg.eps, grad=cfg.backward)   # warm-up
+    times, t_start = [], time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < 10 and len(times) < 50):
+        t0 = time.perf_counter()
+        run_chain(cfg.K, cfg.R, h0, D, Q, G, beta=cfg.beta, eps=cfg.eps, grad=cfg.backward)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 30:
+            break
+    med = statistics.median(times)
+    return {"value": tokens / med, "unit": "read-tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle chain (restated reference read, torch CPU) {cfg.name} with T={tokens} tokens, "
+                      f"{'fwd+bwd' if cfg.backward else 'fwd'}, median of {len(times)} runs, {med:.3f} s/run"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the read shards by tokens "
+              "across GPUs as described in DESIGN.md, but no multi-GPU figure is produced", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(3)
+    from loopback_amd import fused_dattn as FD
+    from loopback_amd.chain import CONFIGS, make_inputs, run_chain
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    h0, D, Q, G = make_inputs(cfg, dev)
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        run_chain(cfg, h0, D, Q, G, args.mode)
+    torch.cuda.synchronize()
+    timer = KernelTimer()
+    t0 = time.perf_counter()
+    for step in range(args.steps):
+        if step == args.steps - 1:
+            FD._TIMER = timer      # the last timed step: every library kernel bracketed by events on its stream
+        run_chain(cfg, h0, D, Q, G, args.mode)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    FD._TIMER = None
+    ms_per_step = 1e3 * elapsed / args.steps
+    ksum = timer.summary()
+    fam, total_bytes = family_bytes(cfg, args.mode)
+    dom = max((k for k in fam if k in ksum), key=lambda k: ksum[k]["total_ms"])
+    launches = ksum[dom]["launches"]
+    bytes_per_launch = fam[dom] / launches
+    mean_s = ksum[dom]["mean_us"] * 1e-6
+    achieved = bytes_per_launch / mean_s / 1e9
+    kernel_ms = sum(v["total_ms"] for v in ksum.values())
+    traffic = None
+    tr_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"traffic_{dom}_{args.config}.json")
+    if os.path.exists(tr_path):
+        with open(tr_path) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": "depth-read tokens/sec (fwd+bwd), d=2048, N=32 stack" if cfg.backward else
+                  f"depth-read tokens/sec (fwd), {cfg.name}",
+        "value": cfg.n_tok * args.steps / elapsed,
+        "unit": "read-tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (seeded N(0,1) updates and h0, N(0,0.02^2) queries; blocks x -> x + D_s)",
+        "config": {"workload": cfg.name, "d": cfg.d, "K": cfg.K, "R": cfg.R, "N": cfg.N, "tokens": cfg.n_tok,
+                   "mode": args.mode, "backward": cfg.backward, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "algorithmic_bytes_per_launch": bytes_per_launch, "mean_launch_us": ksum[dom]["mean_us"],
+                     "launches_per_step": launches},
+        "chain": {"algorithmic_bytes_per_token": total_bytes / cfg.n_tok, "kernel_ms": kernel_ms,
+                  "achieved_gbs": total_bytes / (kernel_ms * 1e-3) / 1e9,
+                  "wall_gbs": total_bytes / (ms_per_step * 1e-3) / 1e9,
+                  "kernels": {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 4),
+                                  "gbs": (fam[k] / (v["total_ms"] * 1e-3) / 1e9) if k in fam else None}
+                              for k, v in sorted(ksum.items())}},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

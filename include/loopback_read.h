@@ -1,0 +1,123 @@
+/*
+ * loopback_read.h -- C ABI of libloopback_read.so, the MI355X (gfx950) kernels of the Loopback depth-attention
+ * read ("delta_attnres"): the write step, the read step (scores stored at write time, or computed online), the
+ * backward and the RMS-scale gradient.
+ *
+ * Conventions (every entry point):
+ *   - device pointers are plain addresses of device memory; tensors are row-major and contiguous, one row of d
+ *     elements per token; every vector pointer (updates, h, x, base, out, g, dv, q rows) is 16-byte aligned;
+ *   - n_tok = b * t tokens, d the width (a multiple of 8, at most LDR_MAX_WIDTH);
+ *   - dtype is LDR_F32 or LDR_BF16 and applies to the update-shaped tensors (updates, base, out, g, dv, h, x);
+ *     every scale, score, coefficient and gradient scalar is fp32;
+ *   - per-source arrays (src_v, src_r, ...) are HOST arrays of n device addresses, copied into the kernel
+ *     arguments (no device pointer table, no host-to-device copy); n <= LDR_MAX_SOURCES;
+ *   - stream is a hipStream_t; nothing synchronizes with the host, nothing allocates device memory;
+ *   - the return value is 0, a negative LDR_E_* code (rejected before any launch), or a positive hipError_t
+ *     from the launch; ldr_strerror() names it.
+ * The reference's Python module launches Triton kernels; the entry points below replace those launches one for one
+ * (file:line into yancyou/Loopback's fused_dattn.py).
+ */
+#ifndef LOOPBACK_READ_H
+#define LOOPBACK_READ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LDR_F32 0
+#define LDR_BF16 1
+
+#define LDR_MAX_SOURCES 64
+#define LDR_MAX_WIDTH 8192
+#define LDR_MAX_QUERIES 64
+
+#define LDR_OK 0
+#define LDR_E_ARG (-1)    /* null pointer, negative size, bad flag */
+#define LDR_E_SHAPE (-2)  /* d not a multiple of 8 or too wide; n or nq out of range */
+#define LDR_E_ALIGN (-3)  /* a vector pointer is not 16-byte aligned */
+#define LDR_E_DTYPE (-4)  /* dtype is neither LDR_F32 nor LDR_BF16 */
+
+/* Version of this ABI; bumped on any signature change. */
+int ldr_abi_version(void);
+
+/* Human-readable text for a return code of any entry point (static storage). */
+const char* ldr_strerror(int code);
+
+/* The row layout the kernels use for width d: each row of d/8 eight-element vectors is covered by *tpr lanes
+ * holding *vpt vectors each. Exposed for tests; returns LDR_E_SHAPE for an unsupported d. */
+int ldr_row_layout(int64_t d, int* vpt, int* tpr);
+
+/* Number of dq partial rows ldr_read_bwd1 writes for (n_tok, d): the caller allocates parts * d fp32. */
+int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d);
+
+/* r[tok] = rsqrt(sum_k x[tok,k]^2 / d + eps).
+ * Replaces _rstd_fwd_kernel and its launches (fused_dattn.py:206-215, 240, 705). */
+int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream);
+
+/* gx[tok,:] = gr[tok] * (-r[tok]^3) / d * x[tok,:], rounded to dtype.
+ * Replaces _rstd_bwd_kernel (fused_dattn.py:218-229, 252). */
+int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
+                 void* stream);
+
+/* The write step of update s: v_out = round(h - x); r_out[tok] = rsqrt(mean(v_out^2) + eps) of the rounded
+ * update; for jj < nq: dots[jj * dots_jstride + tok] = q[jj, :] . v_out[tok, :] (fp32), where q points at the
+ * first query row needed and dots at that query's score slice for source s (nq = 0: no scores).
+ * Replaces _write_stk_kernel (fused_dattn.py:561-585, launched at 684-687). */
+int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, float* dots,
+                   int64_t n_tok, int64_t d, int64_t nq, int64_t dots_jstride, float eps, int dtype, void* stream);
+
+/* Online scores: out[i * out_stride + tok] = q . v_i[tok, :] for the n sources (fp32). Together with
+ * ldr_read_fwd it is the read without stored scores (replaces the score half of _dattn_fwd_stk_kernel,
+ * fused_dattn.py:410-456, and of the list layout's _dattn_fwd_kernel, 55-108). */
+int ldr_dots_online(const uint64_t* src_v, int64_t n, const float* q, float* out, int64_t out_stride,
+                    int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* The read step over n sources from their raw scores dots[i * dots_stride + tok] = q . v_i:
+ *   l_i = dots_i * r_i * inv_sqrt_d + log(max(c0_i, 1e-8));  lse = logsumexp_i l_i;  lse0 = logsumexp_i lc_i
+ *   tc_i = c0_i + M (exp(l_i - lse) - exp(lc_i - lse0)),  M = sum_i c0_i
+ *   out = round(base + sum_i (tc_i - cbar_i) v_i)   (fp32 accumulation, one rounding)
+ * and stores tc [n_tok, n], the logits lg [n_tok, n] and lse [n_tok] for the backward. c0 is a device array of n.
+ * Replaces _dattn_fwd_dots_kernel (fused_dattn.py:588-625, launched at 748-751) and the weighted-sum half of
+ * _dattn_fwd_stk_kernel / _dattn_fwd_kernel (410-456 / 55-108). */
+int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* dots, int64_t dots_stride,
+                 const void* base, const float* cbar, const float* c0, float inv_sqrt_d, void* out, float* tc,
+                 float* lg, float* lse, int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* Backward pass 1 of a read (the only re-read of the sources), with g = dL/dout and gt = dL/dtc (NULL = zeros):
+ *   gd_i = g . v_i,  gp_i = M (gd_i + gt_i),  Sacc = sum_i p_i gp_i,  dz_i = p_i (gp_i - Sacc)
+ *   dcbar[tok, i] = -gd_i;  dr_i[tok] (+)= dz_i (l_i - lc_i) / r_i   (added when dr_accum != 0)
+ *   wz[(i * wz_stride + tok) * 2 + {0,1}] = (tc_i - cbar_i, dz_i r_i inv_sqrt_d)   (the pass-2 scalars)
+ *   dq_part[p, :] = per-workgroup partial of sum_tok sum_i dz_i r_i v_i inv_sqrt_d  (ldr_read_bwd1_parts rows)
+ * Replaces _dattn_bwd1_stk_kernel (fused_dattn.py:459-493, launched at 777-779) and pass 1 of _dattn_bwd_kernel
+ * (111-151); dr is also the dR update of _dattn_bwd2_stk_kernel (532-535). */
+int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const void* g, const float* gt,
+                  const float* lg, const float* lse, const float* tc, const float* cbar, const float* c0,
+                  float inv_sqrt_d, float* dcbar, const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride,
+                  float* dq_part, int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* out[c] = sum_p part[p * d + c] in a fixed order (deterministic).
+ * Replaces the torch dq_part.sum(0) (fused_dattn.py:317, 785). */
+int ldr_reduce_rows(const float* part, int64_t rows, int64_t d, float* out, void* stream);
+
+/* Backward pass 2 of the list layout: dv_i = w_i g + dzr_i q (w, dzr from ldr_read_bwd1's wz), written to the
+ * n per-source gradient tensors, or added (accum != 0) as prev + round(dv_i), rounded again: autograd's own
+ * accumulation of per-read gradients. Replaces pass 2 of _dattn_bwd_kernel (fused_dattn.py:152-181). */
+int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, const float* q, const float* wz,
+                       int64_t wz_stride, int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* The stacked layout's gradient of update i, formed once after every read of it has run its backward:
+ *   dv[tok,:] = round( sum_e ( w_e[tok] g_e[tok,:] + dzr_e[tok] q_e[:] ) + gr[tok] (-r[tok]^3) / d * v[tok,:] )
+ * over the m reads e that hold update i: g_e that read's output gradient, (w_e, dzr_e) its wz pair for source i
+ * (float2 per token), q_e its query (fp32, d). One fp32 sum, one rounding.
+ * Replaces the dV read-modify-write of _dattn_bwd2_stk_kernel (fused_dattn.py:496-536, launched at 781-784) and
+ * _rstd_bwd_acc_kernel (539-552, launched at 717-719). */
+int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
+                    const float* r, const float* gr, void* dv, int64_t n_tok, int64_t d, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOOPBACK_READ_H */

@@ -1,0 +1,1066 @@
+// loopback_read.hip -- MI355X (gfx950, CDNA4) kernels of the Loopback depth-attention read.
+//
+// One read at destination s has n = s + 1 sources v_i (bf16 or fp32 updates, one row of d elements per token) and
+// per-token fp32 RMS scales r_i. Every kernel here is HBM-bound streaming over token rows; the design rules are:
+//   * a row of d elements is d/8 sixteen-byte (bf16) vectors, covered by `tpr` lanes holding `vpt` vectors each
+//     (ldr_row_layout); 256-lane workgroups hold 256/tpr rows side by side, so any d that is a multiple of 8 runs
+//     without padding the row to a power of two;
+//   * per-(token, source) scalars (scores, probabilities, weights) are staged through LDS per tile of tokens with
+//     coalesced loads, then broadcast to the lanes of a row;
+//   * row reductions are 64-wide wavefront butterflies, plus one LDS exchange when a row spans several waves;
+//   * every sum is fp32 in a fixed order (no atomics): results are deterministic run to run.
+// Sources are reached through per-source addresses passed by value in the kernel arguments, so the stacked
+// layout (slices of one tensor) and the list layout (one tensor per source) share the kernels.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <math.h>
+
+#include "loopback_read.h"
+
+namespace {
+
+constexpr int WG = 256;                 // lanes per workgroup (4 wave64s)
+constexpr int MAXS = LDR_MAX_SOURCES;
+constexpr int TT_MAX = 32;              // tokens per tile in the tiled kernels
+constexpr int SP = MAXS + 1;            // padded LDS row of per-source scalars
+
+typedef uint16_t bf16_t;                // bf16 storage (raw bits)
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+struct SrcTab { const void* v[MAXS]; const float* r[MAXS]; };
+struct PtrTab { void* p[MAXS]; };
+struct AsmTab { const void* g[MAXS]; const float* wz[MAXS]; const float* q[MAXS]; };
+
+// ---------------------------------------------------------------------------------------------------------------
+// element I/O: 8 elements (one 16-byte bf16 vector, or two fp32 float4) <-> 8 fp32 registers
+// ---------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  // v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN
+  bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+template <typename T> struct IO;
+
+template <> struct IO<bf16_t> {
+  struct Raw { uint4 u; };
+  static __device__ __forceinline__ Raw raw(const bf16_t* p) { Raw r; r.u = *reinterpret_cast<const uint4*>(p); return r; }
+  static __device__ __forceinline__ Raw zero() { Raw r; r.u = make_uint4(0u, 0u, 0u, 0u); return r; }
+  static __device__ __forceinline__ void unpack(const Raw& r, float (&o)[8]) {
+    o[0] = __uint_as_float(r.u.x << 16); o[1] = __uint_as_float(r.u.x & 0xffff0000u);
+    o[2] = __uint_as_float(r.u.y << 16); o[3] = __uint_as_float(r.u.y & 0xffff0000u);
+    o[4] = __uint_as_float(r.u.z << 16); o[5] = __uint_as_float(r.u.z & 0xffff0000u);
+    o[6] = __uint_as_float(r.u.w << 16); o[7] = __uint_as_float(r.u.w & 0xffff0000u);
+  }
+  static __device__ __forceinline__ void load(const bf16_t* p, float (&o)[8]) { unpack(raw(p), o); }
+  static __device__ __forceinline__ void store(bf16_t* p, const float (&o)[8]) {
+    uint4 u;
+    u.x = pack2(o[0], o[1]); u.y = pack2(o[2], o[3]); u.z = pack2(o[4], o[5]); u.w = pack2(o[6], o[7]);
+    *reinterpret_cast<uint4*>(p) = u;
+  }
+  static __device__ __forceinline__ float round(float x) { return (float)(__bf16)x; }
+};
+
+template <> struct IO<float> {
+  struct Raw { float4 a, b; };
+  static __device__ __forceinline__ Raw raw(const float* p) {
+    Raw r; r.a = reinterpret_cast<const float4*>(p)[0]; r.b = reinterpret_cast<const float4*>(p)[1]; return r;
+  }
+  static __device__ __forceinline__ Raw zero() { Raw r; r.a = make_float4(0.f, 0.f, 0.f, 0.f); r.b = r.a; return r; }
+  static __device__ __forceinline__ void unpack(const Raw& r, float (&o)[8]) {
+    o[0] = r.a.x; o[1] = r.a.y; o[2] = r.a.z; o[3] = r.a.w; o[4] = r.b.x; o[5] = r.b.y; o[6] = r.b.z; o[7] = r.b.w;
+  }
+  static __device__ __forceinline__ void load(const float* p, float (&o)[8]) { unpack(raw(p), o); }
+  static __device__ __forceinline__ void store(float* p, const float (&o)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(o[0], o[1], o[2], o[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(o[4], o[5], o[6], o[7]);
+  }
+  static __device__ __forceinline__ float round(float x) { return x; }
+};
+
+__device__ __forceinline__ void load_f32x8(const float* p, float (&o)[8]) { IO<float>::load(p, o); }
+
+// ---------------------------------------------------------------------------------------------------------------
+// row geometry and reductions
+// ---------------------------------------------------------------------------------------------------------------
+struct Rows {
+  int d8, tpr, rpw, rs, lr;
+  __device__ __forceinline__ Rows(int d, int tpr_)
+      : d8(d >> 3), tpr(tpr_), rpw(WG / tpr_), rs((int)threadIdx.x / tpr_), lr((int)threadIdx.x % tpr_) {}
+  __device__ __forceinline__ int c8(int v) const { return lr + v * tpr; }
+};
+
+// Sum NV values over the tpr lanes of a row (tpr a power of two); every lane of the row ends with the totals,
+// bitwise equal on all of them. tpr <= 64: the row is an aligned lane group of one wave. tpr > 64: the row spans
+// tpr/64 waves and the wave totals meet in `red` (4 * NV floats of LDS); the whole workgroup must then call
+// together (barriers inside).
+template <int NV>
+__device__ __forceinline__ void row_sum(float (&x)[NV], int tpr, float* red) {
+  const int w = tpr < 64 ? tpr : 64;
+  for (int off = w >> 1; off > 0; off >>= 1) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) x[j] += __shfl_xor(x[j], off, 64);
+  }
+  if (tpr > 64) {
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) red[wave * NV + j] = x[j];
+    }
+    __syncthreads();
+    const int nw = tpr >> 6, first = (wave / nw) * nw;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float s = 0.f;
+      for (int k = 0; k < nw; ++k) s += red[(first + k) * NV + j];
+      x[j] = s;
+    }
+  }
+}
+
+// logsumexp of a token's n logits held by `lpt` aligned lanes (up to 8 each; unused slots are -inf): every lane
+// returns the same value. One code path for the scored and the prior-only logits, so equal inputs give bitwise
+// equal results (the zero-query identity tc == c0, out == base).
+__device__ __forceinline__ float lse_lanes(const float (&l)[8], int lpt) {
+  float mx = l[0];
+#pragma unroll
+  for (int m = 1; m < 8; ++m) mx = fmaxf(mx, l[m]);
+  for (int off = lpt >> 1; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float s = 0.f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) s += (l[m] == -INFINITY) ? 0.f : expf(l[m] - mx);
+  for (int off = lpt >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  return mx + logf(s);
+}
+
+// per-read constants from the prior c0 (n floats on the device): c0, lc = log(max(c0, 1e-8)), M = sum c0
+__device__ __forceinline__ void load_prior(const float* __restrict__ c0, int n, float* s_c0, float* s_lc, float* s_M) {
+  const int t = (int)threadIdx.x;
+  if (t < n) {
+    const float c = c0[t];
+    s_c0[t] = c;
+    s_lc[t] = logf(fmaxf(c, 1e-8f));
+  }
+  if (t == 0) {
+    float m = 0.f;
+    for (int i = 0; i < n; ++i) m += c0[i];
+    *s_M = m;
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// rstd forward / backward (list layout, and the stacked layout's scale when the write did not store it)
+// ---------------------------------------------------------------------------------------------------------------
+template <typename T, int VPT>
+__global__ __launch_bounds__(WG) void k_rstd_fwd(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
+                                                 int d, int tpr, float eps) {
+  __shared__ float red[4];
+  const Rows R(d, tpr);
+  const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
+  for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
+    const int64_t tok = gi * R.rpw + R.rs;
+    float ss[1] = {0.f};
+    if (tok < n_tok) {
+      const T* row = x + tok * (int64_t)d;
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        const int c8 = R.c8(v);
+        if (c8 < R.d8) {
+          float e[8];
+          IO<T>::load(row + c8 * 8, e);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) ss[0] += e[k] * e[k];
+        }
+      }
+    }
+    row_sum<1>(ss, tpr, red);
+    if (tok < n_tok && R.lr == 0) r[tok] = rsqrtf(ss[0] / (float)d + eps);
+  }
+}
+
+template <typename T, int VPT>
+__global__ __launch_bounds__(WG) void k_rstd_bwd(const T* __restrict__ x, const float* __restrict__ r,
+                                                 const float* __restrict__ gr, T* __restrict__ gx, int64_t n_tok,
+                                                 int d, int tpr) {
+  const Rows R(d, tpr);
+  const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
+  for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
+    const int64_t tok = gi * R.rpw + R.rs;
+    if (tok >= n_tok) continue;
+    const float rv = r[tok];
+    const float c = gr[tok] * (-rv * rv * rv) / (float)d;
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+      const int c8 = R.c8(v);
+      if (c8 < R.d8) {
+        float e[8];
+        IO<T>::load(x + tok * (int64_t)d + c8 * 8, e);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = c * e[k];
+        IO<T>::store(gx + tok * (int64_t)d + c8 * 8, e);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// write step: V[s] = round(h - x), R[s] from the rounded update, scores against the later read queries.
+// A tile of 32 tokens streams d in chunks of 128 columns: the chunk of the update goes to LDS (fp32) next to the
+// chunk of up to 64 query rows, and 256 lanes form the 32 x nq dot products (lane = token + 32 * query group).
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int WR_TT = 32, WR_KC = 128, WR_KP = WR_KC + 4, WR_MQ = 8;
+
+template <typename T>
+__global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, const T* __restrict__ x,
+                                                   T* __restrict__ v, float* __restrict__ r,
+                                                   const float* __restrict__ q, float* __restrict__ dots,
+                                                   int64_t n_tok, int d, int nq, int64_t dots_jstride, float eps) {
+  __shared__ float sv[WR_TT * WR_KP];
+  __shared__ float sq[LDR_MAX_QUERIES * WR_KP];
+  const int tid = (int)threadIdx.x;
+  const int64_t t0 = (int64_t)blockIdx.x * WR_TT;
+  const int tc = tid & 31, jg = tid >> 5;
+  const int mq = (nq + 7) >> 3;
+  float acc[WR_MQ];
+#pragma unroll
+  for (int m = 0; m < WR_MQ; ++m) acc[m] = 0.f;
+  float ss[2] = {0.f, 0.f};
+  for (int c0 = 0; c0 < d; c0 += WR_KC) {
+    // the update chunk: 32 rows x 16 vectors, two vectors per lane
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int u = tid + WG * e, row = u >> 4, col = c0 + (u & 15) * 8;
+      const int64_t tok = t0 + row;
+      float vv[8];
+      if (tok < n_tok && col < d) {
+        float hv[8], xv[8];
+        IO<T>::load(h + tok * (int64_t)d + col, hv);
+        IO<T>::load(x + tok * (int64_t)d + col, xv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) vv[k] = IO<T>::round(hv[k] - xv[k]);
+        IO<T>::store(v + tok * (int64_t)d + col, vv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss[e] += vv[k] * vv[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) vv[k] = 0.f;
+      }
+      float4* dst = reinterpret_cast<float4*>(&sv[row * WR_KP + (u & 15) * 8]);
+      dst[0] = make_float4(vv[0], vv[1], vv[2], vv[3]);
+      dst[1] = make_float4(vv[4], vv[5], vv[6], vv[7]);
+    }
+    // the query chunk: nq rows x 32 float4
+    for (int idx = tid; idx < nq * (WR_KC / 4); idx += WG) {
+      const int jj = idx >> 5, col = c0 + (idx & 31) * 4;
+      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (col < d) val = *reinterpret_cast<const float4*>(q + (int64_t)jj * d + col);
+      *reinterpret_cast<float4*>(&sq[jj * WR_KP + (idx & 31) * 4]) = val;
+    }
+    __syncthreads();
+    if (nq > 0) {
+      const int kend = (d - c0) < WR_KC ? (d - c0) : WR_KC;
+      for (int k = 0; k < kend; k += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(&sv[tc * WR_KP + k]);
+#pragma unroll
+        for (int m = 0; m < WR_MQ; ++m) {
+          if (m < mq) {
+            const float4 b = *reinterpret_cast<const float4*>(&sq[(jg + 8 * m) * WR_KP + k]);
+            acc[m] += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // the scale: 16 lanes per row, rows tid/16 and tid/16 + 16
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    for (int off = 8; off > 0; off >>= 1) ss[e] += __shfl_xor(ss[e], off, 64);
+    const int64_t tok = t0 + (tid >> 4) + 16 * e;
+    if ((tid & 15) == 0 && tok < n_tok) r[tok] = rsqrtf(ss[e] / (float)d + eps);
+  }
+  const int64_t tok = t0 + tc;
+  if (tok < n_tok) {
+#pragma unroll
+    for (int m = 0; m < WR_MQ; ++m) {
+      const int jj = jg + 8 * m;
+      if (m < mq && jj < nq) dots[(int64_t)jj * dots_jstride + tok] = acc[m];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// online scores: out[i][tok] = q . v_i[tok]  (the read without a stored score table)
+// ---------------------------------------------------------------------------------------------------------------
+template <typename T, int VPT, int C>
+__global__ __launch_bounds__(WG) void k_dots(SrcTab src, int n, const float* __restrict__ q, float* __restrict__ out,
+                                             int64_t out_stride, int64_t n_tok, int d, int tpr) {
+  __shared__ float red[4 * C];
+  const Rows R(d, tpr);
+  float qv[VPT][8];
+#pragma unroll
+  for (int v = 0; v < VPT; ++v) {
+    const int c8 = R.c8(v);
+    if (c8 < R.d8) load_f32x8(q + c8 * 8, qv[v]);
+    else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) qv[v][k] = 0.f;
+    }
+  }
+  const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
+  for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
+    const int64_t tok = gi * R.rpw + R.rs;
+    const bool valid = tok < n_tok;
+    for (int i0 = 0; i0 < n; i0 += C) {
+      typename IO<T>::Raw raw[C][VPT];
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          const int c8 = R.c8(v);
+          if (valid && i0 + c < n && c8 < R.d8)
+            raw[c][v] = IO<T>::raw(static_cast<const T*>(src.v[i0 + c]) + tok * (int64_t)d + c8 * 8);
+          else
+            raw[c][v] = IO<T>::zero();
+        }
+      }
+      float pd[C];
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        pd[c] = 0.f;
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          float e[8];
+          IO<T>::unpack(raw[c][v], e);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) pd[c] += qv[v][k] * e[k];
+        }
+      }
+      row_sum<C>(pd, tpr, red);
+      if (valid && R.lr == 0) {
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+          if (i0 + c < n) out[(int64_t)(i0 + c) * out_stride + tok] = pd[c];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// read forward: softmax weights from the raw scores, then out = base + sum_i w_i v_i in one pass over the sources
+// ---------------------------------------------------------------------------------------------------------------
+template <typename T, int VPT>
+__global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float* __restrict__ dots, int64_t dots_stride,
+                                                 const T* __restrict__ base, const float* __restrict__ cbar,
+                                                 const float* __restrict__ c0, float inv, T* __restrict__ out,
+                                                 float* __restrict__ tc, float* __restrict__ lg,
+                                                 float* __restrict__ lse_out, int64_t n_tok, int d, int tpr, int tt) {
+  __shared__ float s_l[MAXS * (TT_MAX + 1)];   // logits [i][t]
+  __shared__ float s_w[TT_MAX * SP];           // cbar, then the weights [t][i]
+  __shared__ float s_c0[MAXS], s_lc[MAXS], s_M;
+  const Rows R(d, tpr);
+  const int tid = (int)threadIdx.x;
+  load_prior(c0, n, s_c0, s_lc, &s_M);
+  const float M = s_M;
+  const int lpt = WG / tt;   // lanes per token in the softmax
+  const int64_t tiles = (n_tok + tt - 1) / tt;
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t t0 = tile * tt;
+    for (int idx = tid; idx < n * tt; idx += WG) {   // source-major: coalesced over tokens
+      const int i = idx / tt, t = idx - i * tt;
+      const int64_t tok = t0 + t;
+      float l = s_lc[i];
+      if (tok < n_tok) l = dots[(int64_t)i * dots_stride + tok] * src.r[i][tok] * inv + s_lc[i];
+      s_l[i * (TT_MAX + 1) + t] = l;
+    }
+    for (int idx = tid; idx < n * tt; idx += WG) {   // token-major: coalesced over [tok][i]
+      const int t = idx / n, i = idx - t * n;
+      const int64_t tok = t0 + t;
+      s_w[t * SP + i] = tok < n_tok ? cbar[tok * n + i] : 0.f;
+    }
+    __syncthreads();
+    {
+      const int t = tid / lpt, j = tid - t * lpt;
+      const int64_t tok = t0 + t;
+      float ls[8], l0[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const int i = j + m * lpt;
+        ls[m] = (i < n) ? s_l[i * (TT_MAX + 1) + t] : -INFINITY;
+        l0[m] = (i < n) ? s_lc[i] : -INFINITY;
+      }
+      const float lse = lse_lanes(ls, lpt);
+      const float lse0 = lse_lanes(l0, lpt);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const int i = j + m * lpt;
+        if (i < n) {
+          const float p = expf(ls[m] - lse), p0 = expf(l0[m] - lse0);
+          const float tcv = s_c0[i] + M * (p - p0);
+          s_w[t * SP + i] = tcv - s_w[t * SP + i];
+          if (tok < n_tok) {
+            tc[tok * n + i] = tcv;
+            lg[tok * n + i] = ls[m];
+          }
+        }
+      }
+      if (j == 0 && tok < n_tok) lse_out[tok] = lse;
+    }
+    __syncthreads();
+    for (int rr = R.rs; rr < tt; rr += R.rpw) {
+      const int64_t tok = t0 + rr;
+      if (tok >= n_tok) break;
+      const float* wrow = &s_w[rr * SP];
+      float acc[VPT][8];
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        const int c8 = R.c8(v);
+        if (c8 < R.d8) IO<T>::load(base + tok * (int64_t)d + c8 * 8, acc[v]);
+      }
+      int i = 0;
+      for (; i + 4 <= n; i += 4) {
+        typename IO<T>::Raw raw[4][VPT];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) {
+            const int c8 = R.c8(v);
+            if (c8 < R.d8) raw[u][v] = IO<T>::raw(static_cast<const T*>(src.v[i + u]) + tok * (int64_t)d + c8 * 8);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float w = wrow[i + u];
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) {
+            if (R.c8(v) < R.d8) {
+              float e[8];
+              IO<T>::unpack(raw[u][v], e);
+#pragma unroll
+              for (int k = 0; k < 8; ++k) acc[v][k] += w * e[k];
+            }
+          }
+        }
+      }
+      for (; i < n; ++i) {
+        const float w = wrow[i];
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          const int c8 = R.c8(v);
+          if (c8 < R.d8) {
+            float e[8];
+            IO<T>::load(static_cast<const T*>(src.v[i]) + tok * (int64_t)d + c8 * 8, e);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[v][k] += w * e[k];
+          }
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        const int c8 = R.c8(v);
+        if (c8 < R.d8) IO<T>::store(out + tok * (int64_t)d + c8 * 8, acc[v]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// backward pass 1: the only re-read of the sources
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int B1_GRID = 512;
+constexpr int B1_MAX_VPT = 2;   // k_bwd1 holds g and two fp32 accumulators per element
+
+template <typename T, int VPT, int C>
+__global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restrict__ g, const float* __restrict__ gt,
+                                             const float* __restrict__ lg, const float* __restrict__ lse,
+                                             const float* __restrict__ tcp, const float* __restrict__ cbar,
+                                             const float* __restrict__ c0, float inv, float* __restrict__ dcbar,
+                                             PtrTab dr, int dr_accum, float* __restrict__ wz, int64_t wz_stride,
+                                             float* __restrict__ dq_part, int64_t n_tok, int d, int tpr, int tt) {
+  // LDS: six [TT_MAX][SP] scalar planes (probability, scale, upstream tc gradient, g.v, dz, raw logit) during
+  // the tiles; the first d floats are reused for the workgroup's dq sum at the end.
+  __shared__ float lds[6 * TT_MAX * SP];
+  __shared__ float s_sacc[TT_MAX], s_c0[MAXS], s_lc[MAXS], s_M, red[4 * C];
+  float* s_p = lds;
+  float* s_r = lds + 1 * TT_MAX * SP;
+  float* s_gt = lds + 2 * TT_MAX * SP;
+  float* s_gd = lds + 3 * TT_MAX * SP;
+  float* s_dz = lds + 4 * TT_MAX * SP;
+  float* s_w = lds + 5 * TT_MAX * SP;
+  const Rows R(d, tpr);
+  const int tid = (int)threadIdx.x;
+  load_prior(c0, n, s_c0, s_lc, &s_M);
+  const float M = s_M;
+  float dqa[VPT][8];
+#pragma unroll
+  for (int v = 0; v < VPT; ++v)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dqa[v][k] = 0.f;
+  const int64_t tiles = (n_tok + tt - 1) / tt;
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t t0 = tile * tt;
+    for (int idx = tid; idx < n * tt; idx += WG) {   // token-major scalars
+      const int t = idx / n, i = idx - t * n;
+      const int64_t tok = t0 + t;
+      float p = 0.f, gtv = 0.f, w = 0.f, l = 0.f;
+      if (tok < n_tok) {
+        l = lg[tok * n + i];
+        p = expf(l - lse[tok]);
+        if (gt) gtv = gt[tok * n + i];
+        w = tcp[tok * n + i] - cbar[tok * n + i];
+      }
+      s_p[t * SP + i] = p;
+      s_gt[t * SP + i] = gtv;
+      s_w[t * SP + i] = w;
+      s_dz[t * SP + i] = l;   // the raw logit until the epilogue replaces it by dz
+    }
+    for (int idx = tid; idx < n * tt; idx += WG) {   // source-major scales
+      const int i = idx / tt, t = idx - i * tt;
+      const int64_t tok = t0 + t;
+      s_r[t * SP + i] = tok < n_tok ? src.r[i][tok] : 1.f;
+    }
+    __syncthreads();
+    const int rows_per_slot = (tt + R.rpw - 1) / R.rpw;
+    for (int rk = 0; rk < rows_per_slot; ++rk) {   // uniform trip count: row_sum may hold barriers
+      const int rr = R.rs + rk * R.rpw;
+      const int64_t tok = t0 + rr;
+      const bool valid = rr < tt && tok < n_tok;
+      float gv[VPT][8];
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        const int c8 = R.c8(v);
+        if (valid && c8 < R.d8) IO<T>::load(g + tok * (int64_t)d + c8 * 8, gv[v]);
+        else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) gv[v][k] = 0.f;
+        }
+      }
+      float a[VPT][8], b[VPT][8];
+#pragma unroll
+      for (int v = 0; v < VPT; ++v)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) { a[v][k] = 0.f; b[v][k] = 0.f; }
+      float sacc = 0.f;
+      for (int i0 = 0; i0 < n; i0 += C) {
+        typename IO<T>::Raw raw[C][VPT];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) {
+            const int c8 = R.c8(v);
+            if (valid && i0 + c < n && c8 < R.d8)
+              raw[c][v] = IO<T>::raw(static_cast<const T*>(src.v[i0 + c]) + tok * (int64_t)d + c8 * 8);
+            else
+              raw[c][v] = IO<T>::zero();
+          }
+        }
+        float pd[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          pd[c] = 0.f;
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) {
+            float e[8];
+            IO<T>::unpack(raw[c][v], e);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) pd[c] += gv[v][k] * e[k];
+          }
+        }
+        row_sum<C>(pd, tpr, red);
+        if (valid) {
+#pragma unroll
+          for (int c = 0; c < C; ++c) {
+            const int i = i0 + c;
+            if (i < n) {
+              const float gd = pd[c];
+              const float p = s_p[rr * SP + i];
+              const float pr = p * s_r[rr * SP + i];
+              const float gp = M * (gd + s_gt[rr * SP + i]);
+              sacc += p * gp;
+              const float alpha = pr * gp;
+#pragma unroll
+              for (int v = 0; v < VPT; ++v) {
+                float e[8];
+                IO<T>::unpack(raw[c][v], e);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                  a[v][k] += alpha * e[k];
+                  b[v][k] += pr * e[k];
+                }
+              }
+              if (R.lr == 0) s_gd[rr * SP + i] = gd;
+            }
+          }
+        }
+      }
+      if (valid) {
+#pragma unroll
+        for (int v = 0; v < VPT; ++v)
+#pragma unroll
+          for (int k = 0; k < 8; ++k) dqa[v][k] += a[v][k] - sacc * b[v][k];
+        if (R.lr == 0) s_sacc[rr] = sacc;
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < n * tt; idx += WG) {   // token-major: dcbar, dz
+      const int t = idx / n, i = idx - t * n;
+      const int64_t tok = t0 + t;
+      if (tok < n_tok) {
+        const float gd = s_gd[t * SP + i];
+        const float gp = M * (gd + s_gt[t * SP + i]);
+        const float dz = s_p[t * SP + i] * (gp - s_sacc[t]);
+        dcbar[tok * n + i] = -gd;
+        s_dz[t * SP + i] = dz * (s_dz[t * SP + i] - s_lc[i]) / s_r[t * SP + i];   // drstd, logit -> dz z / r
+        s_gd[t * SP + i] = dz;
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < n * tt; idx += WG) {   // source-major: dr, wz
+      const int i = idx / tt, t = idx - i * tt;
+      const int64_t tok = t0 + t;
+      if (tok < n_tok) {
+        float* dri = static_cast<float*>(dr.p[i]);
+        const float drv = s_dz[t * SP + i];
+        dri[tok] = dr_accum ? dri[tok] + drv : drv;
+        const float dz = s_gd[t * SP + i];
+        *reinterpret_cast<float2*>(wz + 2 * ((int64_t)i * wz_stride + tok)) =
+            make_float2(s_w[t * SP + i], dz * s_r[t * SP + i] * inv);
+      }
+    }
+    __syncthreads();
+  }
+  // the workgroup's dq: row slots add their columns in a fixed order
+  float* s_dq = lds;
+  for (int k = 0; k < R.rpw; ++k) {
+    if (R.rs == k) {
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        const int c8 = R.c8(v);
+        if (c8 < R.d8) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float val = dqa[v][e] * inv;
+            s_dq[c8 * 8 + e] = (k == 0) ? val : s_dq[c8 * 8 + e] + val;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  for (int c = tid; c < d; c += WG) dq_part[(int64_t)blockIdx.x * d + c] = s_dq[c];
+}
+
+// out[c] = sum_p part[p][c]: 16 columns per workgroup, 16 row groups (rows p = group mod 16) added in a fixed order
+__global__ __launch_bounds__(WG) void k_reduce_rows(const float* __restrict__ part, int64_t rows, int d,
+                                                    float* __restrict__ out) {
+  __shared__ float s[WG];
+  const int tid = (int)threadIdx.x, cl = tid & 15, grp = tid >> 4;
+  const int c = blockIdx.x * 16 + cl;
+  float acc = 0.f;
+  if (c < d) {
+    int64_t p = grp;
+    for (; p + 7 * 16 < rows; p += 8 * 16) {
+      float a[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) a[u] = part[(p + 16 * u) * d + c];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += a[u];
+    }
+    for (; p < rows; p += 16) acc += part[p * d + c];
+  }
+  s[tid] = acc;
+  __syncthreads();
+  if (grp == 0 && c < d) {
+    float t = s[cl];
+    for (int k = 1; k < 16; ++k) t += s[k * 16 + cl];
+    out[c] = t;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// backward pass 2, list layout: dv_i (=|+=) w_i g + dzr_i q
+// ---------------------------------------------------------------------------------------------------------------
+template <typename T, int VPT>
+__global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, const T* __restrict__ g,
+                                                  const float* __restrict__ q, const float* __restrict__ wz,
+                                                  int64_t wz_stride, int64_t n_tok, int d, int tpr) {
+  const Rows R(d, tpr);
+  float qv[VPT][8];
+#pragma unroll
+  for (int v = 0; v < VPT; ++v) {
+    const int c8 = R.c8(v);
+    if (c8 < R.d8) load_f32x8(q + c8 * 8, qv[v]);
+  }
+  const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
+  for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
+    const int64_t tok = gi * R.rpw + R.rs;
+    if (tok >= n_tok) continue;
+    float gv[VPT][8];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+      const int c8 = R.c8(v);
+      if (c8 < R.d8) IO<T>::load(g + tok * (int64_t)d + c8 * 8, gv[v]);
+    }
+    for (int i = 0; i < n; ++i) {
+      const float2 s = *reinterpret_cast<const float2*>(wz + 2 * ((int64_t)i * wz_stride + tok));
+      T* dvi = static_cast<T*>(dv.p[i]) + tok * (int64_t)d;
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        const int c8 = R.c8(v);
+        if (c8 < R.d8) {
+          float o[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) o[k] = s.x * gv[v][k] + s.y * qv[v][k];
+          if (accum) {
+            float prev[8];
+            IO<T>::load(dvi + c8 * 8, prev);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[k] = prev[k] + IO<T>::round(o[k]);
+          }
+          IO<T>::store(dvi + c8 * 8, o);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// stacked layout: the finished gradient of one update from every read that held it, plus its scale's term
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int AS_RB = 2;   // token rows per lane, sharing each query load
+
+template <typename T, int VPT>
+__global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* __restrict__ vsrc,
+                                                    const float* __restrict__ r, const float* __restrict__ gr,
+                                                    T* __restrict__ dv, int64_t n_tok, int d, int tpr) {
+  const Rows R(d, tpr);
+  const int64_t rows_per_tile = (int64_t)R.rpw * AS_RB;
+  const int64_t tiles = (n_tok + rows_per_tile - 1) / rows_per_tile;
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    int64_t tok[AS_RB];
+    bool ok[AS_RB];
+#pragma unroll
+    for (int k = 0; k < AS_RB; ++k) {
+      tok[k] = tile * rows_per_tile + R.rs + (int64_t)k * R.rpw;
+      ok[k] = tok[k] < n_tok;
+    }
+    float acc[AS_RB][VPT][8];
+#pragma unroll
+    for (int k = 0; k < AS_RB; ++k)
+#pragma unroll
+      for (int v = 0; v < VPT; ++v)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[k][v][e] = 0.f;
+    for (int j = 0; j < m; ++j) {
+      const T* gj = static_cast<const T*>(tab.g[j]);
+      const float* wzj = tab.wz[j];
+      float qv[VPT][8];
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        const int c8 = R.c8(v);
+        if (c8 < R.d8) load_f32x8(tab.q[j] + c8 * 8, qv[v]);
+      }
+#pragma unroll
+      for (int k = 0; k < AS_RB; ++k) {
+        if (!ok[k]) continue;
+        const float2 s = *reinterpret_cast<const float2*>(wzj + 2 * tok[k]);
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          const int c8 = R.c8(v);
+          if (c8 < R.d8) {
+            float e[8];
+            IO<T>::load(gj + tok[k] * (int64_t)d + c8 * 8, e);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) acc[k][v][x] += s.x * e[x] + s.y * qv[v][x];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < AS_RB; ++k) {
+      if (!ok[k]) continue;
+      const float rv = r[tok[k]];
+      const float c = gr ? gr[tok[k]] * (-rv * rv * rv) / (float)d : 0.f;
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        const int c8 = R.c8(v);
+        if (c8 < R.d8) {
+          float e[8];
+          IO<T>::load(vsrc + tok[k] * (int64_t)d + c8 * 8, e);
+#pragma unroll
+          for (int x = 0; x < 8; ++x) acc[k][v][x] += c * e[x];
+          IO<T>::store(dv + tok[k] * (int64_t)d + c8 * 8, acc[k][v]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// host side: argument checks, layout choice, dispatch
+// ---------------------------------------------------------------------------------------------------------------
+int row_layout(int64_t d, int* vpt, int* tpr, int max_vpt = 4) {
+  if (d <= 0 || (d & 7) || d > LDR_MAX_WIDTH) return LDR_E_SHAPE;
+  const int64_t d8 = d >> 3;
+  int64_t best = INT64_MAX;
+  int bv = 0, bt = 0;
+  for (int v = 1; v <= max_vpt; ++v) {
+    for (int t = 8; t <= WG; t <<= 1) {
+      if ((int64_t)v * t < d8) continue;
+      const int64_t key = ((int64_t)v * t - d8) * 16 + (t > 64 ? 8 : 0) + v;   // waste, then one wave per row
+      if (key < best) { best = key; bv = v; bt = t; }
+    }
+  }
+  if (!bv) return LDR_E_SHAPE;
+  *vpt = bv;
+  *tpr = bt;
+  return LDR_OK;
+}
+
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool dtype_ok(int dt) { return dt == LDR_F32 || dt == LDR_BF16; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline unsigned grid_of(int64_t blocks, int64_t cap) { return (unsigned)(blocks < 1 ? 1 : (blocks < cap ? blocks : cap)); }
+inline int launched() { return (int)hipGetLastError(); }
+
+// tokens per tile of the tiled kernels: at least one row per row slot
+inline int tile_tokens(int tpr) { const int rpw = WG / tpr; return rpw > 16 ? rpw : 16; }
+
+int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n) {
+  if (!v || n < 1 || n > MAXS) return LDR_E_ARG;
+  for (int64_t i = 0; i < n; ++i) {
+    s.v[i] = reinterpret_cast<const void*>(v[i]);
+    if (!s.v[i] || !al16(s.v[i])) return s.v[i] ? LDR_E_ALIGN : LDR_E_ARG;
+    s.r[i] = r ? reinterpret_cast<const float*>(r[i]) : nullptr;
+    if (r && !s.r[i]) return LDR_E_ARG;
+  }
+  for (int64_t i = n; i < MAXS; ++i) { s.v[i] = nullptr; s.r[i] = nullptr; }
+  return LDR_OK;
+}
+
+#define LDR_VPT_SWITCH(VPT_RT, ...)                              \
+  switch (VPT_RT) {                                              \
+    case 1: { constexpr int VPT = 1; __VA_ARGS__; } break;       \
+    case 2: { constexpr int VPT = 2; __VA_ARGS__; } break;       \
+    case 3: { constexpr int VPT = 3; __VA_ARGS__; } break;       \
+    case 4: { constexpr int VPT = 4; __VA_ARGS__; } break;       \
+    default: return LDR_E_SHAPE;                                 \
+  }
+
+#define LDR_DTYPE_SWITCH(DT, ...)                                \
+  if ((DT) == LDR_BF16) { typedef bf16_t T; __VA_ARGS__; }       \
+  else { typedef float T; __VA_ARGS__; }
+
+template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
+
+}  // namespace
+
+// ===============================================================================================================
+// C ABI
+// ===============================================================================================================
+extern "C" {
+
+int ldr_abi_version(void) { return 1; }
+
+const char* ldr_strerror(int code) {
+  switch (code) {
+    case LDR_OK: return "ok";
+    case LDR_E_ARG: return "loopback_read: invalid argument (null pointer, bad count or flag)";
+    case LDR_E_SHAPE: return "loopback_read: unsupported shape (d must be a multiple of 8 and <= 8192; 1 <= n <= 64)";
+    case LDR_E_ALIGN: return "loopback_read: a vector pointer is not 16-byte aligned";
+    case LDR_E_DTYPE: return "loopback_read: dtype must be LDR_F32 or LDR_BF16";
+    default: return code > 0 ? hipGetErrorString((hipError_t)code) : "loopback_read: unknown error";
+  }
+}
+
+int ldr_row_layout(int64_t d, int* vpt, int* tpr) {
+  if (!vpt || !tpr) return LDR_E_ARG;
+  return row_layout(d, vpt, tpr);
+}
+
+int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d) {
+  int vpt, tpr;
+  if (n_tok < 1 || row_layout(d, &vpt, &tpr, B1_MAX_VPT) != LDR_OK) return 0;
+  return grid_of(cdiv(n_tok, tile_tokens(tpr)), B1_GRID);
+}
+
+int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (n_tok < 0 || !x || !r) return LDR_E_ARG;
+  if (!al16(x)) return LDR_E_ALIGN;
+  int vpt, tpr, e = row_layout(d, &vpt, &tpr);
+  if (e) return e;
+  if (n_tok == 0) return LDR_OK;
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_rstd_fwd<T, VPT>), dim3(grid), dim3(WG), 0, st,
+                                                                  static_cast<const T*>(x), r, n_tok, (int)d, tpr, eps)))
+  return launched();
+}
+
+int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
+                 void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (n_tok < 0 || !x || !r || !gr || !gx) return LDR_E_ARG;
+  if (!al16(x) || !al16(gx)) return LDR_E_ALIGN;
+  int vpt, tpr, e = row_layout(d, &vpt, &tpr);
+  if (e) return e;
+  if (n_tok == 0) return LDR_OK;
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_rstd_bwd<T, VPT>), dim3(grid), dim3(WG), 0, st,
+                                                                  static_cast<const T*>(x), r, gr, static_cast<T*>(gx),
+                                                                  n_tok, (int)d, tpr)))
+  return launched();
+}
+
+int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, float* dots,
+                   int64_t n_tok, int64_t d, int64_t nq, int64_t dots_jstride, float eps, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (n_tok < 0 || !h || !x || !v_out || !r_out || nq < 0) return LDR_E_ARG;
+  if (nq > LDR_MAX_QUERIES) return LDR_E_SHAPE;
+  if (nq > 0 && (!q || !dots || dots_jstride < n_tok)) return LDR_E_ARG;
+  if (!al16(h) || !al16(x) || !al16(v_out) || (nq > 0 && !al16(q))) return LDR_E_ALIGN;
+  if (d <= 0 || (d & 7) || d > LDR_MAX_WIDTH) return LDR_E_SHAPE;
+  if (n_tok == 0) return LDR_OK;
+  const unsigned grid = (unsigned)cdiv(n_tok, WR_TT);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_write_dots<T>), dim3(grid), dim3(WG), 0, st, static_cast<const T*>(h),
+                                             static_cast<const T*>(x), static_cast<T*>(v_out), r_out, q, dots, n_tok,
+                                             (int)d, (int)nq, dots_jstride, eps))
+  return launched();
+}
+
+int ldr_dots_online(const uint64_t* src_v, int64_t n, const float* q, float* out, int64_t out_stride,
+                    int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (n_tok < 0 || !q || !out || out_stride < n_tok) return LDR_E_ARG;
+  if (!al16(q)) return LDR_E_ALIGN;
+  SrcTab s;
+  int e = fill_src(s, src_v, nullptr, n);
+  if (e) return e;
+  int vpt, tpr;
+  if ((e = row_layout(d, &vpt, &tpr))) return e;
+  if (n_tok == 0) return LDR_OK;
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 4096);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dots<T, VPT, Chunk<VPT>::C>), dim3(grid), dim3(WG),
+                                                                  0, st, s, (int)n, q, out, out_stride, n_tok, (int)d,
+                                                                  tpr)))
+  return launched();
+}
+
+int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* dots, int64_t dots_stride,
+                 const void* base, const float* cbar, const float* c0, float inv_sqrt_d, void* out, float* tc,
+                 float* lg, float* lse, int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (!src_r || n_tok < 0 || !dots || dots_stride < n_tok || !base || !cbar || !c0 || !out || !tc || !lg || !lse)
+    return LDR_E_ARG;
+  if (!al16(base) || !al16(out)) return LDR_E_ALIGN;
+  SrcTab s;
+  int e = fill_src(s, src_v, src_r, n);
+  if (e) return e;
+  int vpt, tpr;
+  if ((e = row_layout(d, &vpt, &tpr))) return e;
+  if (n_tok == 0) return LDR_OK;
+  const int tt = tile_tokens(tpr);
+  const unsigned grid = grid_of(cdiv(n_tok, tt), 65535);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_fwd<T, VPT>), dim3(grid), dim3(WG), 0, st, s,
+                                                                  (int)n, dots, dots_stride, static_cast<const T*>(base),
+                                                                  cbar, c0, inv_sqrt_d, static_cast<T*>(out), tc, lg,
+                                                                  lse, n_tok, (int)d, tpr, tt)))
+  return launched();
+}
+
+int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const void* g, const float* gt,
+                  const float* lg, const float* lse, const float* tc, const float* cbar, const float* c0,
+                  float inv_sqrt_d, float* dcbar, const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride,
+                  float* dq_part, int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (!src_r || n_tok < 0 || !g || !lg || !lse || !tc || !cbar || !c0 || !dcbar || !dr || !wz || !dq_part ||
+      wz_stride < n_tok || (dr_accum != 0 && dr_accum != 1))
+    return LDR_E_ARG;
+  if (!al16(g)) return LDR_E_ALIGN;
+  SrcTab s;
+  int e = fill_src(s, src_v, src_r, n);
+  if (e) return e;
+  PtrTab drt;
+  for (int64_t i = 0; i < MAXS; ++i) {
+    drt.p[i] = i < n ? reinterpret_cast<void*>(dr[i]) : nullptr;
+    if (i < n && !drt.p[i]) return LDR_E_ARG;
+  }
+  int vpt, tpr;
+  if ((e = row_layout(d, &vpt, &tpr, B1_MAX_VPT))) return e;
+  if (n_tok == 0) return LDR_OK;
+  const int tt = tile_tokens(tpr);
+  const unsigned grid = grid_of(cdiv(n_tok, tt), B1_GRID);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_bwd1<T, VPT, Chunk<VPT>::C>), dim3(grid), dim3(WG),
+                                                                  0, st, s, (int)n, static_cast<const T*>(g), gt, lg,
+                                                                  lse, tc, cbar, c0, inv_sqrt_d, dcbar, drt, dr_accum,
+                                                                  wz, wz_stride, dq_part, n_tok, (int)d, tpr, tt)))
+  return launched();
+}
+
+int ldr_reduce_rows(const float* part, int64_t rows, int64_t d, float* out, void* stream) {
+  if (!part || !out || rows < 1 || d < 1) return LDR_E_ARG;
+  const unsigned grid = (unsigned)cdiv(d, 16);
+  hipLaunchKernelGGL(k_reduce_rows, dim3(grid), dim3(WG), 0, static_cast<hipStream_t>(stream), part, rows, (int)d,
+                     out);
+  return launched();
+}
+
+int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, const float* q, const float* wz,
+                       int64_t wz_stride, int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (!dv || n < 1 || n > MAXS || !g || !q || !wz || wz_stride < n_tok || n_tok < 0 || (accum != 0 && accum != 1))
+    return n > MAXS ? LDR_E_SHAPE : LDR_E_ARG;
+  if (!al16(g) || !al16(q)) return LDR_E_ALIGN;
+  PtrTab t;
+  for (int64_t i = 0; i < MAXS; ++i) {
+    t.p[i] = i < n ? reinterpret_cast<void*>(dv[i]) : nullptr;
+    if (i < n && (!t.p[i] || !al16(t.p[i]))) return t.p[i] ? LDR_E_ALIGN : LDR_E_ARG;
+  }
+  int vpt, tpr, e = row_layout(d, &vpt, &tpr);
+  if (e) return e;
+  if (n_tok == 0) return LDR_OK;
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_bwd2_list<T, VPT>), dim3(grid), dim3(WG), 0, st, t,
+                                                                  (int)n, accum, static_cast<const T*>(g), q, wz,
+                                                                  wz_stride, n_tok, (int)d, tpr)))
+  return launched();
+}
+
+int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
+                    const float* r, const float* gr, void* dv, int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (m < 0 || m > MAXS) return LDR_E_SHAPE;
+  if ((m > 0 && (!g || !wz || !q)) || !v || !r || !dv || n_tok < 0) return LDR_E_ARG;
+  if (!al16(v) || !al16(dv)) return LDR_E_ALIGN;
+  AsmTab t;
+  for (int64_t j = 0; j < MAXS; ++j) {
+    t.g[j] = j < m ? reinterpret_cast<const void*>(g[j]) : nullptr;
+    t.wz[j] = j < m ? reinterpret_cast<const float*>(wz[j]) : nullptr;
+    t.q[j] = j < m ? reinterpret_cast<const float*>(q[j]) : nullptr;
+    if (j < m && (!t.g[j] || !t.wz[j] || !t.q[j])) return LDR_E_ARG;
+    if (j < m && (!al16(t.g[j]) || !al16(t.q[j]) || (reinterpret_cast<uintptr_t>(t.wz[j]) & 7u))) return LDR_E_ALIGN;
+  }
+  int vpt, tpr, e = row_layout(d, &vpt, &tpr);
+  if (e) return e;
+  if (n_tok == 0) return LDR_OK;
+  const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * AS_RB), 65535);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT>), dim3(grid), dim3(WG), 0, st,
+                                                                  t, (int)m, static_cast<const T*>(v), r, gr,
+                                                                  static_cast<T*>(dv), n_tok, (int)d, tpr)))
+  return launched();
+}
+
+}  // extern "C"

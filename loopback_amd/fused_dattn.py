@@ -1,0 +1,495 @@
+"""The Loopback depth-attention read on MI355X: a drop-in for yancyou/Loopback's `fused_dattn.py`.
+
+Same names, signatures and gradient conventions as the reference module (fused_dattn.py:185-793); the compute runs
+in hand-written HIP kernels for gfx950 behind the C ABI of `include/loopback_read.h` (loaded by `_lib`). There is no
+Triton, no CUDA path and no fallback: a missing library fails at import, a bad argument raises RuntimeError.
+
+One read at destination s has n = s + 1 sources v_i (the raw block updates) and computes (fused_dattn.py:3-27)
+
+    z_i  = r_i (q . v_i) / sqrt(d),  r_i = rsqrt(mean(v_i^2) + eps)
+    p    = softmax_i(z_i + lc_i),  p0 = softmax_i(lc_i),  lc_i = log max(c0_i, 1e-8),  M = sum_i c0_i
+    tc_i = c0_i + M (p_i - p0_i)                         (the installed coefficients, returned)
+    out  = base + sum_i (tc_i - cbar_i) v_i              (fp32 accumulation, one rounding to the update dtype)
+
+Backward (g = dL/dout, gt = dL/dtc): gd_i = g.v_i, gp_i = M (gd_i + gt_i), Sacc = sum_i p_i gp_i,
+dz_i = p_i (gp_i - Sacc), dq = sum_tok sum_i dz_i r_i v_i / sqrt(d), dv_i = (tc_i - cbar_i) g + dz_i r_i q / sqrt(d),
+dr_i = dz_i z_i / r_i, dcbar_i = -gd_i, dbase = g.
+
+Layouts:
+  * list layout (FusedDattnRead, FusedDattnReadAcc): one tensor per source; the kernels take the n source addresses
+    by value in their arguments (no device pointer array, no host-to-device copy);
+  * stacked layout (DattnStack, FusedDattnReadStk): the updates of a pass in V[n_steps, b, t, d]. With the read
+    queries, each write also stores the update's scores against every later read query, DOTS[j, i, tok]
+    (query-major, then source, then token: coalesced for both the write and the read), and the reads form their
+    softmax from them. The stacked backward does not read-modify-write a gradient stack per read: each read's
+    backward keeps its output gradient g_s and its per-(source, token) scalars (w, dz r / sqrt(d)); the gradient of
+    update i is formed once, when its scale's backward runs (after every read of it), as
+    sum_s (w_si g_s + dzr_si q_s) + the scale's term, in fp32 with one rounding. Same gradients, at least as
+    accurate as the per-read bf16 adds, and about a quarter less HBM traffic over a pass.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib as L
+
+__all__ = ["rstd_ref", "rstd", "fused_read_supported", "FusedDattnRead", "DattnGradAccum", "FusedDattnReadAcc",
+           "DattnStack", "FusedDattnReadStk", "_alias"]
+
+_LIB = L.LIB
+MAX_SOURCES = L.MAX_SOURCES
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# plumbing
+# ---------------------------------------------------------------------------------------------------------------
+def _p(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return L.BF16
+    if dtype == torch.float32:
+        return L.F32
+    raise RuntimeError(f"delta_attnres HIP read: updates must be bfloat16 or float32, got {dtype}")
+
+
+def _require_gpu(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"delta_attnres HIP read: {what} must be a GPU (HIP) tensor, got device {t.device}")
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0
+
+
+def _inv_sqrt(d: int) -> float:
+    return 1.0 / (d ** 0.5)
+
+
+# Optional launch observer: a callable name -> context manager, entered around every library call (the bench uses it
+# to bracket each kernel with HIP events on the launch stream). None in normal use.
+_TIMER = None
+
+
+def _run(name: str, *args) -> None:
+    fn = getattr(_LIB, "ldr_" + name)
+    if _TIMER is None:
+        code = fn(*args)
+    else:
+        with _TIMER(name):
+            code = fn(*args)
+    L.check(code, name)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the RMS scale of a source (fused_dattn.py:197-261)
+# ---------------------------------------------------------------------------------------------------------------
+def rstd_ref(delta: torch.Tensor, eps: float) -> torch.Tensor:
+    """The RMSNorm scale of a source as a torch expression, (b, t, 1) fp32 (fused_dattn.py:197-199). Part of the
+    module's interface for callers; the HIP path below does not use it."""
+    return torch.rsqrt(delta.float().pow(2).mean(-1, keepdim=True) + eps)
+
+
+class _Rstd(torch.autograd.Function):
+    """r = rsqrt(sum x^2 / d + eps) per token; backward gx = gr (-r^3) / d x (fused_dattn.py:232-254)."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, eps: float):
+        xc = x.contiguous()
+        d = xc.shape[-1]
+        n_tok = xc.numel() // d
+        r = torch.empty(xc.shape[:-1] + (1,), device=xc.device, dtype=torch.float32)
+        _run("rstd_fwd", _p(xc), _p(r), n_tok, d, float(eps), _dtype_code(xc.dtype), _stream(xc.device))
+        ctx.save_for_backward(xc, r)
+        return r
+
+    @staticmethod
+    def backward(ctx, gr: torch.Tensor):
+        xc, r = ctx.saved_tensors
+        d = xc.shape[-1]
+        n_tok = xc.numel() // d
+        gx = torch.empty_like(xc)
+        grc = gr.float().contiguous()
+        _run("rstd_bwd", _p(xc), _p(r), _p(grc), _p(gx), n_tok, d, _dtype_code(xc.dtype),
+                                  _stream(xc.device))
+        return gx, None
+
+
+def rstd(delta: torch.Tensor, eps: float) -> torch.Tensor:
+    """The RMSNorm scale of a source, (b, t, 1) fp32, differentiable, computed by the HIP kernels
+    (fused_dattn.py:257-261). GPU tensors only: there is no CPU path in this module."""
+    _require_gpu(delta, "rstd input")
+    return _Rstd.apply(delta, float(eps))
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# list layout (fused_dattn.py:264-395)
+# ---------------------------------------------------------------------------------------------------------------
+def fused_read_supported(base, values, rstds, cbar) -> bool:
+    """The reference's gate (fused_dattn.py:379-395) -- GPU, contiguous, same-shape same-dtype bf16/fp32 sources and
+    base, contiguous fp32 (b, t, 1) rstds, contiguous fp32 (b, t, n) cbar -- plus this build's kernel limits:
+    d a multiple of 8 and at most 8192, at most 64 sources, 16-byte aligned rows."""
+    v0 = values[0]
+    if not v0.is_cuda or v0.dtype not in (torch.bfloat16, torch.float32):
+        return False
+    shape = v0.shape
+    d = shape[-1]
+    if d % 8 or d > L.MAX_WIDTH or len(values) > MAX_SOURCES or len(rstds) != len(values):
+        return False
+    if base.dtype != v0.dtype or base.shape != shape or not base.is_contiguous() or not _aligned(base):
+        return False
+    for v in values:
+        if v.dtype != v0.dtype or v.shape != shape or not v.is_contiguous() or not _aligned(v) or v.device != v0.device:
+            return False
+    rshape = shape[:-1] + (1,)
+    for r in rstds:
+        if r.dtype != torch.float32 or r.shape != rshape or not r.is_contiguous():
+            return False
+    return cbar.dtype == torch.float32 and cbar.shape == shape[:-1] + (len(values),) and cbar.is_contiguous()
+
+
+def _check_list(base, values, rstds, cbar) -> None:
+    if not fused_read_supported(base, values, rstds, cbar):
+        raise RuntimeError("delta_attnres HIP read: unsupported inputs (see fused_read_supported)")
+
+
+def _forward_impl(ctx, q, base, cbar, c0, srcs):
+    n = len(srcs) // 2
+    values, rstds = srcs[:n], srcs[n:]
+    _check_list(base, values, rstds, cbar)
+    v0 = values[0]
+    d = v0.shape[-1]
+    n_tok = v0.numel() // d
+    dev = v0.device
+    dt = _dtype_code(v0.dtype)
+    st = _stream(dev)
+    qc = q.detach().float().contiguous()
+    c0c = c0.detach().float().contiguous()
+    cbar_c = cbar.detach().float().contiguous()
+    base_c = base.detach().contiguous()
+    out = torch.empty_like(base_c)
+    tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+    lg = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+    lse = torch.empty(n_tok, device=dev, dtype=torch.float32)
+    dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
+    vp = L.u64_array(v.data_ptr() for v in values)
+    rp = L.u64_array(r.data_ptr() for r in rstds)
+    _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
+    _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base_c), _p(cbar_c), _p(c0c), _inv_sqrt(d), _p(out),
+                              _p(tc), _p(lg), _p(lse), n_tok, d, dt, st)
+    ctx.save_for_backward(qc, cbar_c, c0c, lg, lse, tc, *values, *rstds)
+    ctx.n, ctx.q_dtype, ctx.base_shape = n, q.dtype, base.shape
+    return out, tc.view(*base.shape[:-1], n)
+
+
+def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, lg, lse, tc, cbar_c, c0c, dr_ptrs, dr_accum, wz, wz_stride, n_tok, d,
+          dtype, dev):
+    """Pass 1 of the backward plus the dq reduction; returns (dq fp32, dcbar [n_tok, n])."""
+    st = _stream(dev)
+    gt_c = None if gt is None else gt.reshape(n_tok, n).float().contiguous()
+    dcbar = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+    parts = L.bwd1_parts(n_tok, d)
+    dq_part = torch.empty((max(1, parts), d), device=dev, dtype=torch.float32)
+    _run("read_bwd1", values_ptrs, rstd_ptrs, n, _p(g), _p(gt_c), _p(lg), _p(lse), _p(tc), _p(cbar_c),
+                               _p(c0c), _inv_sqrt(d), _p(dcbar), dr_ptrs, int(dr_accum), _p(wz), wz_stride,
+                               _p(dq_part), n_tok, d, dtype, st)
+    dq = torch.empty(d, device=dev, dtype=torch.float32)
+    if n_tok > 0:
+        _run("reduce_rows", _p(dq_part), parts, d, _p(dq), st)
+    else:
+        dq.zero_()
+    return dq, dcbar
+
+
+def _backward_impl(ctx, g, gt, dv, accum):
+    """dv: one gradient buffer per source, written (accum False) or added into (accum True) by the kernel."""
+    qc, cbar_c, c0c, lg, lse, tc, *rest = ctx.saved_tensors
+    n = ctx.n
+    values, rstds = rest[:n], rest[n:]
+    v0 = values[0]
+    d = v0.shape[-1]
+    n_tok = v0.numel() // d
+    dev = v0.device
+    dt = _dtype_code(v0.dtype)
+    g = g.to(v0.dtype).contiguous()
+    vp = L.u64_array(v.data_ptr() for v in values)
+    rp = L.u64_array(r.data_ptr() for r in rstds)
+    dr = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
+    wz = torch.empty((n, n_tok, 2), device=dev, dtype=torch.float32)
+    dq, dcbar = _bwd1(vp, rp, n, g, gt, lg, lse, tc, cbar_c, c0c, L.u64_array(dr[i].data_ptr() for i in range(n)),
+                      False, wz, n_tok, n_tok, d, dt, dev)
+    for t in dv:
+        if t.dtype != v0.dtype or not t.is_contiguous() or t.numel() != v0.numel() or not _aligned(t):
+            raise RuntimeError("delta_attnres HIP read: gradient buffers must match the sources")
+    _run("read_bwd2_list", L.u64_array(t.data_ptr() for t in dv), n, int(bool(accum)), _p(g), _p(qc), _p(wz),
+                                    n_tok, n_tok, d, dt, _stream(dev))
+    return dq.to(ctx.q_dtype), g, dcbar.view(*ctx.base_shape[:-1], n), [dr[i].view_as(rstds[i]) for i in range(n)]
+
+
+class FusedDattnRead(torch.autograd.Function):
+    """(out, tc) = FusedDattnRead.apply(q, base, cbar, c0, *values, *rstds) (fused_dattn.py:321-334); backward
+    returns (dq, g, dcbar, None, *dv, *dr)."""
+
+    @staticmethod
+    def forward(ctx, q: torch.Tensor, base: torch.Tensor, cbar: torch.Tensor, c0: torch.Tensor, *srcs: torch.Tensor):
+        return _forward_impl(ctx, q, base, cbar, c0, srcs)
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor, gt: torch.Tensor | None):
+        n = ctx.n
+        values = ctx.saved_tensors[6:6 + n]
+        dv = [torch.empty_like(v) for v in values]   # one tensor per source: autograd releases each as soon as it can
+        dq, g_out, dcbar_v, dr = _backward_impl(ctx, g, gt, dv, accum=False)
+        return (dq, g_out, dcbar_v, None, *dv, *dr)
+
+
+class DattnGradAccum:
+    """Per-forward-pass state of the list layout's in-kernel gradient accumulation (fused_dattn.py:337-350): the first
+    backward of a pass allocates one gradient buffer per source, later backwards add into them inside the kernel
+    (prev + round(dv), rounded: autograd's own bf16 accumulation), and read i (read 1 for source 0) returns the
+    finished buffer."""
+    __slots__ = ("bufs",)
+
+    def __init__(self):
+        self.bufs = {}
+
+
+class FusedDattnReadAcc(torch.autograd.Function):
+    """FusedDattnRead with in-kernel gradient accumulation: apply(acc, step, q, base, cbar, c0, *values, *rstds)
+    (fused_dattn.py:353-376)."""
+
+    @staticmethod
+    def forward(ctx, acc: DattnGradAccum, step: int, q, base, cbar, c0, *srcs):
+        out = _forward_impl(ctx, q, base, cbar, c0, srcs)
+        ctx.acc, ctx.step = acc, int(step)
+        return out
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor, gt: torch.Tensor | None):
+        acc, step, n = ctx.acc, ctx.step, ctx.n
+        values = ctx.saved_tensors[6:6 + n]
+        first = not acc.bufs
+        if first:
+            for i in range(n):
+                acc.bufs[i] = torch.empty_like(values[i])
+        elif any(i not in acc.bufs for i in range(n)):
+            raise RuntimeError("delta_attnres gradient accumulation: a source without a buffer (reads out of order?)")
+        dv = [acc.bufs[i] for i in range(n)]
+        dq, g_out, dcbar_v, dr = _backward_impl(ctx, g, gt, dv, accum=not first)
+        final = [i == step or (step == 1 and i == 0) for i in range(n)]
+        ctx.acc = None                    # release the buffers from this node
+        return (None, None, dq, g_out, dcbar_v, None, *[dv[i] if final[i] else None for i in range(n)], *dr)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# stacked layout (fused_dattn.py:629-793)
+# ---------------------------------------------------------------------------------------------------------------
+def _alias(stack_tensor: torch.Tensor, s: int) -> torch.Tensor:
+    """Slice s of a stack as a tensor that shares its storage but is not an autograd view of it (fused_dattn.py:
+    629-636): later slices are written in place, and autograd forbids a custom Function to return a view whose base
+    is then modified."""
+    sl = stack_tensor[s]
+    out = torch.empty(0, dtype=stack_tensor.dtype, device=stack_tensor.device)
+    out.set_(stack_tensor.untyped_storage(), sl.storage_offset(), sl.shape, sl.stride())
+    return out
+
+
+def _pair(s: int, i: int) -> int:
+    """Row of the (read s >= 1, source i <= s) pair in DattnStack.WZ: reads in order, sources in order."""
+    return s * (s + 1) // 2 - 1 + i
+
+
+class DattnStack:
+    """The stacked storage of one forward pass (fused_dattn.py:639-676): V[n_steps, b, t, d] (the updates) and
+    R[n_steps, b, t, 1] (their RMS scales). Given `query` (the read queries, (n_steps - 1, d); read s uses row s - 1)
+    each write also stores the update's scores against the queries of the reads still to come,
+    DOTS[query j, source i, token] fp32, and the reads use them.
+
+    Backward state: dR [n_steps, b, t, 1] (the scales' gradients, accumulated by the reads' backwards, zeroed on the
+    first), WZ [pairs, b*t, 2] (per (read, source) pair and token: w = tc - cbar and dz r / sqrt(d)), and per read
+    whose backward ran, its output gradient and query (`bwd`). The updates' gradients are assembled from those by the
+    scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
+    transposed operand for its tensor-core product; the HIP write reads Q directly)."""
+    __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "DOTS", "r_done", "WZ", "bwd",
+                 "assembled")
+
+    def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
+        b, t, d = shape
+        n_steps = int(n_steps)
+        if dtype not in (torch.bfloat16, torch.float32):
+            raise RuntimeError(f"delta_attnres stacked read: dtype must be bfloat16 or float32, got {dtype}")
+        if d % 8 or d > L.MAX_WIDTH or n_steps < 1 or n_steps > MAX_SOURCES:
+            raise RuntimeError(f"delta_attnres stacked read: unsupported shape d={d} n_steps={n_steps} (d a multiple "
+                               f"of 8 up to {L.MAX_WIDTH}, at most {MAX_SOURCES} steps)")
+        self.n_steps, self.n_tok, self.d = n_steps, b * t, d
+        self.V = torch.empty((n_steps, b, t, d), dtype=dtype, device=device)
+        self.R = torch.empty((n_steps, b, t, 1), dtype=torch.float32, device=device)
+        _require_gpu(self.V, "the stack")
+        self.dV = self.dR = None
+        self.WZ = None
+        self.bwd = {}
+        self.assembled = set()
+        self.eps = float(eps)
+        self.r_done = [False] * self.n_steps      # R[s] (and the scores of update s) written by the write of s
+        self.Q = self.QT = self.DOTS = None
+        if query is not None:
+            self.Q = query.detach().float().contiguous()
+            nq = self.Q.shape[0]
+            if nq > L.MAX_QUERIES or self.Q.shape[-1] != d:
+                raise RuntimeError(f"delta_attnres stacked read: query must be (<= {L.MAX_QUERIES}, {d}), "
+                                   f"got {tuple(self.Q.shape)}")
+            self.DOTS = torch.empty((max(1, nq), n_steps, b * t), dtype=torch.float32, device=device)
+
+    def write(self, s: int, h: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """V[s] = h - x, returned as the update tensor (an alias of the stack's slice, with the autograd edge to
+        h and x)."""
+        return _WriteDelta.apply(self, s, h, x)
+
+    def rstd(self, s: int, delta: torch.Tensor, eps: float) -> torch.Tensor:
+        """R[s] = the RMS scale of V[s], returned as an alias of the stack (differentiable through `delta`)."""
+        return _RstdStk.apply(self, s, delta, float(eps))
+
+    def grads(self):
+        """Allocate the backward state on the first backward of the pass; False then, True afterwards."""
+        if self.dR is None:
+            self.dR = torch.zeros_like(self.R)
+            pairs = self.n_steps * (self.n_steps + 1) // 2 - 1
+            self.WZ = torch.empty((max(1, pairs), self.n_tok, 2), dtype=torch.float32, device=self.V.device)
+            return False
+        return True
+
+
+class _WriteDelta(torch.autograd.Function):
+    """V[s] = round(h - x), R[s] from the rounded update and the scores against the later read queries, in one pass
+    (fused_dattn.py:679-695); a plain subtraction into the slice for layouts the kernel does not take."""
+
+    @staticmethod
+    def forward(ctx, stack: DattnStack, s: int, h: torch.Tensor, x: torch.Tensor):
+        out = _alias(stack.V, s)
+        V = stack.V
+        if (h.is_cuda and h.is_contiguous() and x.is_contiguous() and h.dtype == V.dtype == x.dtype
+                and h.numel() == x.numel() == stack.n_tok * stack.d and h.shape[-1] == stack.d
+                and _aligned(h) and _aligned(x)):
+            nq, qptr, dptr, jstride = 0, None, None, stack.n_steps * stack.n_tok
+            if stack.Q is not None:
+                j_lo = max(0, s - 1)                  # read s' >= s uses query s' - 1
+                nq = max(0, stack.Q.shape[0] - j_lo)
+                if nq > 0:
+                    qptr, dptr = stack.Q[j_lo], stack.DOTS[j_lo, s]
+            _run("write_dots", _p(h), _p(x), _p(out), _p(stack.R[s]), _p(qptr), _p(dptr), stack.n_tok,
+                                        stack.d, nq, jstride, stack.eps, _dtype_code(V.dtype), _stream(V.device))
+            stack.r_done[s] = True
+        else:
+            torch.sub(h, x, out=out)
+            stack.r_done[s] = False
+        return out
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor):
+        return None, None, g, -g
+
+
+class _RstdStk(torch.autograd.Function):
+    """Forward: R[s] (skipped when the write stored it). Backward: the finished gradient of update s -- every read
+    of it has run its backward by then -- returned as the update's one gradient (fused_dattn.py:698-722)."""
+
+    @staticmethod
+    def forward(ctx, stack: DattnStack, s: int, x: torch.Tensor, eps: float):
+        r = _alias(stack.R, s)
+        if not (stack.r_done[s] and eps == stack.eps):      # else the write already stored R[s]
+            xc = x.contiguous()
+            if xc.numel() != stack.n_tok * stack.d or xc.dtype != stack.V.dtype:
+                raise RuntimeError("delta_attnres stacked read: the scale's input must be the stack's update")
+            _run("rstd_fwd", _p(xc), _p(r), stack.n_tok, stack.d, float(eps), _dtype_code(xc.dtype),
+                                      _stream(xc.device))
+        ctx.stack, ctx.s, ctx.x = stack, s, x
+        return r
+
+    @staticmethod
+    def backward(ctx, gr: torch.Tensor):
+        stack, s, x = ctx.stack, ctx.s, ctx.x
+        if stack.dR is None:
+            raise RuntimeError("delta_attnres stacked read: the scale's backward ran before any read's backward")
+        xc = x.contiguous()
+        reads = sorted(k for k in stack.bwd if k >= max(s, 1))     # the reads of update s whose backward ran
+        dv = torch.empty_like(xc)
+        grc = None if gr is None else gr.float().contiguous()
+        g_ptrs = L.u64_array(stack.bwd[k][0].data_ptr() for k in reads)
+        wz_ptrs = L.u64_array(stack.WZ[_pair(k, s)].data_ptr() for k in reads)
+        q_ptrs = L.u64_array(stack.bwd[k][1].data_ptr() for k in reads)
+        _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc), _p(dv),
+                                     stack.n_tok, stack.d, _dtype_code(xc.dtype), _stream(xc.device))
+        stack.assembled.add(s)
+        for k in [k for k in stack.bwd if all(j in stack.assembled for j in range(k + 1))]:
+            del stack.bwd[k]              # every update read by read k has its gradient: drop g_k
+        ctx.stack = ctx.x = None          # release the stack from this node
+        return None, None, dv.view_as(x), None
+
+
+class FusedDattnReadStk(torch.autograd.Function):
+    """(out, tc) = apply(stack, step, q, base, cbar, c0, *updates, *scales) (fused_dattn.py:725-793): the updates and
+    scales are the stack's slices 0..step (inputs only for autograd's bookkeeping; the kernels read the stack).
+    Backward returns (None, None, dq, g, dcbar, None, None x n, dR alias for the scales whose last read this is)."""
+
+    @staticmethod
+    def forward(ctx, stack: DattnStack, step: int, q, base, cbar, c0, *srcs):
+        n = len(srcs) // 2
+        d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
+        if base.dtype != stack.V.dtype or not base.is_contiguous() or base.shape[:-1] != stack.V.shape[1:3]:
+            raise RuntimeError("delta_attnres stacked read: base must be contiguous, the stack's dtype and shape")
+        if not 1 <= n <= stack.n_steps or base.shape[-1] != d or not _aligned(base):
+            raise RuntimeError(f"delta_attnres stacked read: {n} sources for a stack of {stack.n_steps}")
+        dt = _dtype_code(stack.V.dtype)
+        st = _stream(dev)
+        qc = q.detach().float().contiguous()
+        c0c = c0.detach().float().contiguous()
+        cbar_c = cbar.detach().float().contiguous()
+        if cbar_c.numel() != n_tok * n or c0c.numel() != n:
+            raise RuntimeError("delta_attnres stacked read: cbar must be (b, t, n) and c0 (n,)")
+        out = torch.empty_like(base)
+        tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+        lg = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+        lse = torch.empty(n_tok, device=dev, dtype=torch.float32)
+        vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
+        rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
+        if stack.DOTS is not None and step >= 1 and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
+            dots = stack.DOTS[step - 1]          # the stored scores of query step - 1, [source, token]
+        else:
+            dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
+            _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
+        _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base), _p(cbar_c), _p(c0c), _inv_sqrt(d), _p(out),
+                                  _p(tc), _p(lg), _p(lse), n_tok, d, dt, st)
+        ctx.save_for_backward(qc, cbar_c, c0c, lg, lse, tc)
+        ctx.stack, ctx.step, ctx.n, ctx.q_dtype, ctx.base_shape = stack, int(step), n, q.dtype, base.shape
+        return out, tc.view(*base.shape[:-1], n)
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor, gt: torch.Tensor | None):
+        qc, cbar_c, c0c, lg, lse, tc = ctx.saved_tensors
+        stack, step, n = ctx.stack, ctx.step, ctx.n
+        d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
+        stack.grads()
+        g = g.to(stack.V.dtype).contiguous()
+        vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
+        rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
+        drp = L.u64_array(stack.dR[i].data_ptr() for i in range(n))
+        wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
+        dq, dcbar = _bwd1(vp, rp, n, g, gt, lg, lse, tc, cbar_c, c0c, drp, True, wz, n_tok, n_tok, d,
+                          _dtype_code(stack.V.dtype), dev)
+        stack.bwd[step] = (g, qc)        # for the updates' gradients, formed once per update
+        final = [i == step or (step == 1 and i == 0) for i in range(n)]   # the last read of scale i, in backward order
+        grads = (None, None, dq.to(ctx.q_dtype), g, dcbar.view(*ctx.base_shape[:-1], n), None,
+                 *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
+        # Release the stack from this node: ctx attributes live as long as the graph node, and a training loop that
+        # keeps each micro-batch's loss until the optimizer step would otherwise keep each micro-batch's stack.
+        ctx.stack = None
+        return grads

@@ -1,0 +1,162 @@
+"""The HIP read (list layout, the caller's FusedDattnRead path) against the oracle -- the restated reference read
+LoopDeltaAttnRes.combine -- on the same seeded inputs; mirrors tests/test_fused_dattn.py:87-125 of the reference.
+
+  1. fp32: out, tc and every gradient (the query row, each delta through its value and its RMS scale, proposal and
+     h0 through base, the previous coefficients) within max-abs 1e-5 x RMS of the fp32 oracle, over ragged token
+     counts, 2..20 sources, boundary and in-iteration reads, d in {768, 1024, 1536, 3072};
+  2. bf16: against the fp64 oracle on the same bf16-rounded inputs: max-abs error <= 1e-2 x max |ref| for outputs
+     and all gradients, and no worse than the reference read's own bf16 error (<= 2 err_ref + 2e-3);
+  3. zero query, cbar == prior: out == base and tc == c0 bitwise, fp32 and bf16.
+"""
+import pytest
+import torch
+
+from gpu_helpers import DEV, err_max, err_rms, make
+from oracle.reference_read import OracleCell
+
+pytestmark = pytest.mark.gpu
+
+
+def run_hip(d, n, args, boundary, beta=0.75):
+    from loopback_amd.cell import LoopDeltaAttnRes
+    deltas, proposal, h0, q, prior, coeffs, up, up2 = [
+        [x.to(DEV).requires_grad_() for x in a] if isinstance(a, list) else a.to(DEV) for a in args]
+    proposal.requires_grad_()
+    h0.requires_grad_()
+    nb = n if boundary else n + 1
+    cell = LoopDeltaAttnRes(d, num_loops=2, num_blocks=nb, beta=beta, eps=1e-6).to(DEV)
+    with torch.no_grad():
+        cell.query[n - 2].copy_(q)
+    cf = coeffs.detach().clone().requires_grad_()
+    out, tc, _ = cell.combine(proposal, h0, deltas, cf, prior, 0, n - 1)
+    ((out.float() * up).sum() + (tc * up2).sum()).backward()
+    torch.cuda.synchronize()
+    return dict(out=out.detach(), tc=tc.detach(), dq=cell.query.grad[n - 2], dv=[x.grad for x in deltas],
+                dprop=proposal.grad, dh0=h0.grad, dcoef=cf.grad)
+
+
+def run_oracle(d, n, args, boundary, beta=0.75, dtype=None):
+    deltas, proposal, h0, q, prior, coeffs, up, up2 = args
+    cast = (lambda x: x.to(dtype)) if dtype is not None else (lambda x: x)
+    deltas = [cast(x).detach().clone().requires_grad_() for x in deltas]
+    proposal = cast(proposal).detach().clone().requires_grad_()
+    h0 = cast(h0).detach().clone().requires_grad_()
+    f = (lambda x: x.double()) if dtype == torch.float64 else (lambda x: x)
+    nb = n if boundary else n + 1
+    query = torch.zeros(2 * nb - 1, d, dtype=torch.float64 if dtype == torch.float64 else torch.float32)
+    query[n - 2] = f(q)
+    query.requires_grad_()
+    cf = f(coeffs).detach().clone().requires_grad_()
+    cell = OracleCell(d, 2, nb, beta, 1e-6, query)
+    out, tc, _ = cell.combine(proposal, h0, deltas, cf, f(prior), 0, n - 1)
+    ((out.to(f(up).dtype) * f(up)).sum() + (tc * f(up2)).sum()).backward()
+    return dict(out=out.detach(), tc=tc.detach(), dq=query.grad[n - 2], dv=[x.grad for x in deltas],
+                dprop=proposal.grad, dh0=h0.grad, dcoef=cf.grad)
+
+
+def compare(a, b, fn):
+    e = {k: fn(a[k], b[k]) for k in ("out", "tc", "dq", "dprop", "dcoef")}
+    e["dv"] = max(fn(x, y) for x, y in zip(a["dv"], b["dv"]))
+    e["dh0"] = fn(a["dh0"], b["dh0"]) if b["dh0"] is not None and b["dh0"].abs().max() > 0 else 0.0
+    return e
+
+
+SHAPES_FP32 = [(2, 64, 768), (2, 37, 1024), (1, 50, 1536), (1, 9, 3072)]
+
+
+@pytest.mark.parametrize("b,t,d", SHAPES_FP32)
+@pytest.mark.parametrize("n", [2, 3, 8, 16, 20])
+@pytest.mark.parametrize("boundary", [False, True])
+def test_fp32_matches_reference_read(b, t, d, n, boundary):
+    args = make(b, t, d, n, torch.float32, seed=1000 * n + d + int(boundary))
+    print(f"case fp32 b{b} t{t} d{d} n{n} boundary={boundary}", flush=True)
+    hip = run_hip(d, n, args, boundary)
+    ref = run_oracle(d, n, args, boundary)
+    e = compare(hip, ref, err_rms)
+    assert max(e.values()) <= 1e-5, e
+
+
+@pytest.mark.parametrize("b,t,d", [(2, 256, 1024), (2, 128, 1536), (4, 128, 768)])
+@pytest.mark.parametrize("n", [4, 16, 20])
+def test_bf16_against_fp64(b, t, d, n):
+    args = make(b, t, d, n, torch.bfloat16, seed=7 * n + d)
+    print(f"case bf16 b{b} t{t} d{d} n{n}", flush=True)
+    hip = run_hip(d, n, args, boundary=True)
+    ref_bf16 = run_oracle(d, n, args, boundary=True)
+    ref64 = run_oracle(d, n, args, boundary=True, dtype=torch.float64)
+    ef = compare(hip, ref64, err_max)
+    er = compare(ref_bf16, ref64, err_max)
+    assert max(ef.values()) <= 1e-2, ef
+    assert all(ef[k] <= 2.0 * er[k] + 2e-3 for k in er), (ef, er)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n", [2, 9, 16])
+@pytest.mark.parametrize("boundary", [False, True])
+def test_zero_query_identity_bitwise(dtype, n, boundary):
+    from loopback_amd import fused_dattn as FD
+    b, t, d = 2, 40, 768
+    deltas, proposal, h0, q, prior, coeffs, up, up2 = make(b, t, d, n, dtype, seed=n, zero_query=True)
+    deltas = [x.to(DEV) for x in deltas]
+    proposal, h0, q, prior = proposal.to(DEV), h0.to(DEV), q.to(DEV), prior.to(DEV)
+    coeffs = prior.view(1, 1, -1).expand(b, t, -1).contiguous()
+    base = proposal + 0.75 * (h0 - proposal) if boundary else proposal
+    base_coeffs = torch.cat((coeffs, torch.ones(b, t, 1, device=DEV)), -1)
+    next_prior = torch.cat((prior, torch.ones(1, device=DEV)), -1)
+    if boundary:
+        base_coeffs, next_prior = 0.25 * base_coeffs, 0.25 * next_prior
+    rstds = [FD.rstd(x, 1e-6) for x in deltas]
+    with torch.no_grad():
+        out, tc = FD.FusedDattnRead.apply(q, base, base_coeffs, next_prior, *deltas, *rstds)
+    assert torch.equal(out, base)
+    assert torch.equal(tc, next_prior.view(1, 1, -1).expand(b, t, -1))
+
+
+def test_rstd_matches_reference_scale():
+    from loopback_amd import fused_dattn as FD
+    from oracle.reference_read import rstd_ref
+    for dtype in (torch.float32, torch.bfloat16):
+        x = (torch.randn(3, 33, 1536, generator=torch.Generator().manual_seed(4)) * 1.7).to(dtype)
+        xg = x.to(DEV).requires_grad_()
+        r = FD.rstd(xg, 1e-6)
+        gr = torch.randn(3, 33, 1, generator=torch.Generator().manual_seed(5))
+        (r * gr.to(DEV)).sum().backward()
+        xc = x.double().requires_grad_()
+        rr = rstd_ref(xc, 1e-6)
+        (rr * gr.double()).sum().backward()
+        assert err_rms(r.detach(), rr.detach()) <= 1e-6
+        tol = 1e-5 if dtype == torch.float32 else 1e-2
+        assert err_max(xg.grad, xc.grad) <= tol
+
+
+def test_accumulating_list_layout_matches_plain():
+    """FusedDattnReadAcc (in-kernel accumulation, fused_dattn.py:353-376) gives the plain list layout's gradients:
+    a three-read chain over shared sources, bf16."""
+    from loopback_amd import fused_dattn as FD
+    d, b, t = 256, 1, 64
+    gen = torch.Generator().manual_seed(21)
+    vals = [torch.randn(b, t, d, generator=gen).to(torch.bfloat16) for _ in range(4)]
+    qs = torch.randn(3, d, generator=gen) * 0.5
+    results = []
+    for accumulate in (False, True):
+        vs = [v.to(DEV).requires_grad_() for v in vals]
+        acc = FD.DattnGradAccum()
+        rs = [FD.rstd(v, 1e-6) for v in vs]
+        loss = 0.0
+        cbar = torch.ones(b, t, 1, device=DEV)
+        prior = torch.ones(1, device=DEV)
+        for s in range(1, 4):
+            base = vs[s] * 0.5
+            cb = torch.cat((cbar, torch.ones(b, t, 1, device=DEV)), -1)
+            pr = torch.cat((prior, torch.ones(1, device=DEV)), -1)
+            srcs = (*vs[:s + 1], *rs[:s + 1])
+            if accumulate:
+                out, tc = FD.FusedDattnReadAcc.apply(acc, s, qs[s - 1].to(DEV), base, cb, pr, *srcs)
+            else:
+                out, tc = FD.FusedDattnRead.apply(qs[s - 1].to(DEV), base, cb, pr, *srcs)
+            loss = loss + out.float().pow(2).mean()
+            cbar, prior = tc, pr
+        loss.backward()
+        results.append([v.grad.float().cpu() for v in vs])
+    for a, b_ in zip(*results):
+        assert err_max(a, b_) <= 1e-2

@@ -1,0 +1,124 @@
+"""The stacked layout (DattnStack + FusedDattnReadStk, the trainer's default) and the list layout in K x R chains
+against the oracle chain; mirrors tests/test_dattn_stack.py:68-199 of the reference.
+
+  1. chains with blocks x -> x + D_s, every path ('list', 'stack' = stacked with online scores, 'scores' = stacked
+     with scores stored at the write), fp32 and bf16: the final state and the gradients of h0, every D_s and the
+     query against the oracle chain in the same dtype (norm-relative 1e-5 in fp32, 1e-2 in bf16); in bf16 also no
+     further from the fp64 oracle than the reference read itself is (<= 2 err_ref + 2e-3); 'list' and 'stack' run
+     the same kernels, so their outputs agree bitwise;
+  2. eval (no grad) chains;
+  3. memory: a loss kept after its backward holds no stack.
+"""
+import pytest
+import torch
+
+from gpu_helpers import DEV, err_max, err_norm
+from oracle.reference_read import run_chain as oracle_chain
+
+pytestmark = pytest.mark.gpu
+
+
+def chain_cfg(K, R, dtype, d=256, t=512, backward=True):
+    from loopback_amd.chain import ChainConfig
+    return ChainConfig(f"test-K{K}R{R}", d, K, R, 1, t, dtype, backward, q_std=0.5)
+
+
+def hip_chain(cfg, mode, grad=True):
+    from loopback_amd.chain import make_inputs, run_chain
+    h0, D, Q, G = make_inputs(cfg, "cpu")
+    h, loss, grads = run_chain(cfg, h0.to(DEV), [x.to(DEV) for x in D], Q.to(DEV), G.to(DEV), mode, grad=grad)
+    torch.cuda.synchronize()
+    return h.cpu(), grads
+
+
+def ref_chain(cfg, dtype, grad=True):
+    from loopback_amd.chain import make_inputs
+    h0, D, Q, G = make_inputs(cfg, "cpu")
+    if dtype == torch.float64:
+        h0, D, Q, G = h0.double(), [x.double() for x in D], Q.double(), G.double()
+    states, _, _, _, grads = oracle_chain(cfg.K, cfg.R, h0, D, Q, G, beta=cfg.beta, eps=cfg.eps, grad=grad)
+    return states[-1], grads
+
+
+def grad_list(g):
+    return [g["h0"], g["query"]] + list(g["D"])
+
+
+@pytest.mark.parametrize("K,R", [(2, 4), (3, 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["list", "stack", "scores"])
+def test_chain_matches_oracle(K, R, dtype, mode):
+    cfg = chain_cfg(K, R, dtype)
+    print(f"case chain K{K} R{R} {dtype} {mode}", flush=True)
+    h, g = hip_chain(cfg, mode)
+    hr, gr = ref_chain(cfg, None)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert err_norm(h, hr) <= tol
+    worst = max(err_norm(a, b) for a, b in zip(grad_list(g), grad_list(gr)))
+    assert worst <= tol, worst
+    if dtype == torch.bfloat16:
+        h64, g64 = ref_chain(cfg, torch.float64)
+        assert err_norm(h, h64) <= 2 * err_norm(hr, h64) + 2e-3
+        for a, b, c in zip(grad_list(g), grad_list(gr), grad_list(g64)):
+            assert err_norm(a, c) <= 2 * err_norm(b, c) + 2e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_list_and_stack_outputs_bitwise(dtype):
+    cfg = chain_cfg(3, 3, dtype)
+    hl, gl = hip_chain(cfg, "list")
+    hs, gs = hip_chain(cfg, "stack")
+    assert torch.equal(hl, hs)
+    hw, gw = hip_chain(cfg, "scores")
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert err_norm(hw, hl) <= tol
+    assert max(err_norm(a, b) for a, b in zip(grad_list(gw), grad_list(gl))) <= tol
+
+
+def test_eval_chains():
+    cfg = chain_cfg(3, 3, torch.bfloat16, backward=False)
+    hl, _ = hip_chain(cfg, "list", grad=False)
+    hs, _ = hip_chain(cfg, "stack", grad=False)
+    hw, _ = hip_chain(cfg, "scores", grad=False)
+    hr, _ = ref_chain(cfg, None, grad=False)
+    assert torch.equal(hl, hs)
+    assert err_norm(hw, hr) <= 1e-2 and err_norm(hl, hr) <= 1e-2
+
+
+@pytest.mark.parametrize("mode", ["stack", "scores"])
+def test_kept_loss_holds_no_stack(mode):
+    """After one chain's backward, keeping only its loss (and so its graph) keeps < 5 % of the stack's bytes
+    (tests/test_dattn_stack.py:161-199)."""
+    from loopback_amd.cell import LoopDeltaAttnRes
+    K, R, N, d = 2, 4, 8192, 256
+
+    def once():
+        cell = LoopDeltaAttnRes(d, R, K, beta=0.75, eps=1e-6).to(DEV)
+        with torch.no_grad():
+            cell.query.normal_(0, 0.5)
+        gen = torch.Generator().manual_seed(0)
+        Ds = [(torch.randn(1, N, d, generator=gen) * 0.5).to(torch.bfloat16).to(DEV).requires_grad_()
+              for _ in range(K * R)]
+        h0 = (torch.randn(1, N, d, generator=gen) * 0.5).to(torch.bfloat16).to(DEV).requires_grad_()
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated()
+        stack = cell.new_stack(h0.shape, h0.dtype, h0.device, mode=mode)
+        h, deltas, keys, coeffs, prior = h0, [], [], None, None
+        for s in range(K * R):
+            l, blk = divmod(s, K)
+            hs = h + Ds[s]
+            deltas.append(stack.write(s, hs, h))
+            h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
+        loss = (h.float() ** 2).mean()
+        loss.backward()
+        stack_bytes = 2 * (stack.V.numel() * stack.V.element_size() + stack.R.numel() * stack.R.element_size())
+        del stack, h, hs, deltas, keys, coeffs, prior
+        for p in (*Ds, h0, cell.query):
+            p.grad = None
+        torch.cuda.synchronize()
+        return torch.cuda.memory_allocated() - before, stack_bytes, loss
+
+    once()
+    held, stack_bytes, kept = once()
+    assert held < 0.05 * stack_bytes, (held, stack_bytes)
+    del kept

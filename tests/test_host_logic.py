@@ -1,0 +1,94 @@
+"""Host-side logic that runs without a GPU: the drop-in's gates and errors, the stack's bookkeeping, the traffic
+formula the bench reports against, and the bench's refusal of several GPUs."""
+import os
+import subprocess
+import sys
+
+import pytest
+import torch
+
+from loopback_amd import chain as C
+from loopback_amd import fused_dattn as FD
+from loopback_amd.cell import LoopDeltaAttnRes, stack_mode
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_interface_names():
+    for name in ("rstd_ref", "rstd", "fused_read_supported", "FusedDattnRead", "DattnGradAccum", "FusedDattnReadAcc",
+                 "DattnStack", "FusedDattnReadStk", "_alias"):
+        assert hasattr(FD, name), name
+    for attr in ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "DOTS", "r_done"):
+        assert attr in FD.DattnStack.__slots__
+
+
+def test_supported_is_false_on_cpu():
+    v = [torch.randn(1, 4, 64) for _ in range(3)]
+    r = [torch.ones(1, 4, 1) for _ in range(3)]
+    assert FD.fused_read_supported(v[0].clone(), v, r, torch.ones(1, 4, 3)) is False
+
+
+def test_rstd_refuses_cpu_tensors():
+    with pytest.raises(RuntimeError, match="GPU"):
+        FD.rstd(torch.randn(2, 3, 64), 1e-6)
+
+
+def test_stack_refuses_cpu_and_bad_shapes():
+    with pytest.raises(RuntimeError):
+        FD.DattnStack(4, (1, 8, 64), torch.bfloat16, "cpu")
+    with pytest.raises(RuntimeError):
+        FD.DattnStack(4, (1, 8, 60), torch.bfloat16, "cpu")
+    with pytest.raises(RuntimeError):
+        FD.DattnStack(65, (1, 8, 64), torch.bfloat16, "cpu")
+
+
+def test_pair_rows_cover_the_triangle():
+    N = 32
+    rows = [FD._pair(s, i) for s in range(1, N) for i in range(s + 1)]
+    assert rows == list(range(N * (N + 1) // 2 - 1))
+
+
+def test_cell_validation_errors():
+    cell = LoopDeltaAttnRes(64, 2, 3)
+    assert tuple(cell.query.shape) == (5, 64) and torch.count_nonzero(cell.query) == 0
+    x = torch.zeros(1, 2, 64)
+    with pytest.raises(ValueError):
+        cell.combine(x, x, [x], None, None, 0, 3)
+    with pytest.raises(ValueError):
+        cell.combine(x, x, [x], None, None, 2, 0)
+    with pytest.raises(ValueError):
+        cell.combine(x, x, [x, x], None, None, 0, 0)
+    with pytest.raises(ValueError):
+        LoopDeltaAttnRes(64, 0, 3)
+    with pytest.raises(ValueError):
+        LoopDeltaAttnRes(64, 2, 3, beta=1.0)
+
+
+def test_mode_flags(monkeypatch):
+    monkeypatch.setenv("LOOP_DATTN_STACK", "1")
+    monkeypatch.setenv("LOOP_DATTN_DOTS", "1")
+    assert stack_mode() == "scores"
+    monkeypatch.setenv("LOOP_DATTN_DOTS", "0")
+    assert stack_mode() == "stack"
+    monkeypatch.setenv("LOOP_DATTN_STACK", "0")
+    assert stack_mode() == "list"
+
+
+def test_traffic_formula_matches_the_survey():
+    # headline: d=2048, N=32, bf16 -> 9,797,632 bulk bytes per token; config 3: 849,944 total incl. scalars
+    parts = C.algorithmic_bytes_per_token(32, 2048, 2)
+    assert parts["total"] == 9_797_632
+    assert C.algorithmic_bytes_per_token(8, 768, 2, backward=False)["total"] == (3 * 8 + 35 + 14) * 768 * 2
+
+
+def test_configs():
+    c4 = C.CONFIGS["c4"]
+    assert (c4.d, c4.N, c4.n_tok, c4.dtype, c4.backward) == (2048, 32, 16384, torch.bfloat16, True)
+    assert C.CONFIGS["c1"].n_tok == 512 and C.CONFIGS["c3"].N == 12
+
+
+def test_bench_refuses_several_gpus():
+    res = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode != 0
+    assert "one GPU" in (res.stdout + res.stderr)

@@ -1,0 +1,83 @@
+"""The C ABI library on CPU: it loads, exports every symbol include/loopback_read.h declares, and its host-side
+argument checks reject bad calls before any launch (no GPU is touched by these calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from loopback_amd import build as B
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "loopback_read.h")
+
+
+def declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(ldr_\w+)\s*\(", txt)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(B.LIB):
+        B.build(verbose=False)
+    from loopback_amd import _lib
+    return _lib
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "ldr_read_fwd" in names and "ldr_read_bwd1" in names and "ldr_dv_assemble" in names
+    assert len(names) >= 13
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(lib.PATH)
+    missing = [n for n in declared() if not hasattr(raw, n)]
+    assert not missing, missing
+    assert set(declared()) == set(lib.SIGNATURES), "the ctypes signature table must cover the header exactly"
+
+
+def test_abi_version_and_messages(lib):
+    assert lib.LIB.ldr_abi_version() == lib.ABI_VERSION
+    for code in (0, -1, -2, -3, -4):
+        assert lib.LIB.ldr_strerror(code).decode()
+
+
+@pytest.mark.parametrize("d,expect", [(2048, (4, 64)), (768, (3, 32)), (1024, (2, 64)), (64, (1, 8)),
+                                      (1536, (3, 64)), (3072, (3, 128)), (256, (1, 32)), (8192, (4, 256))])
+def test_row_layout(lib, d, expect):
+    vpt, tpr = lib.row_layout(d)
+    assert (vpt, tpr) == expect
+    assert vpt * tpr * 8 >= d and tpr & (tpr - 1) == 0
+
+
+@pytest.mark.parametrize("d", [0, 7, 100, 8200])
+def test_row_layout_rejects(lib, d):
+    with pytest.raises(RuntimeError):
+        lib.row_layout(d)
+
+
+def test_bwd1_parts(lib):
+    assert lib.bwd1_parts(16384, 2048) == 512
+    assert lib.bwd1_parts(20, 2048) == 2          # 16-token tiles
+    assert lib.bwd1_parts(0, 2048) == 0
+
+
+def test_argument_checks_before_launch(lib):
+    L = lib.LIB
+    null = ctypes.c_void_p(0)
+    assert L.ldr_rstd_fwd(null, null, 16, 64, 1e-6, 1, null) == -1
+    assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 60, 1e-6, 1, null) == -2
+    assert L.ldr_rstd_fwd(ctypes.c_void_p(4100), ctypes.c_void_p(4096), 16, 64, 1e-6, 1, null) == -3
+    assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 64, 1e-6, 7, null) == -4
+    too_many = lib.u64_array([4096] * 65)
+    assert L.ldr_dots_online(too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, 1, null) == -1
+    assert L.ldr_write_dots(ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096),
+                            ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 64, 65, 16, 1e-6,
+                            1, null) == -2
+    assert L.ldr_dv_assemble(too_many, too_many, too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), null,
+                             ctypes.c_void_p(4096), 16, 64, 1, null) == -2
+    # zero tokens: accepted, nothing launched
+    assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 0, 64, 1e-6, 1, null) == 0
