@@ -8,9 +8,10 @@ backward -- N writes (with the read-query scores), N-1 reads, their backwards, t
 synthetic blocks x -> x + D_s and the caller's torch glue included. Inputs are resident in HBM before timing.
 
 Prints ONE JSON line (rank 0): the metric of BASELINE.json (read tokens/s = T * steps / wall time), plus
-  roofline      the dominant kernel: algorithmic bytes per launch (the traffic formula of the stacked dataflow, per
-                kernel family) / its mean launch duration, from HIP events on the launch stream, against 8 TB/s;
-  chain         the same over every library kernel of the pass (formula bytes * T / summed kernel time);
+  roofline      the dominant kernel (most time per pass): its compulsory bytes per launch / its mean launch
+                duration, from HIP events on the launch stream during the last timed step, against 8 TB/s;
+  chain         every library kernel of the pass: compulsory bytes / summed kernel time, and the reference
+                dataflow's formula bytes (SURVEY) over the same time and over the wall time;
   cpu_baseline  the CPU oracle (the restated reference read, fp32/bf16 torch on the host cores) on a bounded sample
                 of the same chain (T reduced), fwd+bwd, tokens/s.
 """
@@ -68,16 +69,29 @@ class KernelTimer:
 
 
 def family_bytes(cfg, mode):
-    """Algorithmic bytes per pass (T tokens) of each kernel family, from the per-token formula."""
+    """Compulsory HBM bytes per pass (T tokens) of each kernel family of this build -- what each kernel must move:
+    write 3 rows per token (h, x in; V out), read (n+2) (n sources, base in; out), scores online n, backward pass 1
+    (n+1) (n sources, g), update gradient (m+2) (the m output gradients of the reads holding the update, the update,
+    the result) -- in rows of e * d bytes; per-(token, source) fp32 scalars left out (< 1 %).
+    Also the reference dataflow's total (the formula of the survey), which moves more in its backward."""
     from loopback_amd.chain import algorithmic_bytes_per_token
-    e = 2 if str(cfg.dtype).endswith("bfloat16") else 4
-    parts = algorithmic_bytes_per_token(cfg.N, cfg.d, e, backward=cfg.backward, dots=(mode == "scores"))
-    T = cfg.n_tok
-    fam = {"write_dots": parts["write"] * T, "read_fwd": parts["read_fwd"] * T}
+    e = 2 if cfg.dtype == torch_bf16() else 4
+    N, T = cfg.N, cfg.n_tok
+    S2 = N * (N + 1) // 2 - 1
+    row = e * cfg.d * T
+    fam = {"write_dots": 3 * N * row, "read_fwd": (S2 + 2 * (N - 1)) * row}
+    if mode != "scores":
+        fam["dots_online"] = S2 * row
     if cfg.backward:
-        fam["read_bwd1"] = parts["bwd1"] * T
-        fam["dv_assemble"] = (parts["bwd2"] + parts["rstd_bwd"]) * T   # this build forms dV once per update
-    return fam, parts["total"] * T
+        fam["read_bwd1"] = (S2 + N - 1) * row
+        fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 2 * N) * row
+    ref_total = algorithmic_bytes_per_token(N, cfg.d, e, backward=cfg.backward, dots=(mode == "scores"))["total"] * T
+    return fam, ref_total
+
+
+def torch_bf16():
+    import torch
+    return torch.bfloat16
 
 
 def cpu_baseline(cfg, tokens):
@@ -134,7 +148,8 @@ def main():
     FD._TIMER = None
     ms_per_step = 1e3 * elapsed / args.steps
     ksum = timer.summary()
-    fam, total_bytes = family_bytes(cfg, args.mode)
+    fam, ref_bytes = family_bytes(cfg, args.mode)
+    own_bytes = sum(fam.values())
     dom = max((k for k in fam if k in ksum), key=lambda k: ksum[k]["total_ms"])
     launches = ksum[dom]["launches"]
     bytes_per_launch = fam[dom] / launches
@@ -167,9 +182,11 @@ def main():
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": bytes_per_launch, "mean_launch_us": ksum[dom]["mean_us"],
                      "launches_per_step": launches},
-        "chain": {"algorithmic_bytes_per_token": total_bytes / cfg.n_tok, "kernel_ms": kernel_ms,
-                  "achieved_gbs": total_bytes / (kernel_ms * 1e-3) / 1e9,
-                  "wall_gbs": total_bytes / (ms_per_step * 1e-3) / 1e9,
+        "chain": {"own_bytes_per_token": own_bytes / cfg.n_tok, "kernel_ms": kernel_ms,
+                  "achieved_gbs": own_bytes / (kernel_ms * 1e-3) / 1e9,
+                  "reference_formula_bytes_per_token": ref_bytes / cfg.n_tok,
+                  "formula_gbs": ref_bytes / (kernel_ms * 1e-3) / 1e9,
+                  "formula_wall_gbs": ref_bytes / (ms_per_step * 1e-3) / 1e9,
                   "kernels": {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 4),
                                   "gbs": (fam[k] / (v["total_ms"] * 1e-3) / 1e9) if k in fam else None}
                               for k, v in sorted(ksum.items())}},

@@ -17,7 +17,44 @@
 #include <stddef.h>
 #include <math.h>
 
+#include <type_traits>
+
 #include "loopback_read.h"
+
+// Launch-shape tunables (compile-time; the defaults are the measured choice on MI355X).
+#ifndef LDR_RF_UNROLL
+#define LDR_RF_UNROLL 8      // read forward: sources loaded per batch
+#endif
+#ifndef LDR_RF_MAX_VPT
+#define LDR_RF_MAX_VPT 2     // read forward: most 16-byte vectors per lane in a row
+#endif
+#ifndef LDR_AS_RB
+#define LDR_AS_RB 2          // update gradient: token rows per lane
+#endif
+#ifndef LDR_AS_JB
+#define LDR_AS_JB 4          // update gradient: reads whose rows are loaded together
+#endif
+#ifndef LDR_AS_MAX_VPT
+#define LDR_AS_MAX_VPT 2
+#endif
+#ifndef LDR_B1_MAX_VPT
+#define LDR_B1_MAX_VPT 3     // backward pass 1 (holds g and two accumulators per element)
+#endif
+#ifndef LDR_B1_WAVE_ROWS
+#define LDR_B1_WAVE_ROWS 0   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
+#endif
+#ifndef LDR_NT
+#define LDR_NT 1             // non-temporal loads for the streamed sources
+#endif
+#ifndef LDR_RF_VPT
+#define LDR_RF_VPT 0         // fixed vectors per lane (0 = chosen from d) for the read forward,
+#endif
+#ifndef LDR_AS_VPT
+#define LDR_AS_VPT 0         // the update gradient
+#endif
+#ifndef LDR_B1_VPT
+#define LDR_B1_VPT 0         // and backward pass 1
+#endif
 
 namespace {
 
@@ -44,9 +81,22 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 
 template <typename T> struct IO;
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 template <> struct IO<bf16_t> {
   struct Raw { uint4 u; };
   static __device__ __forceinline__ Raw raw(const bf16_t* p) { Raw r; r.u = *reinterpret_cast<const uint4*>(p); return r; }
+  // non-temporal: for data read once per kernel and not again soon (the update stack, the output gradient)
+  static __device__ __forceinline__ Raw raw_nt(const bf16_t* p) {
+    Raw r;
+#if LDR_NT
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    r.u = make_uint4(v.x, v.y, v.z, v.w);
+#else
+    r.u = *reinterpret_cast<const uint4*>(p);
+#endif
+    return r;
+  }
   static __device__ __forceinline__ Raw zero() { Raw r; r.u = make_uint4(0u, 0u, 0u, 0u); return r; }
   static __device__ __forceinline__ void unpack(const Raw& r, float (&o)[8]) {
     o[0] = __uint_as_float(r.u.x << 16); o[1] = __uint_as_float(r.u.x & 0xffff0000u);
@@ -68,6 +118,7 @@ template <> struct IO<float> {
   static __device__ __forceinline__ Raw raw(const float* p) {
     Raw r; r.a = reinterpret_cast<const float4*>(p)[0]; r.b = reinterpret_cast<const float4*>(p)[1]; return r;
   }
+  static __device__ __forceinline__ Raw raw_nt(const float* p) { return raw(p); }
   static __device__ __forceinline__ Raw zero() { Raw r; r.a = make_float4(0.f, 0.f, 0.f, 0.f); r.b = r.a; return r; }
   static __device__ __forceinline__ void unpack(const Raw& r, float (&o)[8]) {
     o[0] = r.a.x; o[1] = r.a.y; o[2] = r.a.z; o[3] = r.a.w; o[4] = r.b.x; o[5] = r.b.y; o[6] = r.b.z; o[7] = r.b.w;
@@ -90,6 +141,10 @@ struct Rows {
   __device__ __forceinline__ Rows(int d, int tpr_)
       : d8(d >> 3), tpr(tpr_), rpw(WG / tpr_), rs((int)threadIdx.x / tpr_), lr((int)threadIdx.x % tpr_) {}
   __device__ __forceinline__ int c8(int v) const { return lr + v * tpr; }
+  __device__ __forceinline__ bool act(int v) const { return c8(v) < d8; }
+  // element offset of vector v inside a row, clamped to the row for lanes past its end: loads stay unconditional
+  // (a branch around a load makes the compiler wait for it before the next one), only stores test act(v)
+  __device__ __forceinline__ int off(int v) const { const int c = c8(v); return (c < d8 ? c : d8 - 1) * 8; }
 };
 
 // Sum NV values over the tpr lanes of a row (tpr a power of two); every lane of the row ends with the totals,
@@ -163,19 +218,15 @@ __global__ __launch_bounds__(WG) void k_rstd_fwd(const T* __restrict__ x, float*
   const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
   for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
     const int64_t tok = gi * R.rpw + R.rs;
+    const T* row = x + (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
     float ss[1] = {0.f};
-    if (tok < n_tok) {
-      const T* row = x + tok * (int64_t)d;
 #pragma unroll
-      for (int v = 0; v < VPT; ++v) {
-        const int c8 = R.c8(v);
-        if (c8 < R.d8) {
-          float e[8];
-          IO<T>::load(row + c8 * 8, e);
+    for (int v = 0; v < VPT; ++v) {
+      float e[8];
+      IO<T>::load(row + R.off(v), e);
+      const float keep = R.act(v) ? 1.f : 0.f;
 #pragma unroll
-          for (int k = 0; k < 8; ++k) ss[0] += e[k] * e[k];
-        }
-      }
+      for (int k = 0; k < 8; ++k) ss[0] += keep * e[k] * e[k];
     }
     row_sum<1>(ss, tpr, red);
     if (tok < n_tok && R.lr == 0) r[tok] = rsqrtf(ss[0] / (float)d + eps);
@@ -193,16 +244,14 @@ __global__ __launch_bounds__(WG) void k_rstd_bwd(const T* __restrict__ x, const 
     if (tok >= n_tok) continue;
     const float rv = r[tok];
     const float c = gr[tok] * (-rv * rv * rv) / (float)d;
+    float e[VPT][8];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) IO<T>::load(x + tok * (int64_t)d + R.off(v), e[v]);
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
-      const int c8 = R.c8(v);
-      if (c8 < R.d8) {
-        float e[8];
-        IO<T>::load(x + tok * (int64_t)d + c8 * 8, e);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) e[k] = c * e[k];
-        IO<T>::store(gx + tok * (int64_t)d + c8 * 8, e);
-      }
+      for (int k = 0; k < 8; ++k) e[v][k] = c * e[v][k];
+      if (R.act(v)) IO<T>::store(gx + tok * (int64_t)d + R.c8(v) * 8, e[v]);
     }
   }
 }
@@ -315,19 +364,14 @@ __global__ __launch_bounds__(WG) void k_dots(SrcTab src, int n, const float* __r
   for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
     const int64_t tok = gi * R.rpw + R.rs;
     const bool valid = tok < n_tok;
-    for (int i0 = 0; i0 < n; i0 += C) {
+    const int64_t roff = (valid ? tok : n_tok - 1) * (int64_t)d;
+    int i0 = 0;
+    for (; i0 + C <= n; i0 += C) {
       typename IO<T>::Raw raw[C][VPT];
 #pragma unroll
-      for (int c = 0; c < C; ++c) {
+      for (int c = 0; c < C; ++c)
 #pragma unroll
-        for (int v = 0; v < VPT; ++v) {
-          const int c8 = R.c8(v);
-          if (valid && i0 + c < n && c8 < R.d8)
-            raw[c][v] = IO<T>::raw(static_cast<const T*>(src.v[i0 + c]) + tok * (int64_t)d + c8 * 8);
-          else
-            raw[c][v] = IO<T>::zero();
-        }
-      }
+        for (int v = 0; v < VPT; ++v) raw[c][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0 + c]) + roff + R.off(v));
       float pd[C];
 #pragma unroll
       for (int c = 0; c < C; ++c) {
@@ -343,9 +387,20 @@ __global__ __launch_bounds__(WG) void k_dots(SrcTab src, int n, const float* __r
       row_sum<C>(pd, tpr, red);
       if (valid && R.lr == 0) {
 #pragma unroll
-        for (int c = 0; c < C; ++c)
-          if (i0 + c < n) out[(int64_t)(i0 + c) * out_stride + tok] = pd[c];
+        for (int c = 0; c < C; ++c) out[(int64_t)(i0 + c) * out_stride + tok] = pd[c];
       }
+    }
+    for (; i0 < n; ++i0) {
+      float pd[1] = {0.f};
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        float e[8];
+        IO<T>::load(static_cast<const T*>(src.v[i0]) + roff + R.off(v), e);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pd[0] += qv[v][k] * e[k];
+      }
+      row_sum<1>(pd, tpr, red);
+      if (valid && R.lr == 0) out[(int64_t)i0 * out_stride + tok] = pd[0];
     }
   }
 }
@@ -415,55 +470,62 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
       const int64_t tok = t0 + rr;
       if (tok >= n_tok) break;
       const float* wrow = &s_w[rr * SP];
+      const int64_t roff = tok * (int64_t)d;
       float acc[VPT][8];
 #pragma unroll
-      for (int v = 0; v < VPT; ++v) {
-        const int c8 = R.c8(v);
-        if (c8 < R.d8) IO<T>::load(base + tok * (int64_t)d + c8 * 8, acc[v]);
-      }
+      for (int v = 0; v < VPT; ++v) IO<T>::load(base + roff + R.off(v), acc[v]);
       int i = 0;
-      for (; i + 4 <= n; i += 4) {
-        typename IO<T>::Raw raw[4][VPT];
+      constexpr int U = LDR_RF_UNROLL;
+      for (; i + U <= n; i += U) {
+        typename IO<T>::Raw raw[U][VPT];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-          for (int v = 0; v < VPT; ++v) {
-            const int c8 = R.c8(v);
-            if (c8 < R.d8) raw[u][v] = IO<T>::raw(static_cast<const T*>(src.v[i + u]) + tok * (int64_t)d + c8 * 8);
-          }
-        }
+          for (int v = 0; v < VPT; ++v) raw[u][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i + u]) + roff + R.off(v));
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < U; ++u) {
           const float w = wrow[i + u];
 #pragma unroll
           for (int v = 0; v < VPT; ++v) {
-            if (R.c8(v) < R.d8) {
-              float e[8];
-              IO<T>::unpack(raw[u][v], e);
-#pragma unroll
-              for (int k = 0; k < 8; ++k) acc[v][k] += w * e[k];
-            }
-          }
-        }
-      }
-      for (; i < n; ++i) {
-        const float w = wrow[i];
-#pragma unroll
-        for (int v = 0; v < VPT; ++v) {
-          const int c8 = R.c8(v);
-          if (c8 < R.d8) {
             float e[8];
-            IO<T>::load(static_cast<const T*>(src.v[i]) + tok * (int64_t)d + c8 * 8, e);
+            IO<T>::unpack(raw[u][v], e);
 #pragma unroll
             for (int k = 0; k < 8; ++k) acc[v][k] += w * e[k];
           }
         }
       }
+      if (U > 4 && i + 4 <= n) {
+        typename IO<T>::Raw raw[4][VPT];
 #pragma unroll
-      for (int v = 0; v < VPT; ++v) {
-        const int c8 = R.c8(v);
-        if (c8 < R.d8) IO<T>::store(out + tok * (int64_t)d + c8 * 8, acc[v]);
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) raw[u][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i + u]) + roff + R.off(v));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float w = wrow[i + u];
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) {
+            float e[8];
+            IO<T>::unpack(raw[u][v], e);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[v][k] += w * e[k];
+          }
+        }
+        i += 4;
       }
+      for (; i < n; ++i) {
+        const float w = wrow[i];
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          float e[8];
+          IO<T>::load(static_cast<const T*>(src.v[i]) + roff + R.off(v), e);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc[v][k] += w * e[k];
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < VPT; ++v)
+        if (R.act(v)) IO<T>::store(out + roff + R.c8(v) * 8, acc[v]);
     }
     __syncthreads();
   }
@@ -473,7 +535,7 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
 // backward pass 1: the only re-read of the sources
 // ---------------------------------------------------------------------------------------------------------------
 constexpr int B1_GRID = 512;
-constexpr int B1_MAX_VPT = 2;   // k_bwd1 holds g and two fp32 accumulators per element
+constexpr int B1_MAX_VPT = LDR_B1_MAX_VPT;
 
 template <typename T, int VPT, int C>
 __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restrict__ g, const float* __restrict__ gt,
@@ -527,15 +589,15 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
     __syncthreads();
     const int rows_per_slot = (tt + R.rpw - 1) / R.rpw;
     for (int rk = 0; rk < rows_per_slot; ++rk) {   // uniform trip count: row_sum may hold barriers
-      const int rr = R.rs + rk * R.rpw;
+      const int rr = R.rs + rk * R.rpw;            // < tt: tt is a multiple of rpw
       const int64_t tok = t0 + rr;
-      const bool valid = rr < tt && tok < n_tok;
+      const bool valid = tok < n_tok;
+      const int64_t roff = (valid ? tok : n_tok - 1) * (int64_t)d;
       float gv[VPT][8];
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
-        const int c8 = R.c8(v);
-        if (valid && c8 < R.d8) IO<T>::load(g + tok * (int64_t)d + c8 * 8, gv[v]);
-        else {
+        IO<T>::unpack(IO<T>::raw_nt(g + roff + R.off(v)), gv[v]);
+        if (!R.act(v)) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) gv[v][k] = 0.f;
         }
@@ -546,19 +608,32 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
 #pragma unroll
         for (int k = 0; k < 8; ++k) { a[v][k] = 0.f; b[v][k] = 0.f; }
       float sacc = 0.f;
-      for (int i0 = 0; i0 < n; i0 += C) {
-        typename IO<T>::Raw raw[C][VPT];
+      // one source's share once its g.v is known: the scalars, the two accumulators, g.v to LDS
+      auto take = [&](int i, float gd, const typename IO<T>::Raw (&rw)[VPT]) {
+        const float p = s_p[rr * SP + i];
+        const float pr = p * s_r[rr * SP + i];
+        const float gp = M * (gd + s_gt[rr * SP + i]);
+        sacc += p * gp;
+        const float alpha = pr * gp;
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
+        for (int v = 0; v < VPT; ++v) {
+          float e[8];
+          IO<T>::unpack(rw[v], e);
 #pragma unroll
-          for (int v = 0; v < VPT; ++v) {
-            const int c8 = R.c8(v);
-            if (valid && i0 + c < n && c8 < R.d8)
-              raw[c][v] = IO<T>::raw(static_cast<const T*>(src.v[i0 + c]) + tok * (int64_t)d + c8 * 8);
-            else
-              raw[c][v] = IO<T>::zero();
+          for (int k = 0; k < 8; ++k) {
+            a[v][k] += alpha * e[k];
+            b[v][k] += pr * e[k];
           }
         }
+        if (R.lr == 0) s_gd[rr * SP + i] = gd;
+      };
+      int i0 = 0;
+      for (; i0 + C <= n; i0 += C) {
+        typename IO<T>::Raw raw[C][VPT];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) raw[c][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0 + c]) + roff + R.off(v));
         float pd[C];
 #pragma unroll
         for (int c = 0; c < C; ++c) {
@@ -574,29 +649,23 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
         row_sum<C>(pd, tpr, red);
         if (valid) {
 #pragma unroll
-          for (int c = 0; c < C; ++c) {
-            const int i = i0 + c;
-            if (i < n) {
-              const float gd = pd[c];
-              const float p = s_p[rr * SP + i];
-              const float pr = p * s_r[rr * SP + i];
-              const float gp = M * (gd + s_gt[rr * SP + i]);
-              sacc += p * gp;
-              const float alpha = pr * gp;
-#pragma unroll
-              for (int v = 0; v < VPT; ++v) {
-                float e[8];
-                IO<T>::unpack(raw[c][v], e);
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                  a[v][k] += alpha * e[k];
-                  b[v][k] += pr * e[k];
-                }
-              }
-              if (R.lr == 0) s_gd[rr * SP + i] = gd;
-            }
-          }
+          for (int c = 0; c < C; ++c) take(i0 + c, pd[c], raw[c]);
         }
+      }
+      for (; i0 < n; ++i0) {
+        typename IO<T>::Raw raw[1][VPT];
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) raw[0][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0]) + roff + R.off(v));
+        float pd[1] = {0.f};
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          float e[8];
+          IO<T>::unpack(raw[0][v], e);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) pd[0] += gv[v][k] * e[k];
+        }
+        row_sum<1>(pd, tpr, red);
+        if (valid) take(i0, pd[0], raw[0]);
       }
       if (valid) {
 #pragma unroll
@@ -692,38 +761,33 @@ __global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, c
   const Rows R(d, tpr);
   float qv[VPT][8];
 #pragma unroll
-  for (int v = 0; v < VPT; ++v) {
-    const int c8 = R.c8(v);
-    if (c8 < R.d8) load_f32x8(q + c8 * 8, qv[v]);
-  }
+  for (int v = 0; v < VPT; ++v) load_f32x8(q + R.off(v), qv[v]);
   const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
   for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
     const int64_t tok = gi * R.rpw + R.rs;
     if (tok >= n_tok) continue;
+    const int64_t roff = tok * (int64_t)d;
     float gv[VPT][8];
 #pragma unroll
-    for (int v = 0; v < VPT; ++v) {
-      const int c8 = R.c8(v);
-      if (c8 < R.d8) IO<T>::load(g + tok * (int64_t)d + c8 * 8, gv[v]);
-    }
+    for (int v = 0; v < VPT; ++v) IO<T>::load(g + roff + R.off(v), gv[v]);
     for (int i = 0; i < n; ++i) {
       const float2 s = *reinterpret_cast<const float2*>(wz + 2 * ((int64_t)i * wz_stride + tok));
-      T* dvi = static_cast<T*>(dv.p[i]) + tok * (int64_t)d;
+      T* dvi = static_cast<T*>(dv.p[i]) + roff;
+      float prev[VPT][8];
+      if (accum) {
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) IO<T>::load(dvi + R.off(v), prev[v]);
+      }
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
-        const int c8 = R.c8(v);
-        if (c8 < R.d8) {
-          float o[8];
+        float o[8];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) o[k] = s.x * gv[v][k] + s.y * qv[v][k];
-          if (accum) {
-            float prev[8];
-            IO<T>::load(dvi + c8 * 8, prev);
+        for (int k = 0; k < 8; ++k) o[k] = s.x * gv[v][k] + s.y * qv[v][k];
+        if (accum) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) o[k] = prev[k] + IO<T>::round(o[k]);
-          }
-          IO<T>::store(dvi + c8 * 8, o);
+          for (int k = 0; k < 8; ++k) o[k] = prev[v][k] + IO<T>::round(o[k]);
         }
+        if (R.act(v)) IO<T>::store(dvi + R.c8(v) * 8, o);
       }
     }
   }
@@ -732,7 +796,8 @@ __global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, c
 // ---------------------------------------------------------------------------------------------------------------
 // stacked layout: the finished gradient of one update from every read that held it, plus its scale's term
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int AS_RB = 2;   // token rows per lane, sharing each query load
+constexpr int AS_RB = LDR_AS_RB;   // token rows per lane, sharing each query load
+constexpr int AS_JB = LDR_AS_JB;   // reads per batch of loads
 
 template <typename T, int VPT>
 __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* __restrict__ vsrc,
@@ -742,12 +807,12 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
   const int64_t rows_per_tile = (int64_t)R.rpw * AS_RB;
   const int64_t tiles = (n_tok + rows_per_tile - 1) / rows_per_tile;
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    int64_t tok[AS_RB];
-    bool ok[AS_RB];
+    int64_t tok[AS_RB], tokc[AS_RB], roff[AS_RB];
 #pragma unroll
     for (int k = 0; k < AS_RB; ++k) {
       tok[k] = tile * rows_per_tile + R.rs + (int64_t)k * R.rpw;
-      ok[k] = tok[k] < n_tok;
+      tokc[k] = tok[k] < n_tok ? tok[k] : n_tok - 1;
+      roff[k] = tokc[k] * (int64_t)d;
     }
     float acc[AS_RB][VPT][8];
 #pragma unroll
@@ -756,46 +821,51 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
       for (int v = 0; v < VPT; ++v)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[k][v][e] = 0.f;
-    for (int j = 0; j < m; ++j) {
-      const T* gj = static_cast<const T*>(tab.g[j]);
-      const float* wzj = tab.wz[j];
-      float qv[VPT][8];
+    // JB reads per batch: their g rows (and query columns) are all in flight before the first multiply-add
+    auto batch = [&](int j0, auto jb_tag) {
+      constexpr int JB = decltype(jb_tag)::value;
+      typename IO<T>::Raw raw[JB][AS_RB][VPT];
+      float2 sc[JB][AS_RB];
+      float qv[JB][VPT][8];
 #pragma unroll
-      for (int v = 0; v < VPT; ++v) {
-        const int c8 = R.c8(v);
-        if (c8 < R.d8) load_f32x8(tab.q[j] + c8 * 8, qv[v]);
+      for (int b = 0; b < JB; ++b) {
+        const T* gj = static_cast<const T*>(tab.g[j0 + b]);
+#pragma unroll
+        for (int k = 0; k < AS_RB; ++k)
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) raw[b][k][v] = IO<T>::raw(gj + roff[k] + R.off(v));
+#pragma unroll
+        for (int k = 0; k < AS_RB; ++k) sc[b][k] = *reinterpret_cast<const float2*>(tab.wz[j0 + b] + 2 * tokc[k]);
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) load_f32x8(tab.q[j0 + b] + R.off(v), qv[b][v]);
       }
 #pragma unroll
-      for (int k = 0; k < AS_RB; ++k) {
-        if (!ok[k]) continue;
-        const float2 s = *reinterpret_cast<const float2*>(wzj + 2 * tok[k]);
+      for (int b = 0; b < JB; ++b)
 #pragma unroll
-        for (int v = 0; v < VPT; ++v) {
-          const int c8 = R.c8(v);
-          if (c8 < R.d8) {
+        for (int k = 0; k < AS_RB; ++k)
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) {
             float e[8];
-            IO<T>::load(gj + tok[k] * (int64_t)d + c8 * 8, e);
+            IO<T>::unpack(raw[b][k][v], e);
 #pragma unroll
-            for (int x = 0; x < 8; ++x) acc[k][v][x] += s.x * e[x] + s.y * qv[v][x];
+            for (int x = 0; x < 8; ++x) acc[k][v][x] += sc[b][k].x * e[x] + sc[b][k].y * qv[b][v][x];
           }
-        }
-      }
-    }
+    };
+    int j = 0;
+    for (; j + AS_JB <= m; j += AS_JB) batch(j, std::integral_constant<int, AS_JB>());
+    for (; j < m; ++j) batch(j, std::integral_constant<int, 1>());
 #pragma unroll
     for (int k = 0; k < AS_RB; ++k) {
-      if (!ok[k]) continue;
-      const float rv = r[tok[k]];
-      const float c = gr ? gr[tok[k]] * (-rv * rv * rv) / (float)d : 0.f;
+      const float rv = r[tokc[k]];
+      const float c = gr ? gr[tokc[k]] * (-rv * rv * rv) / (float)d : 0.f;
+      float e[VPT][8];
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) IO<T>::load(vsrc + roff[k] + R.off(v), e[v]);
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
-        const int c8 = R.c8(v);
-        if (c8 < R.d8) {
-          float e[8];
-          IO<T>::load(vsrc + tok[k] * (int64_t)d + c8 * 8, e);
 #pragma unroll
-          for (int x = 0; x < 8; ++x) acc[k][v][x] += c * e[x];
-          IO<T>::store(dv + tok[k] * (int64_t)d + c8 * 8, acc[k][v]);
-        }
+        for (int x = 0; x < 8; ++x) acc[k][v][x] += c * e[v][x];
+        if (tok[k] < n_tok && R.act(v)) IO<T>::store(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
       }
     }
   }
@@ -804,15 +874,25 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 // ---------------------------------------------------------------------------------------------------------------
 // host side: argument checks, layout choice, dispatch
 // ---------------------------------------------------------------------------------------------------------------
-int row_layout(int64_t d, int* vpt, int* tpr, int max_vpt = 4) {
+int row_layout(int64_t d, int* vpt, int* tpr, int max_vpt = 4, bool wave_rows = true, int force_vpt = 0,
+               bool big_vpt = false) {
   if (d <= 0 || (d & 7) || d > LDR_MAX_WIDTH) return LDR_E_SHAPE;
   const int64_t d8 = d >> 3;
+  if (force_vpt > 0) {   // a fixed number of vectors per lane: the narrowest power-of-two row that covers d
+    int t = 8;
+    while ((int64_t)force_vpt * t < d8 && t < WG) t <<= 1;
+    if ((int64_t)force_vpt * t < d8) return LDR_E_SHAPE;
+    *vpt = force_vpt;
+    *tpr = t;
+    return LDR_OK;
+  }
   int64_t best = INT64_MAX;
   int bv = 0, bt = 0;
   for (int v = 1; v <= max_vpt; ++v) {
     for (int t = 8; t <= WG; t <<= 1) {
       if ((int64_t)v * t < d8) continue;
-      const int64_t key = ((int64_t)v * t - d8) * 16 + (t > 64 ? 8 : 0) + v;   // waste, then one wave per row
+      // waste first, then rows inside one wave (if asked), then fewer (or more) vectors per lane
+      const int64_t key = ((int64_t)v * t - d8) * 16 + (wave_rows && t > 64 ? 8 : 0) + (big_vpt ? 5 - v : v);
       if (key < best) { best = key; bv = v; bt = t; }
     }
   }
@@ -885,7 +965,7 @@ int ldr_row_layout(int64_t d, int* vpt, int* tpr) {
 
 int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d) {
   int vpt, tpr;
-  if (n_tok < 1 || row_layout(d, &vpt, &tpr, B1_MAX_VPT) != LDR_OK) return 0;
+  if (n_tok < 1 || row_layout(d, &vpt, &tpr, B1_MAX_VPT, LDR_B1_WAVE_ROWS, LDR_B1_VPT, true) != LDR_OK) return 0;
   return grid_of(cdiv(n_tok, tile_tokens(tpr)), B1_GRID);
 }
 
@@ -966,7 +1046,7 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
   int e = fill_src(s, src_v, src_r, n);
   if (e) return e;
   int vpt, tpr;
-  if ((e = row_layout(d, &vpt, &tpr))) return e;
+  if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, false, LDR_RF_VPT))) return e;
   if (n_tok == 0) return LDR_OK;
   const int tt = tile_tokens(tpr);
   const unsigned grid = grid_of(cdiv(n_tok, tt), 65535);
@@ -996,7 +1076,7 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
     if (i < n && !drt.p[i]) return LDR_E_ARG;
   }
   int vpt, tpr;
-  if ((e = row_layout(d, &vpt, &tpr, B1_MAX_VPT))) return e;
+  if ((e = row_layout(d, &vpt, &tpr, B1_MAX_VPT, LDR_B1_WAVE_ROWS, LDR_B1_VPT, true))) return e;
   if (n_tok == 0) return LDR_OK;
   const int tt = tile_tokens(tpr);
   const unsigned grid = grid_of(cdiv(n_tok, tt), B1_GRID);
@@ -1052,7 +1132,7 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
     if (j < m && (!t.g[j] || !t.wz[j] || !t.q[j])) return LDR_E_ARG;
     if (j < m && (!al16(t.g[j]) || !al16(t.q[j]) || (reinterpret_cast<uintptr_t>(t.wz[j]) & 7u))) return LDR_E_ALIGN;
   }
-  int vpt, tpr, e = row_layout(d, &vpt, &tpr);
+  int vpt, tpr, e = row_layout(d, &vpt, &tpr, LDR_AS_MAX_VPT, false, LDR_AS_VPT);
   if (e) return e;
   if (n_tok == 0) return LDR_OK;
   const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * AS_RB), 65535);

@@ -2,16 +2,21 @@
 LoopDeltaAttnRes.combine -- on the same seeded inputs; mirrors tests/test_fused_dattn.py:87-125 of the reference.
 
   1. fp32: out, tc and every gradient (the query row, each delta through its value and its RMS scale, proposal and
-     h0 through base, the previous coefficients) within max-abs 1e-5 x RMS of the fp32 oracle, over ragged token
-     counts, 2..20 sources, boundary and in-iteration reads, d in {768, 1024, 1536, 3072};
-  2. bf16: against the fp64 oracle on the same bf16-rounded inputs: max-abs error <= 1e-2 x max |ref| for outputs
-     and all gradients, and no worse than the reference read's own bf16 error (<= 2 err_ref + 2e-3);
+     h0 through base, the previous coefficients) within max-abs 1e-5 x RMS of the reference read evaluated exactly
+     (the fp64 oracle on the same fp32 inputs), and within 2e-5 x RMS of the fp32 oracle (two fp32 evaluations,
+     each with its own round-off), over ragged token counts, 2..20 sources, boundary and in-iteration reads,
+     d in {768, 1024, 1536, 3072};
+  2. bf16: against the reference read evaluated exactly (the fp64 oracle on the same bf16-rounded inputs): max-abs
+     error <= 1e-2 x max |ref| for what the kernels compute (out, tc, dq, dv, dcbar), and for everything no worse
+     than the reference read's own bf16 error (<= 2 err_ref + 2e-3) -- dproposal / dh0 come from the caller's
+     bf16 torch glue, the same ops as the reference's; against the bf16 reference read itself (whose gradients
+     round every per-source term to bf16): norm-relative <= 1e-2 for outputs and all gradients;
   3. zero query, cbar == prior: out == base and tc == c0 bitwise, fp32 and bf16.
 """
 import pytest
 import torch
 
-from gpu_helpers import DEV, err_max, err_rms, make
+from gpu_helpers import DEV, err_max, err_norm, err_rms, make
 from oracle.reference_read import OracleCell
 
 pytestmark = pytest.mark.gpu
@@ -72,8 +77,11 @@ def test_fp32_matches_reference_read(b, t, d, n, boundary):
     print(f"case fp32 b{b} t{t} d{d} n{n} boundary={boundary}", flush=True)
     hip = run_hip(d, n, args, boundary)
     ref = run_oracle(d, n, args, boundary)
-    e = compare(hip, ref, err_rms)
-    assert max(e.values()) <= 1e-5, e
+    ref64 = run_oracle(d, n, args, boundary, dtype=torch.float64)
+    e64 = compare(hip, ref64, err_rms)
+    e32 = compare(hip, ref, err_rms)
+    assert max(e64.values()) <= 1e-5, e64
+    assert max(e32.values()) <= 2e-5, e32
 
 
 @pytest.mark.parametrize("b,t,d", [(2, 256, 1024), (2, 128, 1536), (4, 128, 768)])
@@ -84,9 +92,11 @@ def test_bf16_against_fp64(b, t, d, n):
     hip = run_hip(d, n, args, boundary=True)
     ref_bf16 = run_oracle(d, n, args, boundary=True)
     ref64 = run_oracle(d, n, args, boundary=True, dtype=torch.float64)
+    eb = compare(hip, ref_bf16, err_norm)
     ef = compare(hip, ref64, err_max)
     er = compare(ref_bf16, ref64, err_max)
-    assert max(ef.values()) <= 1e-2, ef
+    assert max(eb.values()) <= 1e-2, eb
+    assert max(ef[k] for k in ("out", "tc", "dq", "dv", "dcoef")) <= 1e-2, ef
     assert all(ef[k] <= 2.0 * er[k] + 2e-3 for k in er), (ef, er)
 
 
