@@ -343,6 +343,154 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// write step on the matrix cores (bf16 updates): the scores are a (tokens x d) . (d x queries) product. Each fp32
+// query row is held as three bf16 parts q = hi + mid + lo (the split is exact to ~2^-24 relative); the update is
+// exactly bf16 after its rounding, so three bf16 MFMAs with fp32 accumulation give fp32-accurate scores.
+// A workgroup takes 32 tokens (two 16-row blocks); its 4 waves split d into 64-column chunks (lane quad g holds
+// 16 contiguous columns of its row, i.e. two 8-element k-groups, one per MFMA); the wave partials meet in LDS in a
+// fixed order. v_mfma_f32_16x16x32_bf16 operands: lane l holds row (l % 16) of A and column (l % 16) of B over the
+// k-group of its quad (l / 16); the result holds rows 4 (l / 16) + i, i < 4, of column l % 16.
+// ---------------------------------------------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int WM_TT = 32;   // tokens per workgroup
+constexpr int WM_KC = 64;   // columns per chunk
+constexpr int WM_NB = 4;    // up to 64 queries: four 16-query blocks
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
+
+__global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h, const bf16_t* __restrict__ x,
+                                                   bf16_t* __restrict__ v, float* __restrict__ r,
+                                                   const bf16_t* __restrict__ qb, int64_t qb_part_stride,
+                                                   float* __restrict__ dots, int64_t n_tok, int d, int nq,
+                                                   int64_t dots_jstride, float eps) {
+  __shared__ f32x4_t s_part[4][2][WM_NB][64];
+  __shared__ float s_ss[4][2][16];
+  const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * WM_TT;
+  const int nb = (nq + 15) >> 4;
+  f32x4_t acc[2][WM_NB];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int b = 0; b < WM_NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[2] = {0.f, 0.f};
+  int64_t roff[2];
+  bool tok_ok[2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    const int64_t tok = t0 + 16 * mb + row;
+    tok_ok[mb] = tok < n_tok;
+    roff[mb] = (tok_ok[mb] ? tok : n_tok - 1) * (int64_t)d;
+  }
+  // this lane's query row in each block, clamped (rows past nq are computed and never stored)
+  int qrow[WM_NB];
+#pragma unroll
+  for (int b = 0; b < WM_NB; ++b) qrow[b] = min(16 * b + row, nq > 0 ? nq - 1 : 0);
+  const int nchunks = (d + WM_KC - 1) / WM_KC;
+  for (int c = w; c < nchunks; c += 4) {
+    const int col = c * WM_KC + quad * 16;
+    bool col_ok[2];
+    int cc[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      col_ok[hf] = col + 8 * hf < d;
+      cc[hf] = col_ok[hf] ? col + 8 * hf : 0;
+    }
+    uint4 hr[2][2], xr[2][2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        hr[mb][hf] = *reinterpret_cast<const uint4*>(h + roff[mb] + cc[hf]);
+        xr[mb][hf] = *reinterpret_cast<const uint4*>(x + roff[mb] + cc[hf]);
+      }
+    uint4 va[2][2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        float hv[8], xv[8], vv[8];
+        IO<bf16_t>::unpack(IO<bf16_t>::Raw{hr[mb][hf]}, hv);
+        IO<bf16_t>::unpack(IO<bf16_t>::Raw{xr[mb][hf]}, xv);
+        const bool ok = tok_ok[mb] && col_ok[hf];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) vv[k] = ok ? hv[k] - xv[k] : 0.f;
+        uint4 u;
+        u.x = pack2(vv[0], vv[1]); u.y = pack2(vv[2], vv[3]); u.z = pack2(vv[4], vv[5]); u.w = pack2(vv[6], vv[7]);
+        va[mb][hf] = u;
+        float rv[8];
+        IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);   // the stored (rounded) update
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss[mb] += rv[k] * rv[k];
+        if (ok) *reinterpret_cast<uint4*>(v + roff[mb] + cc[hf]) = u;
+      }
+    for (int p = 0; p < 3; ++p) {
+      const bf16_t* qp = qb + p * qb_part_stride;
+#pragma unroll
+      for (int b = 0; b < WM_NB; ++b) {
+        if (b < nb) {
+          uint4 qv[2];
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            qv[hf] = *reinterpret_cast<const uint4*>(qp + (int64_t)qrow[b] * d + cc[hf]);
+            if (!col_ok[hf]) qv[hf] = make_uint4(0u, 0u, 0u, 0u);
+          }
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qv[hf]),
+                                                                   acc[mb][b], 0, 0, 0);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    ss[mb] += __shfl_xor(ss[mb], 16, 64);
+    ss[mb] += __shfl_xor(ss[mb], 32, 64);
+    if (quad == 0) s_ss[w][mb][row] = ss[mb];
+#pragma unroll
+    for (int b = 0; b < WM_NB; ++b)
+      if (b < nb) s_part[w][mb][b][l] = acc[mb][b];
+  }
+  __syncthreads();
+  if (tid < 32) {
+    const int mb = tid >> 4, rr = tid & 15;
+    const float tot = ((s_ss[0][mb][rr] + s_ss[1][mb][rr]) + s_ss[2][mb][rr]) + s_ss[3][mb][rr];
+    const int64_t tok = t0 + tid;
+    if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
+  }
+  for (int e = tid; e < 2 * nb * 64; e += WG) {
+    const int mb = e / (nb * 64), rem = e - mb * nb * 64, b = rem >> 6, ll = rem & 63;
+    const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
+    const int jj = 16 * b + (ll & 15);
+    if (jj >= nq) continue;
+    const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
+    float* dst = dots + (int64_t)jj * dots_jstride + tok;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (tok + i < n_tok) dst[i] = sum[i];
+  }
+}
+
+// the three bf16 parts of fp32 query rows: qb[p][j][k], p = 0 (hi), 1 (mid), 2 (lo); q = hi + mid + lo
+__global__ __launch_bounds__(WG) void k_split_queries(const float* __restrict__ q, bf16_t* __restrict__ qb, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x; i < n; i += (int64_t)gridDim.x * WG) {
+    const float a = q[i];
+    const __bf16 hi = (__bf16)a;
+    const float r1 = a - (float)hi;
+    const __bf16 mid = (__bf16)r1;
+    const __bf16 lo = (__bf16)(r1 - (float)mid);
+    qb[i] = __builtin_bit_cast(bf16_t, hi);
+    qb[n + i] = __builtin_bit_cast(bf16_t, mid);
+    qb[2 * n + i] = __builtin_bit_cast(bf16_t, lo);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // online scores: out[i][tok] = q . v_i[tok]  (the read without a stored score table)
 // ---------------------------------------------------------------------------------------------------------------
 template <typename T, int VPT, int C>
@@ -945,7 +1093,7 @@ template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 1; }
+int ldr_abi_version(void) { return 2; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -999,20 +1147,41 @@ int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64
   return launched();
 }
 
-int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, float* dots,
-                   int64_t n_tok, int64_t d, int64_t nq, int64_t dots_jstride, float eps, int dtype, void* stream) {
+int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, const void* qb,
+                   int64_t qb_part_stride, float* dots, int64_t n_tok, int64_t d, int64_t nq, int64_t dots_jstride,
+                   float eps, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (n_tok < 0 || !h || !x || !v_out || !r_out || nq < 0) return LDR_E_ARG;
   if (nq > LDR_MAX_QUERIES) return LDR_E_SHAPE;
-  if (nq > 0 && (!q || !dots || dots_jstride < n_tok)) return LDR_E_ARG;
-  if (!al16(h) || !al16(x) || !al16(v_out) || (nq > 0 && !al16(q))) return LDR_E_ALIGN;
+  if (nq > 0 && (!dots || dots_jstride < n_tok)) return LDR_E_ARG;
+  if (nq > 0 && dtype == LDR_BF16 && (!qb || qb_part_stride < nq * d)) return LDR_E_ARG;
+  if (nq > 0 && dtype == LDR_F32 && !q) return LDR_E_ARG;
+  if (!al16(h) || !al16(x) || !al16(v_out) || (nq > 0 && q && !al16(q)) ||
+      (nq > 0 && dtype == LDR_BF16 && (!al16(qb) || (qb_part_stride & 7))))
+    return LDR_E_ALIGN;
   if (d <= 0 || (d & 7) || d > LDR_MAX_WIDTH) return LDR_E_SHAPE;
   if (n_tok == 0) return LDR_OK;
-  const unsigned grid = (unsigned)cdiv(n_tok, WR_TT);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_write_dots<T>), dim3(grid), dim3(WG), 0, st, static_cast<const T*>(h),
-                                             static_cast<const T*>(x), static_cast<T*>(v_out), r_out, q, dots, n_tok,
-                                             (int)d, (int)nq, dots_jstride, eps))
+  if (dtype == LDR_BF16) {   // matrix-core scores
+    const unsigned grid = (unsigned)cdiv(n_tok, WM_TT);
+    hipLaunchKernelGGL(k_write_mfma, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(h),
+                       static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), r_out,
+                       static_cast<const bf16_t*>(qb), qb_part_stride, dots, n_tok, (int)d, (int)nq, dots_jstride, eps);
+  } else {
+    const unsigned grid = (unsigned)cdiv(n_tok, WR_TT);
+    hipLaunchKernelGGL((k_write_dots<float>), dim3(grid), dim3(WG), 0, st, static_cast<const float*>(h),
+                       static_cast<const float*>(x), static_cast<float*>(v_out), r_out, q, dots, n_tok, (int)d, (int)nq,
+                       dots_jstride, eps);
+  }
+  return launched();
+}
+
+int ldr_split_queries(const float* q, int64_t n, void* qb, void* stream) {
+  if (!q || !qb || n < 0) return LDR_E_ARG;
+  if (n == 0) return LDR_OK;
+  const unsigned grid = grid_of(cdiv(n, WG), 1024);
+  hipLaunchKernelGGL(k_split_queries, dim3(grid), dim3(WG), 0, static_cast<hipStream_t>(stream), q,
+                     static_cast<bf16_t*>(qb), n);
   return launched();
 }
 

@@ -319,7 +319,7 @@ class DattnStack:
     whose backward ran, its output gradient and query (`bwd`). The updates' gradients are assembled from those by the
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
     transposed operand for its tensor-core product; the HIP write reads Q directly)."""
-    __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "DOTS", "r_done", "WZ", "bwd",
+    __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
                  "assembled")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
@@ -340,7 +340,7 @@ class DattnStack:
         self.assembled = set()
         self.eps = float(eps)
         self.r_done = [False] * self.n_steps      # R[s] (and the scores of update s) written by the write of s
-        self.Q = self.QT = self.DOTS = None
+        self.Q = self.QT = self.QB = self.DOTS = None
         if query is not None:
             self.Q = query.detach().float().contiguous()
             nq = self.Q.shape[0]
@@ -348,6 +348,9 @@ class DattnStack:
                 raise RuntimeError(f"delta_attnres stacked read: query must be (<= {L.MAX_QUERIES}, {d}), "
                                    f"got {tuple(self.Q.shape)}")
             self.DOTS = torch.empty((max(1, nq), n_steps, b * t), dtype=torch.float32, device=device)
+            if dtype == torch.bfloat16 and nq > 0:   # the queries' bf16 parts: the write's matrix-core operand
+                self.QB = torch.empty((3, nq, d), dtype=torch.bfloat16, device=device)
+                _run("split_queries", _p(self.Q), self.Q.numel(), _p(self.QB), _stream(self.Q.device))
 
     def write(self, s: int, h: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
         """V[s] = h - x, returned as the update tensor (an alias of the stack's slice, with the autograd edge to
@@ -379,14 +382,16 @@ class _WriteDelta(torch.autograd.Function):
         if (h.is_cuda and h.is_contiguous() and x.is_contiguous() and h.dtype == V.dtype == x.dtype
                 and h.numel() == x.numel() == stack.n_tok * stack.d and h.shape[-1] == stack.d
                 and _aligned(h) and _aligned(x)):
-            nq, qptr, dptr, jstride = 0, None, None, stack.n_steps * stack.n_tok
+            nq, qptr, qbptr, qb_stride, dptr, jstride = 0, None, None, 0, None, stack.n_steps * stack.n_tok
             if stack.Q is not None:
                 j_lo = max(0, s - 1)                  # read s' >= s uses query s' - 1
                 nq = max(0, stack.Q.shape[0] - j_lo)
                 if nq > 0:
                     qptr, dptr = stack.Q[j_lo], stack.DOTS[j_lo, s]
-            _run("write_dots", _p(h), _p(x), _p(out), _p(stack.R[s]), _p(qptr), _p(dptr), stack.n_tok,
-                                        stack.d, nq, jstride, stack.eps, _dtype_code(V.dtype), _stream(V.device))
+                    if stack.QB is not None:
+                        qbptr, qb_stride = stack.QB[0, j_lo], stack.QB[0].numel()
+            _run("write_dots", _p(h), _p(x), _p(out), _p(stack.R[s]), _p(qptr), _p(qbptr), qb_stride, _p(dptr),
+                 stack.n_tok, stack.d, nq, jstride, stack.eps, _dtype_code(V.dtype), _stream(V.device))
             stack.r_done[s] = True
         else:
             torch.sub(h, x, out=out)

@@ -102,8 +102,8 @@ def test_eval_chains():
     hs, _ = hip_chain(cfg, "stack", grad=False)
     hw, _ = hip_chain(cfg, "scores", grad=False)
     hr, _ = ref_chain(cfg, None, grad=False)
-    assert torch.equal(hl, hs)
-    assert err_norm(hw, hr) <= 1e-2 and err_norm(hl, hr) <= 1e-2
+    for h in (hl, hs, hw):
+        assert err_norm(h, hr) <= 1e-2
 
 
 @pytest.mark.parametrize("mode", ["stack", "scores"])

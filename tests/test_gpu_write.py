@@ -1,0 +1,39 @@
+"""The stacked write (DattnStack.write, fused_dattn.py:679-695): V[s] = h - x rounded to the stack dtype (bitwise
+what torch's subtraction gives), R[s] the RMS scale of the rounded update, and the scores of the update against
+the queries of the reads still to come, DOTS[j, s, tok] = q_j . V[s, tok] for j >= s - 1 -- against an fp64 matmul
+of the rounded update (bf16: matrix cores from the queries' three bf16 parts; fp32: vector units). Ragged token
+counts and a width with a partial 64-column chunk included."""
+import pytest
+import torch
+
+from gpu_helpers import DEV, err_rms
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,d", [(37, 64), (100, 768), (257, 1096), (64, 2048)])
+@pytest.mark.parametrize("N", [2, 9, 33])
+def test_write_scores(dtype, T, d, N):
+    from loopback_amd import fused_dattn as FD
+    from oracle.reference_read import rstd_ref
+    gen = torch.Generator().manual_seed(T + d + N)
+    Q = (torch.randn(N - 1, d, generator=gen) * 0.3).to(DEV)
+    stack = FD.DattnStack(N, (1, T, d), dtype, DEV, query=Q, eps=1e-6)
+    hs = [torch.randn(1, T, d, generator=gen).to(dtype).to(DEV) for _ in range(N)]
+    xs = [torch.randn(1, T, d, generator=gen).to(dtype).to(DEV) for _ in range(N)]
+    with torch.no_grad():
+        for s in range(N):
+            v = stack.write(s, hs[s], xs[s])
+            assert torch.equal(v, hs[s] - xs[s]), s
+            assert stack.r_done[s]
+    torch.cuda.synchronize()
+    V = stack.V.double().cpu().reshape(N, T, d)
+    rr = rstd_ref(V, 1e-6).squeeze(-1)
+    assert err_rms(stack.R.reshape(N, T).cpu(), rr) <= 2e-6
+    ref = torch.einsum("jd,std->jst", Q.double().cpu(), V)           # [query, source, token]
+    got = stack.DOTS.cpu()
+    for s in range(N):
+        j_lo = max(0, s - 1)
+        if j_lo < N - 1:
+            assert err_rms(got[j_lo:, s], ref[j_lo:, s]) <= 1e-5, s

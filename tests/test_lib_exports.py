@@ -75,8 +75,13 @@ def test_argument_checks_before_launch(lib):
     too_many = lib.u64_array([4096] * 65)
     assert L.ldr_dots_online(too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, 1, null) == -1
     assert L.ldr_write_dots(ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096),
-                            ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 64, 65, 16, 1e-6,
-                            1, null) == -2
+                            ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096), 65 * 64,
+                            ctypes.c_void_p(4096), 16, 64, 65, 16, 1e-6, 1, null) == -2
+    # bf16 scores need the split query parts
+    assert L.ldr_write_dots(ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096),
+                            ctypes.c_void_p(4096), ctypes.c_void_p(4096), null, 0, ctypes.c_void_p(4096), 16, 64, 4,
+                            16, 1e-6, 1, null) == -1
+    assert L.ldr_split_queries(null, 8, ctypes.c_void_p(4096), null) == -1
     assert L.ldr_dv_assemble(too_many, too_many, too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), null,
                              ctypes.c_void_p(4096), 16, 64, 1, null) == -2
     # zero tokens: accepted, nothing launched
