@@ -37,7 +37,21 @@ def parse():
     ap.add_argument("--mode", default="scores", choices=["scores", "stack", "list"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the CPU baseline sample")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 1 GiB device to device once (torch copy kernel): the known-size reference that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     return ap.parse_args()
+
+
+def copy_calibration():
+    import torch
+    a = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    a.fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": a.numel() * 4, "copy_calibration_bytes_written": b.numel() * 4}))
 
 
 class KernelTimer:
@@ -126,6 +140,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(3)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     from loopback_amd import fused_dattn as FD
     from loopback_amd.chain import CONFIGS, make_inputs, run_chain
 
@@ -156,11 +173,15 @@ def main():
     mean_s = ksum[dom]["mean_us"] * 1e-6
     achieved = bytes_per_launch / mean_s / 1e9
     kernel_ms = sum(v["total_ms"] for v in ksum.values())
+    # HBM bytes per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of
+    # this configuration (profiles/traffic_chain_<config>.txt, copy-calibrated), when there is one for this mode
     traffic = None
-    tr_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"traffic_{dom}_{args.config}.json")
+    tr_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"traffic_chain_{args.config}.txt")
     if os.path.exists(tr_path):
         with open(tr_path) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            tr = json.load(f)
+        if tr.get("mode") == args.mode:
+            traffic = tr["hbm_bytes_per_launch"].get(dom)
 
     line = {
         "metric": "depth-read tokens/sec (fwd+bwd), d=2048, N=32 stack" if cfg.backward else

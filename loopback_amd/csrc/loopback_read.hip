@@ -29,13 +29,13 @@
 #define LDR_RF_MAX_VPT 2     // read forward: most 16-byte vectors per lane in a row
 #endif
 #ifndef LDR_AS_RB
-#define LDR_AS_RB 2          // update gradient: token rows per lane
+#define LDR_AS_RB 4          // update gradient: token rows per lane (each query load serves all of them)
 #endif
 #ifndef LDR_AS_JB
-#define LDR_AS_JB 4          // update gradient: reads whose rows are loaded together
+#define LDR_AS_JB 2          // update gradient: reads whose rows are loaded together
 #endif
 #ifndef LDR_AS_MAX_VPT
-#define LDR_AS_MAX_VPT 2
+#define LDR_AS_MAX_VPT 3
 #endif
 #ifndef LDR_B1_MAX_VPT
 #define LDR_B1_MAX_VPT 3     // backward pass 1 (holds g and two accumulators per element)
@@ -944,13 +944,15 @@ __global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, c
 // ---------------------------------------------------------------------------------------------------------------
 // stacked layout: the finished gradient of one update from every read that held it, plus its scale's term
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int AS_RB = LDR_AS_RB;   // token rows per lane, sharing each query load
+// token rows per lane, sharing each query load (fewer when the lane holds 3+ vectors of a row: registers)
+constexpr int as_rb(int vpt) { return vpt >= 3 ? 2 : LDR_AS_RB; }
 constexpr int AS_JB = LDR_AS_JB;   // reads per batch of loads
 
 template <typename T, int VPT>
 __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* __restrict__ vsrc,
                                                     const float* __restrict__ r, const float* __restrict__ gr,
                                                     T* __restrict__ dv, int64_t n_tok, int d, int tpr) {
+  constexpr int AS_RB = as_rb(VPT);
   const Rows R(d, tpr);
   const int64_t rows_per_tile = (int64_t)R.rpw * AS_RB;
   const int64_t tiles = (n_tok + rows_per_tile - 1) / rows_per_tile;
@@ -1301,10 +1303,10 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
     if (j < m && (!t.g[j] || !t.wz[j] || !t.q[j])) return LDR_E_ARG;
     if (j < m && (!al16(t.g[j]) || !al16(t.q[j]) || (reinterpret_cast<uintptr_t>(t.wz[j]) & 7u))) return LDR_E_ALIGN;
   }
-  int vpt, tpr, e = row_layout(d, &vpt, &tpr, LDR_AS_MAX_VPT, false, LDR_AS_VPT);
+  int vpt, tpr, e = row_layout(d, &vpt, &tpr, LDR_AS_MAX_VPT, false, LDR_AS_VPT, true);
   if (e) return e;
   if (n_tok == 0) return LDR_OK;
-  const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * AS_RB), 65535);
+  const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * as_rb(vpt)), 65535);
   hipStream_t st = static_cast<hipStream_t>(stream);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT>), dim3(grid), dim3(WG), 0, st,
                                                                   t, (int)m, static_cast<const T*>(v), r, gr,
