@@ -2,16 +2,17 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--mode scores] [--no-cpu-baseline]
 
-A step is one pass of the read path over one batch: the K x R chain of BASELINE.json's configuration (default
+A step is one pass of the read path over one batch: the K x R chain of the benchmark configuration (default
 config 4: d=2048, K=4, R=8 -> N=32 updates, 31 reads, T = 8 x 2048 tokens, bf16 updates, fp32 scores), forward and
 backward -- N writes (with the read-query scores), N-1 reads, their backwards, the updates' gradients -- with the
 synthetic blocks x -> x + D_s and the caller's torch glue included. Inputs are resident in HBM before timing.
 
-Prints ONE JSON line (rank 0): the metric of BASELINE.json (read tokens/s = T * steps / wall time), plus
+Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / wall time), plus
   roofline      the dominant kernel (most time per pass): its compulsory bytes per launch / its mean launch
                 duration, from HIP events on the launch stream during the last timed step, against 8 TB/s;
   chain         every library kernel of the pass: compulsory bytes / summed kernel time, and the reference
-                dataflow's formula bytes (SURVEY) over the same time and over the wall time;
+                dataflow's bytes (its backward read-modify-writes a gradient stack) over the same time and over
+                the wall time;
   cpu_baseline  the CPU oracle (the restated reference read, fp32/bf16 torch on the host cores) on a bounded sample
                 of the same chain (T reduced), fwd+bwd, tokens/s.
 """
@@ -134,7 +135,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the read shards by tokens "
-              "across GPUs as described in DESIGN.md, but no multi-GPU figure is produced", file=sys.stderr)
+              "across GPUs (only the query gradient is summed over them), but no multi-GPU figure is produced", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():

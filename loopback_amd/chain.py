@@ -8,7 +8,7 @@ h0 + sum_i c_i d_i exactly and the read is the only real computation. Per step s
 
 and the loss is sum(h.float() * G). The layer-loop shape follows modeling_looped_transformer.py:446-481.
 
-Configurations are BASELINE.json's (`CONFIGS`): tokens are b x t = 8 x 2048 unless stated; updates N(0,1), h0
+The benchmark configurations (`CONFIGS`): tokens are b x t = 8 x 2048 unless stated; updates N(0,1), h0
 N(0,1), queries N(0, 0.02^2), lambda = 1/4, eps = 1e-6, seeds 0 (h0), 1 (D), 2 (queries), 3 (G).
 """
 from __future__ import annotations

@@ -1,4 +1,4 @@
-"""BASELINE.json's configurations at their full size (T = 16384 tokens) on the GPU, checked through properties that
+"""The benchmark configurations at their full size (T = 16384 tokens) on the GPU, checked through properties that
 do not need the oracle to run at that size:
   * the read is per token, so the HIP chain over all tokens restricted to a token subset must equal the oracle chain
     (the restated reference read in bf16, on the same inputs) over that subset -- final state, dL/dh0 and every
