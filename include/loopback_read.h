@@ -82,28 +82,44 @@ int ldr_split_queries(const float* q, int64_t n, void* qb, void* stream);
 int ldr_dots_online(const uint64_t* src_v, int64_t n, const float* q, float* out, int64_t out_stride,
                     int64_t n_tok, int64_t d, int dtype, void* stream);
 
-/* The read step over n sources from their raw scores dots[i * dots_stride + tok] = q . v_i:
- *   l_i = dots_i * r_i * inv_sqrt_d + log(max(c0_i, 1e-8));  lse = logsumexp_i l_i;  lse0 = logsumexp_i lc_i
- *   tc_i = c0_i + M (exp(l_i - lse) - exp(lc_i - lse0)),  M = sum_i c0_i
- *   out = round(base + sum_i (tc_i - cbar_i) v_i)   (fp32 accumulation, one rounding)
- * and stores tc [n_tok, n], the logits lg [n_tok, n] and lse [n_tok] for the backward. c0 is a device array of n.
- * Replaces _dattn_fwd_dots_kernel (fused_dattn.py:588-625, launched at 748-751) and the weighted-sum half of
- * _dattn_fwd_stk_kernel / _dattn_fwd_kernel (410-456 / 55-108). */
-int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* dots, int64_t dots_stride,
-                 const void* base, const float* cbar, const float* c0, float inv_sqrt_d, void* out, float* tc,
-                 float* lg, float* lse, int64_t n_tok, int64_t d, int dtype, void* stream);
+/* The coefficient inputs of a read (ldr_read_fwd, ldr_read_bwd1) come as the read takes them -- cbar [n_tok, n]
+ * and c0 [n] with cbar_cols = c0_cols = n and lam = 1 -- or as the previous read left them, fused with the caller's
+ * bookkeeping (looped_transformer.py:383-391): coeffs [n_tok, n-1] and prior [n-1] with cbar_cols = c0_cols = n-1,
+ * the newest source's entries implied, cbar = lam * [coeffs, 1] and c0 = lam * [prior, 1] (lam = 1 - beta at an
+ * iteration end, 1 otherwise). */
 
-/* Backward pass 1 of a read (the only re-read of the sources), with g = dL/dout and gt = dL/dtc (NULL = zeros):
+/* The read step over n sources from their raw scores dots[i * dots_stride + tok] = q . v_i:
+ *   l_i = dots_i * r_i * inv_sqrt_d + log(max(c0_i, 1e-8));  p = softmax_i(l);  p0 = softmax_i(lc)
+ *   tc_i = c0_i + M (p_i - p0_i),  M = sum_i c0_i
+ *   out = round(base + sum_i (tc_i - cbar_i) v_i)   (fp32 accumulation, one rounding)
+ * (softmax as exp(l - max) / sum). With h0 != NULL (an iteration end, fused with looped_transformer.py:380-381) base
+ * is the proposal and the read first forms round(base + round(beta * round(h0 - base))), the caller's own rounding
+ * sequence. Stores tc [n_tok, n], the probabilities p [n_tok, n] for the backward, and c0 into next_prior [n] when
+ * not NULL (the caller's next prior). Replaces _dattn_fwd_dots_kernel (fused_dattn.py:588-625, launched at 748-751)
+ * and the weighted-sum half of _dattn_fwd_stk_kernel / _dattn_fwd_kernel (410-456 / 55-108). */
+int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* dots, int64_t dots_stride,
+                 const void* base, const void* h0, float beta, const float* cbar, int64_t cbar_cols, const float* c0,
+                 int64_t c0_cols, float lam, float inv_sqrt_d, void* out, float* tc, float* p, float* next_prior,
+                 int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* Backward pass 1 of a read (the only re-read of the sources), with g = dL/dout, gt = dL/dtc (NULL = zeros), and
+ * the forward's p and raw scores dots (as ldr_read_fwd took them):
  *   gd_i = g . v_i,  gp_i = M (gd_i + gt_i),  Sacc = sum_i p_i gp_i,  dz_i = p_i (gp_i - Sacc)
- *   dcbar[tok, i] = -gd_i;  dr_i[tok] (+)= dz_i (l_i - lc_i) / r_i   (added when dr_accum != 0)
+ *   dcbar[tok, i] = -lam gd_i for i < dcbar_cols (the gradient of cbar, or with dcbar_cols = n-1 that of the
+ *     previous coefficients through the caller's bookkeeping)
+ *   dr_i[tok] (+)= dz_i dots_i inv_sqrt_d   (= dz_i z_i / r_i; added when dr_accum != 0)
  *   wz[(i * wz_stride + tok) * 2 + {0,1}] = (tc_i - cbar_i, dz_i r_i inv_sqrt_d)   (the pass-2 scalars)
  *   dq_part[p, :] = per-workgroup partial of sum_tok sum_i dz_i r_i v_i inv_sqrt_d  (ldr_read_bwd1_parts rows)
+ *   with g_prop / g_h0 (both or neither): the iteration-end blend's gradients g_h0 = round(beta g),
+ *     g_prop = round(g - g_h0), rounded as autograd rounds them
  * Replaces _dattn_bwd1_stk_kernel (fused_dattn.py:459-493, launched at 777-779) and pass 1 of _dattn_bwd_kernel
  * (111-151); dr is also the dR update of _dattn_bwd2_stk_kernel (532-535). */
 int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const void* g, const float* gt,
-                  const float* lg, const float* lse, const float* tc, const float* cbar, const float* c0,
-                  float inv_sqrt_d, float* dcbar, const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride,
-                  float* dq_part, int64_t n_tok, int64_t d, int dtype, void* stream);
+                  const float* p, const float* dots, int64_t dots_stride, const float* tc, const float* cbar,
+                  int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, float* dcbar,
+                  int64_t dcbar_cols, const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride,
+                  float* dq_part, void* g_prop, void* g_h0, float beta, int64_t n_tok, int64_t d, int dtype,
+                  void* stream);
 
 /* out[c] = sum_p part[p * d + c] in a fixed order (deterministic).
  * Replaces the torch dq_part.sum(0) (fused_dattn.py:317, 785). */
@@ -118,11 +134,13 @@ int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, 
 /* The stacked layout's gradient of update i, formed once after every read of it has run its backward:
  *   dv[tok,:] = round( sum_e ( w_e[tok] g_e[tok,:] + dzr_e[tok] q_e[:] ) + gr[tok] (-r[tok]^3) / d * v[tok,:] )
  * over the m reads e that hold update i: g_e that read's output gradient, (w_e, dzr_e) its wz pair for source i
- * (float2 per token), q_e its query (fp32, d). One fp32 sum, one rounding.
+ * (float2 per token), q_e its query (fp32, d). One fp32 sum, one rounding; gr may be NULL (no scale gradient).
+ * dv_neg (may be NULL) receives -dv, the write's gradient to x (fused_dattn.py:694-695).
  * Replaces the dV read-modify-write of _dattn_bwd2_stk_kernel (fused_dattn.py:496-536, launched at 781-784) and
  * _rstd_bwd_acc_kernel (539-552, launched at 717-719). */
 int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                    const float* r, const float* gr, void* dv, int64_t n_tok, int64_t d, int dtype, void* stream);
+                    const float* r, const float* gr, void* dv, void* dv_neg, int64_t n_tok, int64_t d, int dtype,
+                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -5,7 +5,9 @@ port's copy is looped_transformer.py:334-424) and its mode switches (`_fused_dat
 stack creation, modeling_looped_transformer.py:437-444):
   * LOOP_DATTN_STACK=1 (default): the updates live in a DattnStack and the stacked kernels read it;
     LOOP_DATTN_DOTS=1 (default): the stack also stores each update's scores at its write;
-  * LOOP_DATTN_STACK=0: the list layout (FusedDattnRead), one tensor per update.
+  * LOOP_DATTN_STACK=0: the list layout (FusedDattnRead), one tensor per update;
+  * LOOP_DATTN_FUSE_GLUE=1 (default, this build's own switch): in the stacked layout the glue below runs inside the
+    read's kernels (FusedCombineStk); 0 keeps it as torch ops.
 The glue around the kernels -- the iteration-end blend base = proposal + beta (h0 - proposal), the coefficient
 bookkeeping (cat, lambda scaling) -- is the reference's, op for op. Unlike the reference, the cell has no PyTorch
 read of its own: an unsupported layout raises instead of falling back (that read lives in oracle/ as the checker).
@@ -18,6 +20,12 @@ import torch
 import torch.nn as nn
 
 from . import fused_dattn as FD
+
+
+def fuse_glue() -> bool:
+    """LOOP_DATTN_FUSE_GLUE=0 keeps the caller's glue (blend, coefficient bookkeeping) as torch ops around the
+    stacked read, as the reference cell has it; the default runs it inside the read's kernels."""
+    return os.environ.get("LOOP_DATTN_FUSE_GLUE", "1") == "1"
 
 
 def stack_mode() -> str:
@@ -71,6 +79,13 @@ class LoopDeltaAttnRes(nn.Module):
             raise ValueError(f"delta_attnres step {step} received {len(deltas)} deltas, expected {step + 1}")
 
         at_boundary = block_idx == self.num_blocks - 1
+        if stack is not None and step >= 1 and fuse_glue():
+            # the stacked read with the glue below inside its kernels (same results; no glue kernels)
+            if keys is not None and len(keys) < len(deltas):
+                keys.append(stack.rstd(step, deltas[-1], self.eps))
+            R_list = keys if keys is not None else [FD._alias(stack.R, i) for i in range(len(deltas))]
+            return FD.FusedCombineStk.apply(stack, step, self.query[step - 1], proposal, h0 if at_boundary else None,
+                                            coeffs, prior_coeffs, self.beta, at_boundary, *deltas, *R_list)
         base = proposal + self.beta * (h0 - proposal) if at_boundary else proposal
 
         b, t, _ = proposal.shape

@@ -40,6 +40,9 @@
 #ifndef LDR_B1_MAX_VPT
 #define LDR_B1_MAX_VPT 3     // backward pass 1 (holds g and two accumulators per element)
 #endif
+#ifndef LDR_B1_C
+#define LDR_B1_C 0           // backward pass 1: sources per chunk (0 = by vectors per lane)
+#endif
 #ifndef LDR_B1_WAVE_ROWS
 #define LDR_B1_WAVE_ROWS 0   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
@@ -110,6 +113,13 @@ template <> struct IO<bf16_t> {
     u.x = pack2(o[0], o[1]); u.y = pack2(o[2], o[3]); u.z = pack2(o[4], o[5]); u.w = pack2(o[6], o[7]);
     *reinterpret_cast<uint4*>(p) = u;
   }
+  // stores -o (rounded): the sign bits of the rounded values flipped, exact
+  static __device__ __forceinline__ void store_neg(bf16_t* p, const float (&o)[8]) {
+    uint4 u;
+    u.x = pack2(o[0], o[1]) ^ 0x80008000u; u.y = pack2(o[2], o[3]) ^ 0x80008000u;
+    u.z = pack2(o[4], o[5]) ^ 0x80008000u; u.w = pack2(o[6], o[7]) ^ 0x80008000u;
+    *reinterpret_cast<uint4*>(p) = u;
+  }
   static __device__ __forceinline__ float round(float x) { return (float)(__bf16)x; }
 };
 
@@ -127,6 +137,15 @@ template <> struct IO<float> {
   static __device__ __forceinline__ void store(float* p, const float (&o)[8]) {
     reinterpret_cast<float4*>(p)[0] = make_float4(o[0], o[1], o[2], o[3]);
     reinterpret_cast<float4*>(p)[1] = make_float4(o[4], o[5], o[6], o[7]);
+  }
+  static __device__ __forceinline__ void store_neg(float* p, const float (&o)[8]) {
+    uint4 a, b;
+    a.x = __float_as_uint(o[0]) ^ 0x80000000u; a.y = __float_as_uint(o[1]) ^ 0x80000000u;
+    a.z = __float_as_uint(o[2]) ^ 0x80000000u; a.w = __float_as_uint(o[3]) ^ 0x80000000u;
+    b.x = __float_as_uint(o[4]) ^ 0x80000000u; b.y = __float_as_uint(o[5]) ^ 0x80000000u;
+    b.z = __float_as_uint(o[6]) ^ 0x80000000u; b.w = __float_as_uint(o[7]) ^ 0x80000000u;
+    reinterpret_cast<uint4*>(p)[0] = a;
+    reinterpret_cast<uint4*>(p)[1] = b;
   }
   static __device__ __forceinline__ float round(float x) { return x; }
 };
@@ -179,29 +198,53 @@ __device__ __forceinline__ void row_sum(float (&x)[NV], int tpr, float* red) {
 // logsumexp of a token's n logits held by `lpt` aligned lanes (up to 8 each; unused slots are -inf): every lane
 // returns the same value. One code path for the scored and the prior-only logits, so equal inputs give bitwise
 // equal results (the zero-query identity tc == c0, out == base).
-__device__ __forceinline__ float lse_lanes(const float (&l)[8], int lpt) {
+// softmax over a token's logits spread over lpt lanes (8 each, -inf past n), in place: p = exp(l - max) / sum.
+// The division form (not exp(l - logsumexp)) keeps p within a few ulp, as torch's softmax computes it.
+__device__ __forceinline__ void softmax_lanes(float (&l)[8], int lpt) {
   float mx = l[0];
 #pragma unroll
   for (int m = 1; m < 8; ++m) mx = fmaxf(mx, l[m]);
   for (int off = lpt >> 1; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   float s = 0.f;
 #pragma unroll
-  for (int m = 0; m < 8; ++m) s += (l[m] == -INFINITY) ? 0.f : expf(l[m] - mx);
+  for (int m = 0; m < 8; ++m) {
+    l[m] = (l[m] == -INFINITY) ? 0.f : expf(l[m] - mx);
+    s += l[m];
+  }
   for (int off = lpt >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-  return mx + logf(s);
+#pragma unroll
+  for (int m = 0; m < 8; ++m) l[m] = l[m] / s;
 }
 
-// per-read constants from the prior c0 (n floats on the device): c0, lc = log(max(c0, 1e-8)), M = sum c0
-__device__ __forceinline__ void load_prior(const float* __restrict__ c0, int n, float* s_c0, float* s_lc, float* s_M) {
+// The coefficient inputs of a read. Either as the read takes them (cbar [tok][n], c0 [n], lam = 1), or -- fused
+// with the caller's bookkeeping -- as the previous read left them: coeffs [tok][n-1] and prior [n-1], the newest
+// source's entries implied, cbar = lam * [coeffs, 1] and c0 = lam * [prior, 1] (lam = 1 - beta at an iteration end,
+// else 1). x * 1.0f == x, so the plain form is exact.
+struct Coef {
+  const float* cbar;
+  int cbar_cols;   // n, or n - 1 (the newest column implied)
+  const float* c0;
+  int c0_cols;     // n, or n - 1
+  float lam;
+};
+
+__device__ __forceinline__ float coef_cbar(const Coef& c, int64_t tok, int i) {
+#pragma clang fp contract(off)   // the product is rounded on its own, as the caller's scaling is (never fused into a use)
+  return i < c.cbar_cols ? c.lam * c.cbar[tok * c.cbar_cols + i] : c.lam;
+}
+
+// per-read constants from the prior: c0, lc = log(max(c0, 1e-8)), M = sum c0 (in source order)
+__device__ __forceinline__ void load_prior(const Coef& c, int n, float* s_c0, float* s_lc, float* s_M) {
   const int t = (int)threadIdx.x;
   if (t < n) {
-    const float c = c0[t];
-    s_c0[t] = c;
-    s_lc[t] = logf(fmaxf(c, 1e-8f));
+    const float v = t < c.c0_cols ? c.lam * c.c0[t] : c.lam;
+    s_c0[t] = v;
+    s_lc[t] = logf(fmaxf(v, 1e-8f));
   }
+  __syncthreads();
   if (t == 0) {
     float m = 0.f;
-    for (int i = 0; i < n; ++i) m += c0[i];
+    for (int i = 0; i < n; ++i) m += s_c0[i];
     *s_M = m;
   }
   __syncthreads();
@@ -556,19 +599,21 @@ __global__ __launch_bounds__(WG) void k_dots(SrcTab src, int n, const float* __r
 // ---------------------------------------------------------------------------------------------------------------
 // read forward: softmax weights from the raw scores, then out = base + sum_i w_i v_i in one pass over the sources
 // ---------------------------------------------------------------------------------------------------------------
-template <typename T, int VPT>
+template <typename T, int VPT, bool BLEND>
 __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float* __restrict__ dots, int64_t dots_stride,
-                                                 const T* __restrict__ base, const float* __restrict__ cbar,
-                                                 const float* __restrict__ c0, float inv, T* __restrict__ out,
-                                                 float* __restrict__ tc, float* __restrict__ lg,
-                                                 float* __restrict__ lse_out, int64_t n_tok, int d, int tpr, int tt) {
+                                                 const T* __restrict__ base, const T* __restrict__ h0, float beta,
+                                                 Coef cf, float inv, T* __restrict__ out, float* __restrict__ tc,
+                                                 float* __restrict__ prob, float* __restrict__ next_prior,
+                                                 int64_t n_tok, int d, int tpr,
+                                                 int tt) {
   __shared__ float s_l[MAXS * (TT_MAX + 1)];   // logits [i][t]
   __shared__ float s_w[TT_MAX * SP];           // cbar, then the weights [t][i]
   __shared__ float s_c0[MAXS], s_lc[MAXS], s_M;
   const Rows R(d, tpr);
   const int tid = (int)threadIdx.x;
-  load_prior(c0, n, s_c0, s_lc, &s_M);
+  load_prior(cf, n, s_c0, s_lc, &s_M);
   const float M = s_M;
+  if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
   const int lpt = WG / tt;   // lanes per token in the softmax
   const int64_t tiles = (n_tok + tt - 1) / tt;
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
@@ -583,35 +628,33 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
     for (int idx = tid; idx < n * tt; idx += WG) {   // token-major: coalesced over [tok][i]
       const int t = idx / n, i = idx - t * n;
       const int64_t tok = t0 + t;
-      s_w[t * SP + i] = tok < n_tok ? cbar[tok * n + i] : 0.f;
+      s_w[t * SP + i] = tok < n_tok ? coef_cbar(cf, tok, i) : 0.f;
     }
     __syncthreads();
     {
       const int t = tid / lpt, j = tid - t * lpt;
       const int64_t tok = t0 + t;
-      float ls[8], l0[8];
+      float ps[8], p0[8];
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int i = j + m * lpt;
-        ls[m] = (i < n) ? s_l[i * (TT_MAX + 1) + t] : -INFINITY;
-        l0[m] = (i < n) ? s_lc[i] : -INFINITY;
+        ps[m] = (i < n) ? s_l[i * (TT_MAX + 1) + t] : -INFINITY;
+        p0[m] = (i < n) ? s_lc[i] : -INFINITY;
       }
-      const float lse = lse_lanes(ls, lpt);
-      const float lse0 = lse_lanes(l0, lpt);
+      softmax_lanes(ps, lpt);
+      softmax_lanes(p0, lpt);
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int i = j + m * lpt;
         if (i < n) {
-          const float p = expf(ls[m] - lse), p0 = expf(l0[m] - lse0);
-          const float tcv = s_c0[i] + M * (p - p0);
+          const float tcv = s_c0[i] + M * (ps[m] - p0[m]);
           s_w[t * SP + i] = tcv - s_w[t * SP + i];
           if (tok < n_tok) {
             tc[tok * n + i] = tcv;
-            lg[tok * n + i] = ls[m];
+            prob[tok * n + i] = ps[m];
           }
         }
       }
-      if (j == 0 && tok < n_tok) lse_out[tok] = lse;
     }
     __syncthreads();
     for (int rr = R.rs; rr < tt; rr += R.rpw) {
@@ -622,6 +665,17 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
       float acc[VPT][8];
 #pragma unroll
       for (int v = 0; v < VPT; ++v) IO<T>::load(base + roff + R.off(v), acc[v]);
+      if (BLEND) {   // iteration end: base = proposal + beta (h0 - proposal), each step rounded as the caller's ops
+#pragma clang fp contract(off)   // three separately rounded operations, as torch runs them (no fused multiply-add)
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          float hv[8];
+          IO<T>::load(h0 + roff + R.off(v), hv);
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            acc[v][k] = IO<T>::round(acc[v][k] + IO<T>::round(beta * IO<T>::round(hv[k] - acc[v][k])));
+        }
+      }
       int i = 0;
       constexpr int U = LDR_RF_UNROLL;
       for (; i + U <= n; i += U) {
@@ -687,13 +741,14 @@ constexpr int B1_MAX_VPT = LDR_B1_MAX_VPT;
 
 template <typename T, int VPT, int C>
 __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restrict__ g, const float* __restrict__ gt,
-                                             const float* __restrict__ lg, const float* __restrict__ lse,
-                                             const float* __restrict__ tcp, const float* __restrict__ cbar,
-                                             const float* __restrict__ c0, float inv, float* __restrict__ dcbar,
-                                             PtrTab dr, int dr_accum, float* __restrict__ wz, int64_t wz_stride,
-                                             float* __restrict__ dq_part, int64_t n_tok, int d, int tpr, int tt) {
-  // LDS: six [TT_MAX][SP] scalar planes (probability, scale, upstream tc gradient, g.v, dz, raw logit) during
-  // the tiles; the first d floats are reused for the workgroup's dq sum at the end.
+                                             const float* __restrict__ prob, const float* __restrict__ dots,
+                                             int64_t dots_stride, const float* __restrict__ tcp, Coef cf, float inv,
+                                             float* __restrict__ dcbar, int dcbar_cols, PtrTab dr, int dr_accum,
+                                             float* __restrict__ wz, int64_t wz_stride, float* __restrict__ dq_part,
+                                             T* __restrict__ g_prop, T* __restrict__ g_h0, float beta, int64_t n_tok,
+                                             int d, int tpr, int tt) {
+  // LDS: six [TT_MAX][SP] scalar planes (probability, scale, upstream tc gradient, g.v, raw score then dr, and
+  // tc - cbar) during the tiles; the first d floats are reused for the workgroup's dq sum at the end.
   __shared__ float lds[6 * TT_MAX * SP];
   __shared__ float s_sacc[TT_MAX], s_c0[MAXS], s_lc[MAXS], s_M, red[4 * C];
   float* s_p = lds;
@@ -704,7 +759,7 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
   float* s_w = lds + 5 * TT_MAX * SP;
   const Rows R(d, tpr);
   const int tid = (int)threadIdx.x;
-  load_prior(c0, n, s_c0, s_lc, &s_M);
+  load_prior(cf, n, s_c0, s_lc, &s_M);
   const float M = s_M;
   float dqa[VPT][8];
 #pragma unroll
@@ -717,22 +772,21 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
     for (int idx = tid; idx < n * tt; idx += WG) {   // token-major scalars
       const int t = idx / n, i = idx - t * n;
       const int64_t tok = t0 + t;
-      float p = 0.f, gtv = 0.f, w = 0.f, l = 0.f;
+      float p = 0.f, gtv = 0.f, w = 0.f;
       if (tok < n_tok) {
-        l = lg[tok * n + i];
-        p = expf(l - lse[tok]);
+        p = prob[tok * n + i];
         if (gt) gtv = gt[tok * n + i];
-        w = tcp[tok * n + i] - cbar[tok * n + i];
+        w = tcp[tok * n + i] - coef_cbar(cf, tok, i);
       }
       s_p[t * SP + i] = p;
       s_gt[t * SP + i] = gtv;
       s_w[t * SP + i] = w;
-      s_dz[t * SP + i] = l;   // the raw logit until the epilogue replaces it by dz
     }
-    for (int idx = tid; idx < n * tt; idx += WG) {   // source-major scales
+    for (int idx = tid; idx < n * tt; idx += WG) {   // source-major: scales and raw scores
       const int i = idx / tt, t = idx - i * tt;
       const int64_t tok = t0 + t;
       s_r[t * SP + i] = tok < n_tok ? src.r[i][tok] : 1.f;
+      s_dz[t * SP + i] = tok < n_tok ? dots[i * dots_stride + tok] : 0.f;   // q . v_i until the epilogue
     }
     __syncthreads();
     const int rows_per_slot = (tt + R.rpw - 1) / R.rpw;
@@ -748,6 +802,21 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
         if (!R.act(v)) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) gv[v][k] = 0.f;
+        }
+      }
+      if (g_prop && valid) {   // the blend's gradients: beta g to h0, g - beta g to the proposal (rounded as autograd)
+#pragma clang fp contract(off)   // a product and a difference, each rounded (no fused multiply-add)
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          if (!R.act(v)) continue;
+          float gb[8], gpv[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            gb[k] = IO<T>::round(beta * gv[v][k]);
+            gpv[k] = gv[v][k] - gb[k];
+          }
+          IO<T>::store(g_h0 + roff + R.c8(v) * 8, gb);
+          IO<T>::store(g_prop + roff + R.c8(v) * 8, gpv);
         }
       }
       float a[VPT][8], b[VPT][8];
@@ -831,8 +900,8 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
         const float gd = s_gd[t * SP + i];
         const float gp = M * (gd + s_gt[t * SP + i]);
         const float dz = s_p[t * SP + i] * (gp - s_sacc[t]);
-        dcbar[tok * n + i] = -gd;
-        s_dz[t * SP + i] = dz * (s_dz[t * SP + i] - s_lc[i]) / s_r[t * SP + i];   // drstd, logit -> dz z / r
+        if (i < dcbar_cols) dcbar[tok * dcbar_cols + i] = -(cf.lam * gd);
+        s_dz[t * SP + i] = dz * s_dz[t * SP + i] * inv;   // dr = dz z / r = dz (q . v) / sqrt(d)
         s_gd[t * SP + i] = dz;
       }
     }
@@ -951,7 +1020,8 @@ constexpr int AS_JB = LDR_AS_JB;   // reads per batch of loads
 template <typename T, int VPT>
 __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* __restrict__ vsrc,
                                                     const float* __restrict__ r, const float* __restrict__ gr,
-                                                    T* __restrict__ dv, int64_t n_tok, int d, int tpr) {
+                                                    T* __restrict__ dv, T* __restrict__ dv_neg, int64_t n_tok, int d,
+                                                    int tpr) {
   constexpr int AS_RB = as_rb(VPT);
   const Rows R(d, tpr);
   const int64_t rows_per_tile = (int64_t)R.rpw * AS_RB;
@@ -1015,7 +1085,10 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
       for (int v = 0; v < VPT; ++v) {
 #pragma unroll
         for (int x = 0; x < 8; ++x) acc[k][v][x] += c * e[v][x];
-        if (tok[k] < n_tok && R.act(v)) IO<T>::store(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
+        if (tok[k] < n_tok && R.act(v)) {
+          IO<T>::store(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
+          if (dv_neg) IO<T>::store_neg(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
+        }
       }
     }
   }
@@ -1087,6 +1160,8 @@ int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n) {
   else { typedef float T; __VA_ARGS__; }
 
 template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
+// backward pass 1: sources per row reduction (one LDS exchange per chunk when a row spans two waves)
+template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_B1_C : (VPT == 1 ? 8 : VPT == 2 ? 4 : 2); };
 
 }  // namespace
 
@@ -1095,7 +1170,7 @@ template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 2; }
+int ldr_abi_version(void) { return 4; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -1207,37 +1282,56 @@ int ldr_dots_online(const uint64_t* src_v, int64_t n, const float* q, float* out
 }
 
 int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* dots, int64_t dots_stride,
-                 const void* base, const float* cbar, const float* c0, float inv_sqrt_d, void* out, float* tc,
-                 float* lg, float* lse, int64_t n_tok, int64_t d, int dtype, void* stream) {
+                 const void* base, const void* h0, float beta, const float* cbar, int64_t cbar_cols, const float* c0,
+                 int64_t c0_cols, float lam, float inv_sqrt_d, void* out, float* tc, float* p, float* next_prior,
+                 int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (!src_r || n_tok < 0 || !dots || dots_stride < n_tok || !base || !cbar || !c0 || !out || !tc || !lg || !lse)
+  if (!src_r || n_tok < 0 || !dots || dots_stride < n_tok || !base || !cbar || !c0 || !out || !tc || !p)
     return LDR_E_ARG;
-  if (!al16(base) || !al16(out)) return LDR_E_ALIGN;
+  if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1)) return LDR_E_ARG;
+  if (!al16(base) || !al16(out) || (h0 && !al16(h0))) return LDR_E_ALIGN;
   SrcTab s;
   int e = fill_src(s, src_v, src_r, n);
   if (e) return e;
   int vpt, tpr;
   if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, false, LDR_RF_VPT))) return e;
   if (n_tok == 0) return LDR_OK;
+  const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
   const int tt = tile_tokens(tpr);
   const unsigned grid = grid_of(cdiv(n_tok, tt), 65535);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_fwd<T, VPT>), dim3(grid), dim3(WG), 0, st, s,
-                                                                  (int)n, dots, dots_stride, static_cast<const T*>(base),
-                                                                  cbar, c0, inv_sqrt_d, static_cast<T*>(out), tc, lg,
-                                                                  lse, n_tok, (int)d, tpr, tt)))
+  if (h0) {
+    LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_fwd<T, VPT, true>), dim3(grid), dim3(WG), 0,
+                                                                    st, s, (int)n, dots, dots_stride,
+                                                                    static_cast<const T*>(base),
+                                                                    static_cast<const T*>(h0), beta, cf, inv_sqrt_d,
+                                                                    static_cast<T*>(out), tc, p, next_prior, n_tok,
+                                                                    (int)d, tpr, tt)))
+  } else {
+    LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_fwd<T, VPT, false>), dim3(grid), dim3(WG),
+                                                                    0, st, s, (int)n, dots, dots_stride,
+                                                                    static_cast<const T*>(base), nullptr, beta, cf,
+                                                                    inv_sqrt_d, static_cast<T*>(out), tc, p,
+                                                                    next_prior, n_tok, (int)d, tpr, tt)))
+  }
   return launched();
 }
 
 int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const void* g, const float* gt,
-                  const float* lg, const float* lse, const float* tc, const float* cbar, const float* c0,
-                  float inv_sqrt_d, float* dcbar, const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride,
-                  float* dq_part, int64_t n_tok, int64_t d, int dtype, void* stream) {
+                  const float* p, const float* dots, int64_t dots_stride, const float* tc, const float* cbar,
+                  int64_t cbar_cols,
+                  const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, float* dcbar, int64_t dcbar_cols,
+                  const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride, float* dq_part, void* g_prop,
+                  void* g_h0, float beta, int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (!src_r || n_tok < 0 || !g || !lg || !lse || !tc || !cbar || !c0 || !dcbar || !dr || !wz || !dq_part ||
-      wz_stride < n_tok || (dr_accum != 0 && dr_accum != 1))
+  if (!src_r || n_tok < 0 || !g || !p || !dots || dots_stride < n_tok || !tc || !cbar || !c0 || !dcbar || !dr ||
+      !wz || !dq_part ||
+      wz_stride < n_tok || (dr_accum != 0 && dr_accum != 1) || (!g_prop) != (!g_h0))
     return LDR_E_ARG;
-  if (!al16(g)) return LDR_E_ALIGN;
+  if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1) || dcbar_cols < 0 ||
+      dcbar_cols > n)
+    return LDR_E_ARG;
+  if (!al16(g) || (g_prop && (!al16(g_prop) || !al16(g_h0)))) return LDR_E_ALIGN;
   SrcTab s;
   int e = fill_src(s, src_v, src_r, n);
   if (e) return e;
@@ -1249,13 +1343,17 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
   int vpt, tpr;
   if ((e = row_layout(d, &vpt, &tpr, B1_MAX_VPT, LDR_B1_WAVE_ROWS, LDR_B1_VPT, true))) return e;
   if (n_tok == 0) return LDR_OK;
+  const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
   const int tt = tile_tokens(tpr);
   const unsigned grid = grid_of(cdiv(n_tok, tt), B1_GRID);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_bwd1<T, VPT, Chunk<VPT>::C>), dim3(grid), dim3(WG),
-                                                                  0, st, s, (int)n, static_cast<const T*>(g), gt, lg,
-                                                                  lse, tc, cbar, c0, inv_sqrt_d, dcbar, drt, dr_accum,
-                                                                  wz, wz_stride, dq_part, n_tok, (int)d, tpr, tt)))
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_bwd1<T, VPT, B1Chunk<VPT>::C>), dim3(grid),
+                                                                  dim3(WG), 0, st, s, (int)n, static_cast<const T*>(g),
+                                                                  gt, p, dots, dots_stride, tc, cf, inv_sqrt_d, dcbar,
+                                                                  (int)dcbar_cols, drt, dr_accum, wz, wz_stride,
+                                                                  dq_part, static_cast<T*>(g_prop),
+                                                                  static_cast<T*>(g_h0), beta, n_tok, (int)d, tpr,
+                                                                  tt)))
   return launched();
 }
 
@@ -1290,11 +1388,12 @@ int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, 
 }
 
 int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                    const float* r, const float* gr, void* dv, int64_t n_tok, int64_t d, int dtype, void* stream) {
+                    const float* r, const float* gr, void* dv, void* dv_neg, int64_t n_tok, int64_t d, int dtype,
+                    void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (m < 0 || m > MAXS) return LDR_E_SHAPE;
   if ((m > 0 && (!g || !wz || !q)) || !v || !r || !dv || n_tok < 0) return LDR_E_ARG;
-  if (!al16(v) || !al16(dv)) return LDR_E_ALIGN;
+  if (!al16(v) || !al16(dv) || (dv_neg && !al16(dv_neg))) return LDR_E_ALIGN;
   AsmTab t;
   for (int64_t j = 0; j < MAXS; ++j) {
     t.g[j] = j < m ? reinterpret_cast<const void*>(g[j]) : nullptr;
@@ -1310,7 +1409,8 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT>), dim3(grid), dim3(WG), 0, st,
                                                                   t, (int)m, static_cast<const T*>(v), r, gr,
-                                                                  static_cast<T*>(dv), n_tok, (int)d, tpr)))
+                                                                  static_cast<T*>(dv), static_cast<T*>(dv_neg), n_tok,
+                                                                  (int)d, tpr)))
   return launched();
 }
 

@@ -178,30 +178,35 @@ def _forward_impl(ctx, q, base, cbar, c0, srcs):
     base_c = base.detach().contiguous()
     out = torch.empty_like(base_c)
     tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
-    lg = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
-    lse = torch.empty(n_tok, device=dev, dtype=torch.float32)
+    prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
     dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
     vp = L.u64_array(v.data_ptr() for v in values)
     rp = L.u64_array(r.data_ptr() for r in rstds)
     _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
-    _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base_c), _p(cbar_c), _p(c0c), _inv_sqrt(d), _p(out),
-                              _p(tc), _p(lg), _p(lse), n_tok, d, dt, st)
-    ctx.save_for_backward(qc, cbar_c, c0c, lg, lse, tc, *values, *rstds)
+    _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base_c), _p(None), 0.0, _p(cbar_c), n, _p(c0c), n, 1.0,
+         _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
+    ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc, *values, *rstds)
     ctx.n, ctx.q_dtype, ctx.base_shape = n, q.dtype, base.shape
     return out, tc.view(*base.shape[:-1], n)
 
 
-def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, lg, lse, tc, cbar_c, c0c, dr_ptrs, dr_accum, wz, wz_stride, n_tok, d,
-          dtype, dev):
-    """Pass 1 of the backward plus the dq reduction; returns (dq fp32, dcbar [n_tok, n])."""
+def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_ptrs, dr_accum, wz, wz_stride, n_tok, d,
+          dtype, dev, cols=None, lam=1.0, g_prop=None, g_h0=None, beta=0.0):
+    """Pass 1 of the backward plus the dq reduction; returns (dq fp32, dcbar [n_tok, cols]). prob and dots are the
+    forward's probabilities [n_tok, n] and raw scores [n, >= n_tok] (row stride dots.stride(0)). cols = n: cbar_c and c0c
+    are the read's own; cols = n - 1: they are the previous read's coefficients and prior (scaled by lam, the newest
+    entry implied) and dcbar is the gradient of those coefficients. g_prop / g_h0 receive the iteration-end blend's
+    gradients when given."""
     st = _stream(dev)
+    cols = n if cols is None else cols
     gt_c = None if gt is None else gt.reshape(n_tok, n).float().contiguous()
-    dcbar = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+    dcbar = torch.empty((n_tok, cols), device=dev, dtype=torch.float32)
     parts = L.bwd1_parts(n_tok, d)
     dq_part = torch.empty((max(1, parts), d), device=dev, dtype=torch.float32)
-    _run("read_bwd1", values_ptrs, rstd_ptrs, n, _p(g), _p(gt_c), _p(lg), _p(lse), _p(tc), _p(cbar_c),
-                               _p(c0c), _inv_sqrt(d), _p(dcbar), dr_ptrs, int(dr_accum), _p(wz), wz_stride,
-                               _p(dq_part), n_tok, d, dtype, st)
+    _run("read_bwd1", values_ptrs, rstd_ptrs, n, _p(g), _p(gt_c), _p(prob), _p(dots), dots.stride(0), _p(tc),
+         _p(cbar_c), cols,
+         _p(c0c), cols, float(lam), _inv_sqrt(d), _p(dcbar), cols, dr_ptrs, int(dr_accum), _p(wz), wz_stride,
+         _p(dq_part), _p(g_prop), _p(g_h0), float(beta), n_tok, d, dtype, st)
     dq = torch.empty(d, device=dev, dtype=torch.float32)
     if n_tok > 0:
         _run("reduce_rows", _p(dq_part), parts, d, _p(dq), st)
@@ -212,7 +217,7 @@ def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, lg, lse, tc, cbar_c, c0c, dr_ptrs, d
 
 def _backward_impl(ctx, g, gt, dv, accum):
     """dv: one gradient buffer per source, written (accum False) or added into (accum True) by the kernel."""
-    qc, cbar_c, c0c, lg, lse, tc, *rest = ctx.saved_tensors
+    qc, cbar_c, c0c, prob, dots, tc, *rest = ctx.saved_tensors
     n = ctx.n
     values, rstds = rest[:n], rest[n:]
     v0 = values[0]
@@ -225,7 +230,7 @@ def _backward_impl(ctx, g, gt, dv, accum):
     rp = L.u64_array(r.data_ptr() for r in rstds)
     dr = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
     wz = torch.empty((n, n_tok, 2), device=dev, dtype=torch.float32)
-    dq, dcbar = _bwd1(vp, rp, n, g, gt, lg, lse, tc, cbar_c, c0c, L.u64_array(dr[i].data_ptr() for i in range(n)),
+    dq, dcbar = _bwd1(vp, rp, n, g, gt, prob, dots, tc, cbar_c, c0c, L.u64_array(dr[i].data_ptr() for i in range(n)),
                       False, wz, n_tok, n_tok, d, dt, dev)
     for t in dv:
         if t.dtype != v0.dtype or not t.is_contiguous() or t.numel() != v0.numel() or not _aligned(t):
@@ -320,7 +325,7 @@ class DattnStack:
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
     transposed operand for its tensor-core product; the HIP write reads Q directly)."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
-                 "assembled")
+                 "assembled", "neg")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
@@ -338,6 +343,7 @@ class DattnStack:
         self.WZ = None
         self.bwd = {}
         self.assembled = set()
+        self.neg = {}         # s -> (gradient of update s, its negation), handed from _RstdStk to _WriteDelta
         self.eps = float(eps)
         self.r_done = [False] * self.n_steps      # R[s] (and the scores of update s) written by the write of s
         self.Q = self.QT = self.QB = self.DOTS = None
@@ -373,10 +379,12 @@ class DattnStack:
 
 class _WriteDelta(torch.autograd.Function):
     """V[s] = round(h - x), R[s] from the rounded update and the scores against the later read queries, in one pass
-    (fused_dattn.py:679-695); a plain subtraction into the slice for layouts the kernel does not take."""
+    (fused_dattn.py:679-695); a plain subtraction into the slice for layouts the kernel does not take. Backward
+    (g, -g): -g comes ready from the kernel that formed g when it is that kernel's output."""
 
     @staticmethod
     def forward(ctx, stack: DattnStack, s: int, h: torch.Tensor, x: torch.Tensor):
+        ctx.stack, ctx.s = stack, s
         out = _alias(stack.V, s)
         V = stack.V
         if (h.is_cuda and h.is_contiguous() and x.is_contiguous() and h.dtype == V.dtype == x.dtype
@@ -400,6 +408,12 @@ class _WriteDelta(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g: torch.Tensor):
+        stack, s = ctx.stack, ctx.s
+        ctx.stack = None
+        pair = stack.neg.pop(s, None) if stack is not None else None
+        if (pair is not None and g.data_ptr() == pair[0].data_ptr() and g.shape == pair[0].shape
+                and g.stride() == pair[0].stride() and g.dtype == pair[0].dtype):
+            return None, None, g, pair[1]
         return None, None, g, -g
 
 
@@ -427,17 +441,20 @@ class _RstdStk(torch.autograd.Function):
         xc = x.contiguous()
         reads = sorted(k for k in stack.bwd if k >= max(s, 1))     # the reads of update s whose backward ran
         dv = torch.empty_like(xc)
+        dv_neg = torch.empty_like(xc)
         grc = None if gr is None else gr.float().contiguous()
         g_ptrs = L.u64_array(stack.bwd[k][0].data_ptr() for k in reads)
         wz_ptrs = L.u64_array(stack.WZ[_pair(k, s)].data_ptr() for k in reads)
         q_ptrs = L.u64_array(stack.bwd[k][1].data_ptr() for k in reads)
-        _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc), _p(dv),
+        _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc), _p(dv), _p(dv_neg),
                                      stack.n_tok, stack.d, _dtype_code(xc.dtype), _stream(xc.device))
         stack.assembled.add(s)
         for k in [k for k in stack.bwd if all(j in stack.assembled for j in range(k + 1))]:
             del stack.bwd[k]              # every update read by read k has its gradient: drop g_k
+        if dv.shape == x.shape:
+            stack.neg[s] = (dv, dv_neg)   # the write's backward returns dv_neg for its x input
         ctx.stack = ctx.x = None          # release the stack from this node
-        return None, None, dv.view_as(x), None
+        return None, None, dv.view(x.shape), None
 
 
 class FusedDattnReadStk(torch.autograd.Function):
@@ -462,8 +479,7 @@ class FusedDattnReadStk(torch.autograd.Function):
             raise RuntimeError("delta_attnres stacked read: cbar must be (b, t, n) and c0 (n,)")
         out = torch.empty_like(base)
         tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
-        lg = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
-        lse = torch.empty(n_tok, device=dev, dtype=torch.float32)
+        prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
         vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
         rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
         if stack.DOTS is not None and step >= 1 and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
@@ -471,15 +487,15 @@ class FusedDattnReadStk(torch.autograd.Function):
         else:
             dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
             _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
-        _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base), _p(cbar_c), _p(c0c), _inv_sqrt(d), _p(out),
-                                  _p(tc), _p(lg), _p(lse), n_tok, d, dt, st)
-        ctx.save_for_backward(qc, cbar_c, c0c, lg, lse, tc)
+        _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base), _p(None), 0.0, _p(cbar_c), n, _p(c0c), n, 1.0,
+             _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
+        ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc)
         ctx.stack, ctx.step, ctx.n, ctx.q_dtype, ctx.base_shape = stack, int(step), n, q.dtype, base.shape
         return out, tc.view(*base.shape[:-1], n)
 
     @staticmethod
     def backward(ctx, g: torch.Tensor, gt: torch.Tensor | None):
-        qc, cbar_c, c0c, lg, lse, tc = ctx.saved_tensors
+        qc, cbar_c, c0c, prob, dots, tc = ctx.saved_tensors
         stack, step, n = ctx.stack, ctx.step, ctx.n
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         stack.grads()
@@ -488,7 +504,7 @@ class FusedDattnReadStk(torch.autograd.Function):
         rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
         drp = L.u64_array(stack.dR[i].data_ptr() for i in range(n))
         wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
-        dq, dcbar = _bwd1(vp, rp, n, g, gt, lg, lse, tc, cbar_c, c0c, drp, True, wz, n_tok, n_tok, d,
+        dq, dcbar = _bwd1(vp, rp, n, g, gt, prob, dots, tc, cbar_c, c0c, drp, True, wz, n_tok, n_tok, d,
                           _dtype_code(stack.V.dtype), dev)
         stack.bwd[step] = (g, qc)        # for the updates' gradients, formed once per update
         final = [i == step or (step == 1 and i == 0) for i in range(n)]   # the last read of scale i, in backward order
@@ -496,5 +512,87 @@ class FusedDattnReadStk(torch.autograd.Function):
                  *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
         # Release the stack from this node: ctx attributes live as long as the graph node, and a training loop that
         # keeps each micro-batch's loss until the optimizer step would otherwise keep each micro-batch's stack.
+        ctx.stack = None
+        return grads
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# extension (no counterpart in the reference module): the caller's glue fused into the stacked read
+# ---------------------------------------------------------------------------------------------------------------
+class FusedCombineStk(torch.autograd.Function):
+    """One read of `LoopDeltaAttnRes.combine` (modeling_looped_transformer.py:148-169) for step >= 1 on the stacked
+    layout, with the caller's glue inside the kernels: the iteration-end blend base = proposal + beta (h0 - proposal)
+    (rounded step by step as the caller's ops round), the bookkeeping cbar = lam [coeffs, 1], c0 = lam [prior, 1]
+    (lam = 1 - beta at an iteration end, else 1), and next_prior = c0 written by the read. The read itself is
+    FusedDattnReadStk's. Backward: the blend's gradients (g - beta g to the proposal, beta g to h0) and the
+    coefficients' gradient lam (-g.v) come out of backward pass 1; no separate glue kernels.
+
+    (out, tc, next_prior) = apply(stack, step, q, proposal, h0, coeffs, prior, beta, at_boundary, *updates, *scales)
+    with coeffs (b, t, n-1) and prior (n-1,) the previous read's outputs; next_prior carries no gradient (the prior
+    is a constant of the schedule, as in the reference)."""
+
+    @staticmethod
+    def forward(ctx, stack: DattnStack, step: int, q, proposal, h0, coeffs, prior, beta: float, at_boundary: bool,
+                *srcs):
+        n = len(srcs) // 2
+        d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
+        if (proposal.dtype != stack.V.dtype or not proposal.is_contiguous() or proposal.shape[:-1] != stack.V.shape[1:3]
+                or proposal.shape[-1] != d or not _aligned(proposal)):
+            raise RuntimeError("delta_attnres fused combine: proposal must be contiguous, the stack's dtype and shape")
+        if at_boundary and (h0 is None or h0.dtype != proposal.dtype or h0.shape != proposal.shape
+                            or not h0.is_contiguous() or not _aligned(h0)):
+            raise RuntimeError("delta_attnres fused combine: h0 must match the proposal at an iteration end")
+        if not 2 <= n <= stack.n_steps:
+            raise RuntimeError(f"delta_attnres fused combine: {n} sources for a stack of {stack.n_steps}")
+        dt = _dtype_code(stack.V.dtype)
+        st = _stream(dev)
+        lam = 1.0 - float(beta) if at_boundary else 1.0
+        qc = q.detach().float().contiguous()
+        coeffs_c = coeffs.detach().float().contiguous()
+        prior_c = prior.detach().float().contiguous()
+        if coeffs_c.numel() != n_tok * (n - 1) or prior_c.numel() != n - 1:
+            raise RuntimeError("delta_attnres fused combine: coeffs must be (b, t, n-1) and prior (n-1,)")
+        out = torch.empty_like(proposal)
+        tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+        prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+        next_prior = torch.empty(n, device=dev, dtype=torch.float32)
+        vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
+        rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
+        if stack.DOTS is not None and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
+            dots = stack.DOTS[step - 1]
+        else:
+            dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
+            _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
+        _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(proposal), _p(h0 if at_boundary else None), float(beta),
+             _p(coeffs_c), n - 1, _p(prior_c), n - 1, lam, _inv_sqrt(d), _p(out), _p(tc), _p(prob),
+             _p(next_prior), n_tok, d, dt, st)
+        ctx.save_for_backward(qc, coeffs_c, prior_c, prob, dots, tc)
+        ctx.stack, ctx.step, ctx.n, ctx.q_dtype, ctx.shape = stack, int(step), n, q.dtype, proposal.shape
+        ctx.beta, ctx.at_boundary, ctx.lam = float(beta), bool(at_boundary), lam
+        ctx.mark_non_differentiable(next_prior)
+        return out, tc.view(*proposal.shape[:-1], n), next_prior
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor, gt: torch.Tensor | None, gnp):
+        qc, coeffs_c, prior_c, prob, dots, tc = ctx.saved_tensors
+        stack, step, n = ctx.stack, ctx.step, ctx.n
+        d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
+        stack.grads()
+        g = g.to(stack.V.dtype).contiguous()
+        g_prop = g_h0 = None
+        if ctx.at_boundary:
+            g_prop, g_h0 = torch.empty_like(g), torch.empty_like(g)
+        vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
+        rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
+        drp = L.u64_array(stack.dR[i].data_ptr() for i in range(n))
+        wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
+        dq, dcoeffs = _bwd1(vp, rp, n, g, gt, prob, dots, tc, coeffs_c, prior_c, drp, True, wz, n_tok, n_tok, d,
+                            _dtype_code(stack.V.dtype), dev, cols=n - 1, lam=ctx.lam, g_prop=g_prop, g_h0=g_h0,
+                            beta=ctx.beta)
+        stack.bwd[step] = (g, qc)
+        final = [i == step or (step == 1 and i == 0) for i in range(n)]
+        grads = (None, None, dq.to(ctx.q_dtype), g_prop if ctx.at_boundary else g, g_h0,
+                 dcoeffs.view(*ctx.shape[:-1], n - 1), None, None, None,
+                 *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
         ctx.stack = None
         return grads

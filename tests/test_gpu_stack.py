@@ -76,6 +76,26 @@ def test_layouts_agree(dtype):
         assert max(err_norm(a, b) for a, b in zip(grad_list(g), grad_list(gl))) <= tol
 
 
+@pytest.mark.parametrize("K,R", [(3, 3), (1, 5)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["stack", "scores"])
+def test_fused_glue_matches_torch_glue(monkeypatch, K, R, dtype, mode):
+    """The stacked read with the caller's glue in its kernels (FusedCombineStk) against the same read with the glue
+    as torch ops (LOOP_DATTN_FUSE_GLUE=0): the forward is the same sequence of roundings, so the same bits; the
+    gradients agree to round-off (autograd adds a proposal's gradient terms in another order). K = 1 makes every
+    read an iteration end."""
+    cfg = chain_cfg(K, R, dtype)
+    print(f"case glue K{K} R{R} {dtype} {mode}", flush=True)
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", "0")
+    ht, gt = hip_chain(cfg, mode)
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", "1")
+    hf, gf = hip_chain(cfg, mode)
+    assert torch.equal(hf, ht)
+    tol = 1e-6 if dtype == torch.float32 else 4e-3
+    worst = max(err_norm(a, b) for a, b in zip(grad_list(gf), grad_list(gt)))
+    assert worst <= tol, worst
+
+
 def test_stack_and_list_read_bitwise_on_shared_scales():
     """One read, both layouts, the same sources and the same scale tensors: the same kernels give the same bits."""
     from loopback_amd import fused_dattn as FD

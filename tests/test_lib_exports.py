@@ -83,6 +83,18 @@ def test_argument_checks_before_launch(lib):
                             16, 1e-6, 1, null) == -1
     assert L.ldr_split_queries(null, 8, ctypes.c_void_p(4096), null) == -1
     assert L.ldr_dv_assemble(too_many, too_many, too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), null,
-                             ctypes.c_void_p(4096), 16, 64, 1, null) == -2
+                             ctypes.c_void_p(4096), null, 16, 64, 1, null) == -2
+    # a blend needs both gradient outputs
+    one = lib.u64_array([4096])
+    p = ctypes.c_void_p(4096)
+    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, p,
+                           null, 0.5, 16, 64, 1, null) == -1
+    # the raw scores' row stride covers the tokens
+    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 8, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, null,
+                           null, 0.0, 16, 64, 1, null) == -1
+    # coefficient columns: n (as the read takes them) or n - 1 (fused bookkeeping), nothing else
+    two = lib.u64_array([4096, 4096])
+    assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 3, p, 2, 1.0, 0.125, p, p, p, null, 16, 64, 1,
+                          null) == -1
     # zero tokens: accepted, nothing launched
     assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 0, 64, 1e-6, 1, null) == 0
