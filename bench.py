@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import argparse
 import contextlib
+import gc
 import json
 import os
 import statistics
@@ -86,8 +87,9 @@ class KernelTimer:
 def family_bytes(cfg, mode):
     """Compulsory HBM bytes per pass (T tokens) of each kernel family of this build -- what each kernel must move:
     write 3 rows per token (h, x in; V out), read (n+2) (n sources, base in; out), scores online n, backward pass 1
-    (n+1) (n sources, g), update gradient (m+2) (the m output gradients of the reads holding the update, the update,
-    the result) -- in rows of e * d bytes; per-(token, source) fp32 scalars left out (< 1 %).
+    (n+1) (n sources, g), update gradient (m+3) (the m output gradients of the reads holding the update, the update,
+    the result and its negation for the write's x) -- in rows of e * d bytes; per-(token, source) fp32 scalars left
+    out (< 1 %).
     Also the reference dataflow's total (the formula of the survey), which moves more in its backward."""
     from loopback_amd.chain import algorithmic_bytes_per_token
     e = 2 if cfg.dtype == torch_bf16() else 4
@@ -99,7 +101,7 @@ def family_bytes(cfg, mode):
         fam["dots_online"] = S2 * row
     if cfg.backward:
         fam["read_bwd1"] = (S2 + N - 1) * row
-        fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 2 * N) * row
+        fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 3 * N) * row
     ref_total = algorithmic_bytes_per_token(N, cfg.d, e, backward=cfg.backward, dots=(mode == "scores"))["total"] * T
     return fam, ref_total
 
@@ -155,6 +157,11 @@ def main():
     for _ in range(args.warmup):
         run_chain(cfg, h0, D, Q, G, args.mode)
     torch.cuda.synchronize()
+    # The interpreter's long-lived objects (torch, the loaded modules) go to the permanent generation, as a serving
+    # or training loop does after start-up: a full cyclic collection walks them all (~40 ms here) and would stall
+    # the launch stream once every few steps; the steps themselves create no cycles that need collecting.
+    gc.collect()
+    gc.freeze()
     timer = KernelTimer()
     t0 = time.perf_counter()
     for step in range(args.steps):

@@ -38,13 +38,13 @@
 #define LDR_AS_MAX_VPT 3
 #endif
 #ifndef LDR_B1_MAX_VPT
-#define LDR_B1_MAX_VPT 3     // backward pass 1 (holds g and two accumulators per element)
+#define LDR_B1_MAX_VPT 4     // backward pass 1 (holds g and two accumulators per element)
 #endif
 #ifndef LDR_B1_C
 #define LDR_B1_C 0           // backward pass 1: sources per chunk (0 = by vectors per lane)
 #endif
 #ifndef LDR_B1_WAVE_ROWS
-#define LDR_B1_WAVE_ROWS 0   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
+#define LDR_B1_WAVE_ROWS 1   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
 #ifndef LDR_NT
 #define LDR_NT 1             // non-temporal loads for the streamed sources
@@ -819,11 +819,13 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
           IO<T>::store(g_prop + roff + R.c8(v) * 8, gpv);
         }
       }
-      float a[VPT][8], b[VPT][8];
+      // dq of the row is sum_i p_i r_i (gp_i - Sacc) v_i: the gp part goes straight into the running dq, the
+      // Sacc part (Sacc known only after the last source) through b = sum_i p_i r_i v_i
+      float b[VPT][8];
 #pragma unroll
       for (int v = 0; v < VPT; ++v)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) { a[v][k] = 0.f; b[v][k] = 0.f; }
+        for (int k = 0; k < 8; ++k) b[v][k] = 0.f;
       float sacc = 0.f;
       // one source's share once its g.v is known: the scalars, the two accumulators, g.v to LDS
       auto take = [&](int i, float gd, const typename IO<T>::Raw (&rw)[VPT]) {
@@ -838,7 +840,7 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
           IO<T>::unpack(rw[v], e);
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
-            a[v][k] += alpha * e[k];
+            dqa[v][k] += alpha * e[k];
             b[v][k] += pr * e[k];
           }
         }
@@ -888,7 +890,7 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
 #pragma unroll
         for (int v = 0; v < VPT; ++v)
 #pragma unroll
-          for (int k = 0; k < 8; ++k) dqa[v][k] += a[v][k] - sacc * b[v][k];
+          for (int k = 0; k < 8; ++k) dqa[v][k] -= sacc * b[v][k];
         if (R.lr == 0) s_sacc[rr] = sacc;
       }
     }
