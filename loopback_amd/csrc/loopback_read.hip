@@ -26,13 +26,13 @@
 #define LDR_RF_UNROLL 8      // read forward: sources loaded per batch
 #endif
 #ifndef LDR_RF_MAX_VPT
-#define LDR_RF_MAX_VPT 2     // read forward: most 16-byte vectors per lane in a row
+#define LDR_RF_MAX_VPT 4     // read forward: most 16-byte vectors per lane in a row
 #endif
 #ifndef LDR_AS_RB
 #define LDR_AS_RB 4          // update gradient: token rows per lane (each query load serves all of them)
 #endif
 #ifndef LDR_AS_JB
-#define LDR_AS_JB 2          // update gradient: reads whose rows are loaded together
+#define LDR_AS_JB 1          // update gradient: reads whose rows are loaded together
 #endif
 #ifndef LDR_AS_MAX_VPT
 #define LDR_AS_MAX_VPT 3
@@ -399,25 +399,25 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int WM_TT = 32;   // tokens per workgroup
 constexpr int WM_KC = 64;   // columns per chunk
-constexpr int WM_NB = 4;    // up to 64 queries: four 16-query blocks
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
+template <int NB>   // NB 16-query blocks (nq <= 16 NB); NB = 0: no scores
 __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h, const bf16_t* __restrict__ x,
                                                    bf16_t* __restrict__ v, float* __restrict__ r,
                                                    const bf16_t* __restrict__ qb, int64_t qb_part_stride,
                                                    float* __restrict__ dots, int64_t n_tok, int d, int nq,
                                                    int64_t dots_jstride, float eps) {
-  __shared__ f32x4_t s_part[4][2][WM_NB][64];
+  constexpr int NBA = NB > 0 ? NB : 1;   // array extents
+  __shared__ f32x4_t s_part[4][2][NBA][64];
   __shared__ float s_ss[4][2][16];
   const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
   const int64_t t0 = (int64_t)blockIdx.x * WM_TT;
-  const int nb = (nq + 15) >> 4;
-  f32x4_t acc[2][WM_NB];
+  f32x4_t acc[2][NBA];
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-    for (int b = 0; b < WM_NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float ss[2] = {0.f, 0.f};
   int64_t roff[2];
   bool tok_ok[2];
@@ -428,11 +428,25 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
     roff[mb] = (tok_ok[mb] ? tok : n_tok - 1) * (int64_t)d;
   }
   // this lane's query row in each block, clamped (rows past nq are computed and never stored)
-  int qrow[WM_NB];
+  int qrow[NBA];
 #pragma unroll
-  for (int b = 0; b < WM_NB; ++b) qrow[b] = min(16 * b + row, nq > 0 ? nq - 1 : 0);
+  for (int b = 0; b < NBA; ++b) qrow[b] = min(16 * b + row, nq > 0 ? nq - 1 : 0);
   const int nchunks = (d + WM_KC - 1) / WM_KC;
-  for (int c = w; c < nchunks; c += 4) {
+  // a chunk's h and x rows: both 16-token blocks, the lane's two 8-column halves (clamped in bounds)
+  auto load_hx = [&](int c, uint4 (&hr)[2][2], uint4 (&xr)[2][2]) {
+    const int col = c * WM_KC + quad * 16;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int cc = col + 8 * hf < d ? col + 8 * hf : 0;
+        hr[mb][hf] = *reinterpret_cast<const uint4*>(h + roff[mb] + cc);
+        xr[mb][hf] = *reinterpret_cast<const uint4*>(x + roff[mb] + cc);
+      }
+  };
+  uint4 hr[2][2], xr[2][2];
+  if (w < nchunks) load_hx(w, hr, xr);
+  for (int c = w; c < nchunks; c += 4) {   // wave-uniform trip count
     const int col = c * WM_KC + quad * 16;
     bool col_ok[2];
     int cc[2];
@@ -441,14 +455,18 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
       col_ok[hf] = col + 8 * hf < d;
       cc[hf] = col_ok[hf] ? col + 8 * hf : 0;
     }
-    uint4 hr[2][2], xr[2][2];
+    // the chunk's query parts (cache-resident), requested before the data is touched
+    uint4 qv[3][NBA][2];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int p = 0; p < 3 * (NB > 0); ++p)
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        hr[mb][hf] = *reinterpret_cast<const uint4*>(h + roff[mb] + cc[hf]);
-        xr[mb][hf] = *reinterpret_cast<const uint4*>(x + roff[mb] + cc[hf]);
-      }
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          qv[p][b][hf] = *reinterpret_cast<const uint4*>(qb + p * qb_part_stride + (int64_t)qrow[b] * d + cc[hf]);
+    // the next chunk's rows in flight while this one is computed
+    uint4 hn[2][2], xn[2][2];
+    if (c + 4 < nchunks) load_hx(c + 4, hn, xn);
     uint4 va[2][2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
@@ -469,26 +487,25 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
         for (int k = 0; k < 8; ++k) ss[mb] += rv[k] * rv[k];
         if (ok) *reinterpret_cast<uint4*>(v + roff[mb] + cc[hf]) = u;
       }
-    for (int p = 0; p < 3; ++p) {
-      const bf16_t* qp = qb + p * qb_part_stride;
 #pragma unroll
-      for (int b = 0; b < WM_NB; ++b) {
-        if (b < nb) {
-          uint4 qv[2];
+    for (int p = 0; p < 3 * (NB > 0); ++p)
 #pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            qv[hf] = *reinterpret_cast<const uint4*>(qp + (int64_t)qrow[b] * d + cc[hf]);
-            if (!col_ok[hf]) qv[hf] = make_uint4(0u, 0u, 0u, 0u);
-          }
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const uint4 qh = col_ok[hf] ? qv[p][b][hf] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
           for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
-              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qv[hf]),
-                                                                   acc[mb][b], 0, 0, 0);
+            acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qh), acc[mb][b],
+                                                                 0, 0, 0);
         }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        hr[mb][hf] = hn[mb][hf];
+        xr[mb][hf] = xn[mb][hf];
       }
-    }
   }
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
@@ -496,8 +513,7 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
     ss[mb] += __shfl_xor(ss[mb], 32, 64);
     if (quad == 0) s_ss[w][mb][row] = ss[mb];
 #pragma unroll
-    for (int b = 0; b < WM_NB; ++b)
-      if (b < nb) s_part[w][mb][b][l] = acc[mb][b];
+    for (int b = 0; b < NB; ++b) s_part[w][mb][b][l] = acc[mb][b];
   }
   __syncthreads();
   if (tid < 32) {
@@ -506,8 +522,8 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
     const int64_t tok = t0 + tid;
     if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
   }
-  for (int e = tid; e < 2 * nb * 64; e += WG) {
-    const int mb = e / (nb * 64), rem = e - mb * nb * 64, b = rem >> 6, ll = rem & 63;
+  for (int e = tid; e < 2 * NB * 64; e += WG) {
+    const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
     const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
     const int jj = 16 * b + (ll & 15);
     if (jj >= nq) continue;
@@ -1243,9 +1259,16 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == LDR_BF16) {   // matrix-core scores
     const unsigned grid = (unsigned)cdiv(n_tok, WM_TT);
-    hipLaunchKernelGGL(k_write_mfma, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(h),
-                       static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), r_out,
-                       static_cast<const bf16_t*>(qb), qb_part_stride, dots, n_tok, (int)d, (int)nq, dots_jstride, eps);
+    const bf16_t* qbp = nq > 0 ? static_cast<const bf16_t*>(qb) : nullptr;
+#define LDR_WM_LAUNCH(NBV)                                                                                        \
+  hipLaunchKernelGGL(k_write_mfma<NBV>, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(h),               \
+                     static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), r_out, qbp, qb_part_stride, dots, \
+                     n_tok, (int)d, (int)nq, dots_jstride, eps)
+    if (nq == 0) LDR_WM_LAUNCH(0);
+    else if (nq <= 16) LDR_WM_LAUNCH(1);
+    else if (nq <= 32) LDR_WM_LAUNCH(2);
+    else LDR_WM_LAUNCH(4);
+#undef LDR_WM_LAUNCH
   } else {
     const unsigned grid = (unsigned)cdiv(n_tok, WR_TT);
     hipLaunchKernelGGL((k_write_dots<float>), dim3(grid), dim3(WG), 0, st, static_cast<const float*>(h),
@@ -1296,7 +1319,7 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
   int e = fill_src(s, src_v, src_r, n);
   if (e) return e;
   int vpt, tpr;
-  if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, false, LDR_RF_VPT))) return e;
+  if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, true, LDR_RF_VPT))) return e;
   if (n_tok == 0) return LDR_OK;
   const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
   const int tt = tile_tokens(tpr);
