@@ -191,12 +191,12 @@ def _forward_impl(ctx, q, base, cbar, c0, srcs):
 
 
 def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_ptrs, dr_accum, wz, wz_stride, n_tok, d,
-          dtype, dev, cols=None, lam=1.0, g_prop=None, g_h0=None, beta=0.0):
+          dtype, dev, cols=None, lam=1.0, g_prop=None, g_h0=None, beta=0.0, dq=None):
     """Pass 1 of the backward plus the dq reduction; returns (dq fp32, dcbar [n_tok, cols]). prob and dots are the
     forward's probabilities [n_tok, n] and raw scores [n, >= n_tok] (row stride dots.stride(0)). cols = n: cbar_c and c0c
     are the read's own; cols = n - 1: they are the previous read's coefficients and prior (scaled by lam, the newest
     entry implied) and dcbar is the gradient of those coefficients. g_prop / g_h0 receive the iteration-end blend's
-    gradients when given."""
+    gradients when given. dq: an fp32 row of d to reduce the query gradient into (else a new one)."""
     st = _stream(dev)
     cols = n if cols is None else cols
     gt_c = None if gt is None else gt.reshape(n_tok, n).float().contiguous()
@@ -207,7 +207,7 @@ def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_ptrs
          _p(cbar_c), cols,
          _p(c0c), cols, float(lam), _inv_sqrt(d), _p(dcbar), cols, dr_ptrs, int(dr_accum), _p(wz), wz_stride,
          _p(dq_part), _p(g_prop), _p(g_h0), float(beta), n_tok, d, dtype, st)
-    dq = torch.empty(d, device=dev, dtype=torch.float32)
+    dq = torch.empty(d, device=dev, dtype=torch.float32) if dq is None else dq
     if n_tok > 0:
         _run("reduce_rows", _p(dq_part), parts, d, _p(dq), st)
     else:
@@ -325,7 +325,7 @@ class DattnStack:
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
     transposed operand for its tensor-core product; the HIP write reads Q directly)."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
-                 "assembled", "neg")
+                 "assembled", "neg", "dQ")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
@@ -344,6 +344,7 @@ class DattnStack:
         self.bwd = {}
         self.assembled = set()
         self.neg = {}         # s -> (gradient of update s, its negation), handed from _RstdStk to _WriteDelta
+        self.dQ = None        # the query gradient rows of the fused combines' backwards (fp32)
         self.eps = float(eps)
         self.r_done = [False] * self.n_steps      # R[s] (and the scores of update s) written by the write of s
         self.Q = self.QT = self.QB = self.DOTS = None
@@ -525,14 +526,17 @@ class FusedCombineStk(torch.autograd.Function):
     (rounded step by step as the caller's ops round), the bookkeeping cbar = lam [coeffs, 1], c0 = lam [prior, 1]
     (lam = 1 - beta at an iteration end, else 1), and next_prior = c0 written by the read. The read itself is
     FusedDattnReadStk's. Backward: the blend's gradients (g - beta g to the proposal, beta g to h0) and the
-    coefficients' gradient lam (-g.v) come out of backward pass 1; no separate glue kernels.
+    coefficients' gradient lam (-g.v) come out of backward pass 1; no separate glue kernels. The query is the whole
+    (n_steps - 1, d) parameter (read `step` uses row step - 1): each backward reduces its row straight into the stack's
+    fp32 query gradient, which the last backward of the pass (read 1) returns -- one gradient tensor per pass instead
+    of a zero-filled one per read.
 
-    (out, tc, next_prior) = apply(stack, step, q, proposal, h0, coeffs, prior, beta, at_boundary, *updates, *scales)
-    with coeffs (b, t, n-1) and prior (n-1,) the previous read's outputs; next_prior carries no gradient (the prior
-    is a constant of the schedule, as in the reference)."""
+    (out, tc, next_prior) = apply(stack, step, query, proposal, h0, coeffs, prior, beta, at_boundary, *updates,
+    *scales) with coeffs (b, t, n-1) and prior (n-1,) the previous read's outputs; next_prior carries no gradient
+    (the prior is a constant of the schedule, as in the reference)."""
 
     @staticmethod
-    def forward(ctx, stack: DattnStack, step: int, q, proposal, h0, coeffs, prior, beta: float, at_boundary: bool,
+    def forward(ctx, stack: DattnStack, step: int, query, proposal, h0, coeffs, prior, beta: float, at_boundary: bool,
                 *srcs):
         n = len(srcs) // 2
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
@@ -542,12 +546,14 @@ class FusedCombineStk(torch.autograd.Function):
         if at_boundary and (h0 is None or h0.dtype != proposal.dtype or h0.shape != proposal.shape
                             or not h0.is_contiguous() or not _aligned(h0)):
             raise RuntimeError("delta_attnres fused combine: h0 must match the proposal at an iteration end")
-        if not 2 <= n <= stack.n_steps:
-            raise RuntimeError(f"delta_attnres fused combine: {n} sources for a stack of {stack.n_steps}")
+        if not 2 <= n <= stack.n_steps or n != step + 1:
+            raise RuntimeError(f"delta_attnres fused combine: {n} sources at step {step} of a stack of {stack.n_steps}")
+        if query.dim() != 2 or query.shape[-1] != d or not 1 <= step <= query.shape[0]:
+            raise RuntimeError(f"delta_attnres fused combine: query must be (n_steps - 1, {d}) with a row for step {step}")
         dt = _dtype_code(stack.V.dtype)
         st = _stream(dev)
         lam = 1.0 - float(beta) if at_boundary else 1.0
-        qc = q.detach().float().contiguous()
+        qc = query[step - 1].detach().float().contiguous()
         coeffs_c = coeffs.detach().float().contiguous()
         prior_c = prior.detach().float().contiguous()
         if coeffs_c.numel() != n_tok * (n - 1) or prior_c.numel() != n - 1:
@@ -567,18 +573,22 @@ class FusedCombineStk(torch.autograd.Function):
              _p(coeffs_c), n - 1, _p(prior_c), n - 1, lam, _inv_sqrt(d), _p(out), _p(tc), _p(prob),
              _p(next_prior), n_tok, d, dt, st)
         ctx.save_for_backward(qc, coeffs_c, prior_c, prob, dots, tc)
-        ctx.stack, ctx.step, ctx.n, ctx.q_dtype, ctx.shape = stack, int(step), n, q.dtype, proposal.shape
+        ctx.stack, ctx.step, ctx.n, ctx.shape = stack, int(step), n, proposal.shape
+        ctx.q_shape, ctx.q_dtype = query.shape, query.dtype
         ctx.beta, ctx.at_boundary, ctx.lam = float(beta), bool(at_boundary), lam
         ctx.mark_non_differentiable(next_prior)
+        ctx.set_materialize_grads(False)
         return out, tc.view(*proposal.shape[:-1], n), next_prior
 
     @staticmethod
-    def backward(ctx, g: torch.Tensor, gt: torch.Tensor | None, gnp):
+    def backward(ctx, g: torch.Tensor | None, gt: torch.Tensor | None, gnp):
         qc, coeffs_c, prior_c, prob, dots, tc = ctx.saved_tensors
         stack, step, n = ctx.stack, ctx.step, ctx.n
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         stack.grads()
-        g = g.to(stack.V.dtype).contiguous()
+        if stack.dQ is None or stack.dQ.shape != ctx.q_shape:
+            stack.dQ = torch.zeros(ctx.q_shape, device=dev, dtype=torch.float32)
+        g = torch.zeros(ctx.shape, device=dev, dtype=stack.V.dtype) if g is None else g.to(stack.V.dtype).contiguous()
         g_prop = g_h0 = None
         if ctx.at_boundary:
             g_prop, g_h0 = torch.empty_like(g), torch.empty_like(g)
@@ -586,12 +596,13 @@ class FusedCombineStk(torch.autograd.Function):
         rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
         drp = L.u64_array(stack.dR[i].data_ptr() for i in range(n))
         wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
-        dq, dcoeffs = _bwd1(vp, rp, n, g, gt, prob, dots, tc, coeffs_c, prior_c, drp, True, wz, n_tok, n_tok, d,
-                            _dtype_code(stack.V.dtype), dev, cols=n - 1, lam=ctx.lam, g_prop=g_prop, g_h0=g_h0,
-                            beta=ctx.beta)
+        _, dcoeffs = _bwd1(vp, rp, n, g, gt, prob, dots, tc, coeffs_c, prior_c, drp, True, wz, n_tok, n_tok, d,
+                           _dtype_code(stack.V.dtype), dev, cols=n - 1, lam=ctx.lam, g_prop=g_prop, g_h0=g_h0,
+                           beta=ctx.beta, dq=stack.dQ[step - 1])
         stack.bwd[step] = (g, qc)
         final = [i == step or (step == 1 and i == 0) for i in range(n)]
-        grads = (None, None, dq.to(ctx.q_dtype), g_prop if ctx.at_boundary else g, g_h0,
+        dquery = stack.dQ.to(ctx.q_dtype) if step == 1 else None   # read 1's backward is the pass's last
+        grads = (None, None, dquery, g_prop if ctx.at_boundary else g, g_h0,
                  dcoeffs.view(*ctx.shape[:-1], n - 1), None, None, None,
                  *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
         ctx.stack = None

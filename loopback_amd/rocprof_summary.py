@@ -1,0 +1,167 @@
+"""Summaries of rocprofv3 output for the headline chain: per-kernel time of one pass (kernel trace) and HBM bytes per
+launch (FETCH_SIZE / WRITE_SIZE counter passes, scaled by what the same counters read for a device-to-device copy of
+known size). Writes the markdown tables kept with the profiles and the per-launch traffic figure bench.py reports.
+
+    python -m loopback_amd.rocprof_summary --trace gpurun_out/kt/kt_kernel_trace.csv \\
+        --stats gpurun_out/kt/kt_kernel_stats.csv --fetch gpurun_out/pf/pf_counter_collection.csv \\
+        --write gpurun_out/pw/pw_counter_collection.csv \\
+        --calib-fetch gpurun_out/cf/cf_counter_collection.csv --calib-write gpurun_out/cw/cw_counter_collection.csv \\
+        --config c4 --mode scores --out profiles
+
+The passes are split at the one k_split_queries launch each chain pass starts with; the last complete pass of the
+trace and the last pass of each counter run are the ones summarized.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import os
+import sys
+
+FAMILIES = [("k_read_fwd", "read_fwd"), ("k_bwd1", "read_bwd1"), ("k_dv_assemble", "dv_assemble"),
+            ("k_write_mfma", "write_dots"), ("k_write_dots", "write_dots"), ("k_dots", "dots_online"),
+            ("k_reduce_rows", "reduce_rows"), ("k_split_queries", "split_queries"), ("k_rstd", "rstd"),
+            ("k_bwd2_list", "read_bwd2_list")]
+COPY_BYTES = 1 << 30   # bench.py --copy-calibration copies 1 GiB
+
+
+def family(name: str) -> str:
+    for key, fam in FAMILIES:
+        if key in name:
+            return fam
+    return "torch / runtime"
+
+
+def _rows(path):
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _passes(rows, key="Start_Timestamp"):
+    """The rows of each chain pass, in launch order (a pass starts at its k_split_queries launch)."""
+    rows = sorted(rows, key=lambda r: int(r[key]))
+    starts = [i for i, r in enumerate(rows) if "k_split_queries" in r["Kernel_Name"]]
+    return [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
+
+
+def trace_pass(path):
+    """Per-family launches and GPU time of the last complete pass of a kernel trace; also the pass's span."""
+    passes = _passes(_rows(path))
+    if len(passes) < 2:
+        raise SystemExit("kernel trace: need at least two chain passes")
+    p = passes[-2]   # the last complete pass (the final one runs into the end of the program)
+    out = {}
+    for r in p:
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        t = out.setdefault(family(r["Kernel_Name"]), [0, 0.0])
+        t[0] += 1
+        t[1] += us
+    nxt = passes[-1][0]
+    span_ms = (int(nxt["Start_Timestamp"]) - int(p[0]["Start_Timestamp"])) / 1e6
+    return out, span_ms
+
+
+def counter_pass(path, counter):
+    """Per-family launches and counter total (KiB) of the last pass of a counter run."""
+    rows = [r for r in _rows(path) if r["Counter_Name"] == counter]
+    # one row per dispatch per counter
+    p = _passes(rows, key="Dispatch_Id")[-1]
+    out = {}
+    for r in p:
+        t = out.setdefault(family(r["Kernel_Name"]), [0, 0.0])
+        t[0] += 1
+        t[1] += float(r["Counter_Value"])
+    return out
+
+
+def calibration(path, counter):
+    rows = [r for r in _rows(path) if r["Counter_Name"] == counter and "copyBuffer" in r["Kernel_Name"]]
+    if not rows:
+        raise SystemExit(f"calibration: no copy kernel in {path}")
+    kib = max(float(r["Counter_Value"]) for r in rows)
+    return (COPY_BYTES / 1024) / kib
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--trace", required=True)
+    ap.add_argument("--stats", default=None, help="the --stats kernel summary of the same trace run")
+    ap.add_argument("--fetch", required=True)
+    ap.add_argument("--write", required=True)
+    ap.add_argument("--calib-fetch", required=True)
+    ap.add_argument("--calib-write", required=True)
+    ap.add_argument("--config", default="c4")
+    ap.add_argument("--mode", default="scores")
+    ap.add_argument("--out", default="profiles")
+    ap.add_argument("--commands", default="", help="the commands that produced the inputs (quoted into the summaries)")
+    a = ap.parse_args(argv)
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, root)
+    import bench   # the byte model the bench line uses
+    from loopback_amd.chain import CONFIGS
+    cfg = CONFIGS[a.config]
+    fam_bytes, _ = bench.family_bytes(cfg, a.mode)
+
+    kt, span_ms = trace_pass(a.trace)
+    fetch = counter_pass(a.fetch, "FETCH_SIZE")
+    write = counter_pass(a.write, "WRITE_SIZE")
+    fs = calibration(a.calib_fetch, "FETCH_SIZE")
+    ws = calibration(a.calib_write, "WRITE_SIZE")
+
+    busy = sum(v[1] for v in kt.values()) / 1e3
+    lines = [f"# Kernel time per chain pass: config {a.config} ({cfg.name}), mode {a.mode}", ""]
+    if a.commands:
+        lines += ["Commands:", "", *["    " + c for c in a.commands.split(";;")], ""]
+    lines += [f"One pass (the last complete one of the trace): span {span_ms:.2f} ms between pass starts, "
+              f"{busy:.2f} ms of kernel time.", "",
+              "| kernel family | launches | total ms | mean us | algorithmic GB | GB/s at the mean |",
+              "|---|---|---|---|---|---|"]
+    for famname, (n, us) in sorted(kt.items(), key=lambda x: -x[1][1]):
+        ab = fam_bytes.get(famname)
+        gbs = f"{ab / (us * 1e-6) / 1e9:.0f}" if ab else "-"
+        lines.append(f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | "
+                     f"{ab / 1e9:.2f} | {gbs} |" if ab else f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | - | - |")
+    if a.stats:   # rocprofv3's own per-kernel summary over the whole run (warm-up and timed passes)
+        st = sorted(_rows(a.stats), key=lambda r: -float(r["TotalDurationNs"]))[:12]
+        lines += ["", "rocprofv3 --stats over the whole run (all passes; names shortened):", "",
+                  "| kernel | calls | total ms | average us | % |", "|---|---|---|---|---|"]
+        for r in st:
+            name = r["Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:80]
+            lines.append(f"| `{name}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.2f} | "
+                         f"{float(r['AverageNs']) / 1e3:.1f} | {r['Percentage']} |")
+    with open(os.path.join(a.out, f"kernels_chain_{a.config}.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+    per_launch = {}
+    lines = [f"# HBM traffic per kernel: config {a.config} ({cfg.name}), mode {a.mode}, one pass", ""]
+    if a.commands:
+        lines += ["Commands:", "", *["    " + c for c in a.commands.split(";;")], ""]
+    lines += [f"Calibration: a 1 GiB device-to-device copy reads FETCH_SIZE = {(COPY_BYTES / 1024) / fs:.0f} KiB and "
+              f"WRITE_SIZE = {(COPY_BYTES / 1024) / ws:.0f} KiB, so FETCH_SIZE is scaled by {fs:.3f} and WRITE_SIZE "
+              f"by {ws:.3f}.", "",
+              "| kernel | launches | fetched GB (scaled) | written GB (scaled) | algorithmic GB | measured / algorithmic "
+              "| HBM bytes per launch |", "|---|---|---|---|---|---|---|"]
+    for famname in sorted(fam_bytes, key=lambda k: -fam_bytes[k]):
+        if famname not in fetch:
+            continue
+        n = fetch[famname][0]
+        fb = fetch[famname][1] * 1024 * fs
+        wb = write.get(famname, [0, 0.0])[1] * 1024 * ws
+        per_launch[famname] = (fb + wb) / n
+        lines.append(f"| `{famname}` | {n} | {fb / 1e9:.2f} | {wb / 1e9:.2f} | {fam_bytes[famname] / 1e9:.2f} | "
+                     f"{(fb + wb) / fam_bytes[famname]:.3f} | {per_launch[famname]:.0f} |")
+    lines += ["", "Algorithmic bytes: the compulsory rows of each kernel family (bench.py `family_bytes`); per-(token, "
+              "source) fp32 scalars are not counted, which is most of the excess."]
+    with open(os.path.join(a.out, f"traffic_chain_{a.config}.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    with open(os.path.join(a.out, f"traffic_chain_{a.config}.txt"), "w") as f:
+        json.dump({"config": a.config, "mode": a.mode,
+                   "source": f"profiles/traffic_chain_{a.config}.md (commands and calibration there)",
+                   "fetch_scale": fs, "write_scale": ws, "hbm_bytes_per_launch": per_launch}, f, indent=1)
+        f.write("\n")
+
+
+if __name__ == "__main__":
+    main()
