@@ -90,7 +90,8 @@ def family_bytes(cfg, mode):
     (n+1) (n sources, g), update gradient (m+3) (the m output gradients of the reads holding the update, the update,
     the result and its negation for the write's x) -- in rows of e * d bytes; per-(token, source) fp32 scalars left
     out (< 1 %). With the caller's glue in the stacked read, a read at an iteration end also reads h0 and its
-    backward pass 1 writes the blend's two gradients.
+    backward pass 1 writes the blend's two gradients, and the update gradient of each update a read took as its
+    proposal also reads that read's proposal gradient (the add autograd would otherwise run).
     Also the reference dataflow's total (the formula of the survey), which moves more in its backward."""
     from loopback_amd.cell import fuse_glue
     from loopback_amd.chain import algorithmic_bytes_per_token
@@ -98,13 +99,14 @@ def family_bytes(cfg, mode):
     N, T = cfg.N, cfg.n_tok
     S2 = N * (N + 1) // 2 - 1
     row = e * cfg.d * T
-    ends = sum(1 for s in range(1, N) if s % cfg.K == cfg.K - 1) if mode != "list" and fuse_glue() else 0
+    fused = mode != "list" and fuse_glue()
+    ends = sum(1 for s in range(1, N) if s % cfg.K == cfg.K - 1) if fused else 0
     fam = {"write_dots": 3 * N * row, "read_fwd": (S2 + 2 * (N - 1) + ends) * row}
     if mode != "scores":
         fam["dots_online"] = S2 * row
     if cfg.backward:
         fam["read_bwd1"] = (S2 + N - 1 + 2 * ends) * row
-        fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 3 * N) * row
+        fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 3 * N + (N - 1 if fused else 0)) * row
     ref_total = algorithmic_bytes_per_token(N, cfg.d, e, backward=cfg.backward, dots=(mode == "scores"))["total"] * T
     return fam, ref_total
 

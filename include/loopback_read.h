@@ -135,12 +135,14 @@ int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, 
  *   dv[tok,:] = round( sum_e ( w_e[tok] g_e[tok,:] + dzr_e[tok] q_e[:] ) + gr[tok] (-r[tok]^3) / d * v[tok,:] )
  * over the m reads e that hold update i: g_e that read's output gradient, (w_e, dzr_e) its wz pair for source i
  * (float2 per token), q_e its query (fp32, d). One fp32 sum, one rounding; gr may be NULL (no scale gradient).
- * dv_neg (may be NULL) receives -dv, the write's gradient to x (fused_dattn.py:694-695).
+ * dv_neg (may be NULL) receives -dv, the write's gradient to x (fused_dattn.py:694-695). With add != NULL (another
+ * gradient of the write's h, e.g. the read that took h as its proposal) dv holds round(dv + add) instead, the sum
+ * autograd would form; dv_neg stays -dv.
  * Replaces the dV read-modify-write of _dattn_bwd2_stk_kernel (fused_dattn.py:496-536, launched at 781-784) and
  * _rstd_bwd_acc_kernel (539-552, launched at 717-719). */
 int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                    const float* r, const float* gr, void* dv, void* dv_neg, int64_t n_tok, int64_t d, int dtype,
-                    void* stream);
+                    const float* r, const float* gr, const void* add, void* dv, void* dv_neg, int64_t n_tok, int64_t d,
+                    int dtype, void* stream);
 
 #ifdef __cplusplus
 }

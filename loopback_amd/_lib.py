@@ -12,7 +12,7 @@ import torch  # noqa: F401  -- first: the library must bind to the HIP runtime t
 
 from . import build as _build
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 F32, BF16 = 0, 1
 MAX_SOURCES = 64
 MAX_WIDTH = 8192
@@ -46,7 +46,7 @@ SIGNATURES = {
     "ldr_read_bwd2_list": (_i32, [_u64p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32,
                                   _c_void_p]),
     "ldr_dv_assemble": (_i32, [_u64p, _u64p, _u64p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                               _i64, _i64, _i32, _c_void_p]),
+                               _c_void_p, _i64, _i64, _i32, _c_void_p]),
 }
 
 

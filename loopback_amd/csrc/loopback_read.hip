@@ -1038,7 +1038,8 @@ constexpr int AS_JB = LDR_AS_JB;   // reads per batch of loads
 template <typename T, int VPT>
 __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* __restrict__ vsrc,
                                                     const float* __restrict__ r, const float* __restrict__ gr,
-                                                    T* __restrict__ dv, T* __restrict__ dv_neg, int64_t n_tok, int d,
+                                                    const T* __restrict__ add, T* __restrict__ dv,
+                                                    T* __restrict__ dv_neg, int64_t n_tok, int d,
                                                     int tpr) {
   constexpr int AS_RB = as_rb(VPT);
   const Rows R(d, tpr);
@@ -1096,16 +1097,24 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
     for (int k = 0; k < AS_RB; ++k) {
       const float rv = r[tokc[k]];
       const float c = gr ? gr[tokc[k]] * (-rv * rv * rv) / (float)d : 0.f;
-      float e[VPT][8];
+      float e[VPT][8], a[VPT][8];
 #pragma unroll
       for (int v = 0; v < VPT; ++v) IO<T>::load(vsrc + roff[k] + R.off(v), e[v]);
+      if (add) {   // a gradient of the write's h from elsewhere, added as autograd would add it
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) IO<T>::load(add + roff[k] + R.off(v), a[v]);
+      }
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
 #pragma unroll
         for (int x = 0; x < 8; ++x) acc[k][v][x] += c * e[v][x];
         if (tok[k] < n_tok && R.act(v)) {
-          IO<T>::store(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
           if (dv_neg) IO<T>::store_neg(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
+          if (add) {
+#pragma unroll
+            for (int x = 0; x < 8; ++x) acc[k][v][x] = IO<T>::round(acc[k][v][x]) + a[v][x];
+          }
+          IO<T>::store(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
         }
       }
     }
@@ -1188,7 +1197,7 @@ template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 4; }
+int ldr_abi_version(void) { return 5; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -1413,12 +1422,12 @@ int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, 
 }
 
 int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                    const float* r, const float* gr, void* dv, void* dv_neg, int64_t n_tok, int64_t d, int dtype,
-                    void* stream) {
+                    const float* r, const float* gr, const void* add, void* dv, void* dv_neg, int64_t n_tok, int64_t d,
+                    int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (m < 0 || m > MAXS) return LDR_E_SHAPE;
   if ((m > 0 && (!g || !wz || !q)) || !v || !r || !dv || n_tok < 0) return LDR_E_ARG;
-  if (!al16(v) || !al16(dv) || (dv_neg && !al16(dv_neg))) return LDR_E_ALIGN;
+  if (!al16(v) || !al16(dv) || (dv_neg && !al16(dv_neg)) || (add && !al16(add))) return LDR_E_ALIGN;
   AsmTab t;
   for (int64_t j = 0; j < MAXS; ++j) {
     t.g[j] = j < m ? reinterpret_cast<const void*>(g[j]) : nullptr;
@@ -1434,7 +1443,8 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT>), dim3(grid), dim3(WG), 0, st,
                                                                   t, (int)m, static_cast<const T*>(v), r, gr,
-                                                                  static_cast<T*>(dv), static_cast<T*>(dv_neg), n_tok,
+                                                                  static_cast<const T*>(add), static_cast<T*>(dv),
+                                                                  static_cast<T*>(dv_neg), n_tok,
                                                                   (int)d, tpr)))
   return launched();
 }

@@ -31,6 +31,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import weakref
 
 import torch
 
@@ -325,7 +326,7 @@ class DattnStack:
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
     transposed operand for its tensor-core product; the HIP write reads Q directly)."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
-                 "assembled", "neg", "dQ")
+                 "assembled", "neg", "dQ", "wh", "gadd")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
@@ -345,6 +346,8 @@ class DattnStack:
         self.assembled = set()
         self.neg = {}         # s -> (gradient of update s, its negation), handed from _RstdStk to _WriteDelta
         self.dQ = None        # the query gradient rows of the fused combines' backwards (fp32)
+        self.wh = {}          # s -> weak reference to the write's h (a fused combine that takes it as its proposal
+        self.gadd = {}        # hands its proposal gradient, gadd[s], to the update's gradient kernel)
         self.eps = float(eps)
         self.r_done = [False] * self.n_steps      # R[s] (and the scores of update s) written by the write of s
         self.Q = self.QT = self.QB = self.DOTS = None
@@ -386,6 +389,7 @@ class _WriteDelta(torch.autograd.Function):
     @staticmethod
     def forward(ctx, stack: DattnStack, s: int, h: torch.Tensor, x: torch.Tensor):
         ctx.stack, ctx.s = stack, s
+        stack.wh[s] = weakref.ref(h)
         out = _alias(stack.V, s)
         V = stack.V
         if (h.is_cuda and h.is_contiguous() and x.is_contiguous() and h.dtype == V.dtype == x.dtype
@@ -411,11 +415,18 @@ class _WriteDelta(torch.autograd.Function):
     def backward(ctx, g: torch.Tensor):
         stack, s = ctx.stack, ctx.s
         ctx.stack = None
-        pair = stack.neg.pop(s, None) if stack is not None else None
-        if (pair is not None and g.data_ptr() == pair[0].data_ptr() and g.shape == pair[0].shape
-                and g.stride() == pair[0].stride() and g.dtype == pair[0].dtype):
-            return None, None, g, pair[1]
-        return None, None, g, -g
+        if stack is None:
+            return None, None, g, -g
+        prep = stack.neg.pop(s, None)        # (gradient of h, gradient of x, the added proposal gradient or None)
+        left = stack.gadd.pop(s, None)       # a proposal gradient no update-gradient kernel took
+        if prep is not None:
+            dh, dx, added = prep
+            if (g.data_ptr() == dh.data_ptr() and g.shape == dh.shape and g.stride() == dh.stride()
+                    and g.dtype == dh.dtype):
+                return None, None, g, dx
+            # other consumers of the update added to its gradient: h takes all of it, x all but the proposal's
+            return None, None, g, -(g - added) if added is not None else -g
+        return None, None, (g if left is None else g + left), -g
 
 
 class _RstdStk(torch.autograd.Function):
@@ -444,16 +455,19 @@ class _RstdStk(torch.autograd.Function):
         dv = torch.empty_like(xc)
         dv_neg = torch.empty_like(xc)
         grc = None if gr is None else gr.float().contiguous()
+        added = stack.gadd.pop(s, None)       # the gradient of the write's h from the combine that took it
+        if added is not None and (added.shape != x.shape or added.dtype != xc.dtype or not added.is_contiguous()):
+            added = added.to(xc.dtype).contiguous().view(x.shape)
         g_ptrs = L.u64_array(stack.bwd[k][0].data_ptr() for k in reads)
         wz_ptrs = L.u64_array(stack.WZ[_pair(k, s)].data_ptr() for k in reads)
         q_ptrs = L.u64_array(stack.bwd[k][1].data_ptr() for k in reads)
-        _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc), _p(dv), _p(dv_neg),
-                                     stack.n_tok, stack.d, _dtype_code(xc.dtype), _stream(xc.device))
+        _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc), _p(added), _p(dv),
+             _p(dv_neg), stack.n_tok, stack.d, _dtype_code(xc.dtype), _stream(xc.device))
         stack.assembled.add(s)
         for k in [k for k in stack.bwd if all(j in stack.assembled for j in range(k + 1))]:
             del stack.bwd[k]              # every update read by read k has its gradient: drop g_k
         if dv.shape == x.shape:
-            stack.neg[s] = (dv, dv_neg)   # the write's backward returns dv_neg for its x input
+            stack.neg[s] = (dv, dv_neg, added)   # the write's backward returns dv_neg for its x input
         ctx.stack = ctx.x = None          # release the stack from this node
         return None, None, dv.view(x.shape), None
 
@@ -576,6 +590,12 @@ class FusedCombineStk(torch.autograd.Function):
         ctx.stack, ctx.step, ctx.n, ctx.shape = stack, int(step), n, proposal.shape
         ctx.q_shape, ctx.q_dtype = query.shape, query.dtype
         ctx.beta, ctx.at_boundary, ctx.lam = float(beta), bool(at_boundary), lam
+        # the proposal is the write's h of this step and the newest scale comes from that update's scale node: the
+        # proposal's gradient then goes to the update's gradient kernel, which adds it (no separate add)
+        wr = stack.wh.get(step)
+        scale = srcs[n + step]
+        ctx.linked = (proposal.requires_grad and wr is not None and wr() is proposal and scale.grad_fn is not None
+                      and type(scale.grad_fn).__name__ == "_RstdStkBackward")
         ctx.mark_non_differentiable(next_prior)
         ctx.set_materialize_grads(False)
         return out, tc.view(*proposal.shape[:-1], n), next_prior
@@ -602,7 +622,11 @@ class FusedCombineStk(torch.autograd.Function):
         stack.bwd[step] = (g, qc)
         final = [i == step or (step == 1 and i == 0) for i in range(n)]
         dquery = stack.dQ.to(ctx.q_dtype) if step == 1 else None   # read 1's backward is the pass's last
-        grads = (None, None, dquery, g_prop if ctx.at_boundary else g, g_h0,
+        dprop = g_prop if ctx.at_boundary else g
+        if ctx.linked:
+            stack.gadd[step] = dprop
+            dprop = None
+        grads = (None, None, dquery, dprop, g_h0,
                  dcoeffs.view(*ctx.shape[:-1], n - 1), None, None, None,
                  *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
         ctx.stack = None

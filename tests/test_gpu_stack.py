@@ -96,6 +96,39 @@ def test_fused_glue_matches_torch_glue(monkeypatch, K, R, dtype, mode):
     assert worst <= tol, worst
 
 
+@pytest.mark.parametrize("K,R", [(3, 3), (1, 4)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_proposal_gradient_through_update_kernel(K, R, dtype):
+    """A fused combine whose proposal is the write's h hands the proposal's gradient to the update-gradient kernel,
+    which adds it as autograd would (round(round(dv) + g)); with the proposal a copy of h the same sum is formed by
+    autograd. Every gradient agrees bitwise, and no handed-over gradient is left behind."""
+    from loopback_amd.cell import LoopDeltaAttnRes
+    from loopback_amd.chain import make_inputs
+    cfg = chain_cfg(K, R, dtype)
+    h0c, Dc, Q, G = make_inputs(cfg, "cpu")
+    outs = []
+    for copy in (False, True):
+        cell = LoopDeltaAttnRes(cfg.d, cfg.R, cfg.K, beta=cfg.beta, eps=cfg.eps).to(DEV)
+        with torch.no_grad():
+            cell.query.copy_(Q.to(DEV))
+        h0 = h0c.to(DEV).requires_grad_()
+        D = [x.to(DEV).requires_grad_() for x in Dc]
+        stack = cell.new_stack(h0.shape, h0.dtype, h0.device, mode="scores")
+        h, deltas, keys, coeffs, prior = h0, [], [], None, None
+        for s in range(cfg.N):
+            l, blk = divmod(s, cfg.K)
+            hs = h + D[s]
+            deltas.append(stack.write(s, hs, h))
+            h, coeffs, prior = cell.combine(hs.clone() if copy else hs, h0, deltas, coeffs, prior, l, blk,
+                                            keys=keys, stack=stack)
+        (h.float() * G.to(DEV)).sum().backward()
+        torch.cuda.synchronize()
+        assert not stack.gadd and not stack.neg
+        outs.append([h0.grad.cpu(), cell.query.grad.cpu()] + [x.grad.cpu() for x in D])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 def test_stack_and_list_read_bitwise_on_shared_scales():
     """One read, both layouts, the same sources and the same scale tensors: the same kernels give the same bits."""
     from loopback_amd import fused_dattn as FD

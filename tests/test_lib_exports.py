@@ -83,7 +83,11 @@ def test_argument_checks_before_launch(lib):
                             16, 1e-6, 1, null) == -1
     assert L.ldr_split_queries(null, 8, ctypes.c_void_p(4096), null) == -1
     assert L.ldr_dv_assemble(too_many, too_many, too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), null,
-                             ctypes.c_void_p(4096), null, 16, 64, 1, null) == -2
+                             null, ctypes.c_void_p(4096), null, 16, 64, 1, null) == -2
+    # a misaligned added gradient
+    assert L.ldr_dv_assemble(one_src := lib.u64_array([4096]), one_src, one_src, 1, ctypes.c_void_p(4096),
+                             ctypes.c_void_p(4096), null, ctypes.c_void_p(4100), ctypes.c_void_p(4096), null, 16, 64,
+                             1, null) == -3
     # a blend needs both gradient outputs
     one = lib.u64_array([4096])
     p = ctypes.c_void_p(4096)
