@@ -94,8 +94,8 @@ int ldr_dots_online(const uint64_t* src_v, int64_t n, const float* q, float* out
  *   out = round(base + sum_i (tc_i - cbar_i) v_i)   (fp32 accumulation, one rounding)
  * (softmax as exp(l - max) / sum). With h0 != NULL (an iteration end, fused with looped_transformer.py:380-381) base
  * is the proposal and the read first forms round(base + round(beta * round(h0 - base))), the caller's own rounding
- * sequence. Stores tc [n_tok, n], the probabilities p [n_tok, n] for the backward, and c0 into next_prior [n] when
- * not NULL (the caller's next prior). Replaces _dattn_fwd_dots_kernel (fused_dattn.py:588-625, launched at 748-751)
+ * sequence. Stores tc [n_tok, n], the probabilities p [n_tok, n] for the backward (p may be NULL: a read without a
+ * backward), and c0 into next_prior [n] when not NULL (the caller's next prior). Replaces _dattn_fwd_dots_kernel (fused_dattn.py:588-625, launched at 748-751)
  * and the weighted-sum half of _dattn_fwd_stk_kernel / _dattn_fwd_kernel (410-456 / 55-108). */
 int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* dots, int64_t dots_stride,
                  const void* base, const void* h0, float beta, const float* cbar, int64_t cbar_cols, const float* c0,

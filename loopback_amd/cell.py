@@ -117,3 +117,26 @@ class LoopDeltaAttnRes(nn.Module):
             raise RuntimeError("delta_attnres: the HIP read does not take this layout (fused_read_supported is False)")
         out, target = FD.FusedDattnRead.apply(self.query[step - 1], base, base_coeffs, next_prior, *deltas, *R_list)
         return out, target, next_prior
+
+
+def remap_query(query: torch.Tensor, num_blocks: int, trained_loops: int, num_loops: int,
+                policy: str = "last") -> torch.Tensor:
+    """The read queries of a cell run for `num_loops` iterations, from one trained with `trained_loops`
+    (scripts/eval_extra_visits.py:43-63, the `loop_dattn.query` entry): read s uses row s - 1; reads the trained
+    cell had keep their row; a read past them takes, with policy "last", the row of the read at the same block
+    position in the last trained iteration ((trained_loops - 1) K + s mod K - 1, when that is a read), with "zero"
+    a zero row (its prior alone). Returns a new (num_blocks * num_loops - 1, d) tensor."""
+    K, R0, R = int(num_blocks), int(trained_loops), int(num_loops)
+    if policy not in ("last", "zero"):
+        raise ValueError(f"remap_query: policy must be 'last' or 'zero', got {policy!r}")
+    if query.dim() != 2 or query.shape[0] != K * R0 - 1:
+        raise ValueError(f"remap_query: query must be ({K * R0 - 1}, d), got {tuple(query.shape)}")
+    out = query.new_zeros((K * R - 1, query.shape[1]))
+    for s in range(1, K * R):
+        if s < K * R0:
+            out[s - 1] = query[s - 1]
+        elif policy == "last":
+            row = (R0 - 1) * K + s % K - 1
+            if row >= 0:
+                out[s - 1] = query[row]
+    return out

@@ -667,7 +667,7 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
           s_w[t * SP + i] = tcv - s_w[t * SP + i];
           if (tok < n_tok) {
             tc[tok * n + i] = tcv;
-            prob[tok * n + i] = ps[m];
+            if (prob) prob[tok * n + i] = ps[m];   // for the backward only
           }
         }
       }
@@ -1320,7 +1320,7 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
                  int64_t c0_cols, float lam, float inv_sqrt_d, void* out, float* tc, float* p, float* next_prior,
                  int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (!src_r || n_tok < 0 || !dots || dots_stride < n_tok || !base || !cbar || !c0 || !out || !tc || !p)
+  if (!src_r || n_tok < 0 || !dots || dots_stride < n_tok || !base || !cbar || !c0 || !out || !tc)
     return LDR_E_ARG;
   if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1)) return LDR_E_ARG;
   if (!al16(base) || !al16(out) || (h0 && !al16(h0))) return LDR_E_ALIGN;

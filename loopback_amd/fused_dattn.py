@@ -179,14 +179,16 @@ def _forward_impl(ctx, q, base, cbar, c0, srcs):
     base_c = base.detach().contiguous()
     out = torch.empty_like(base_c)
     tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
-    prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+    grad = any(ctx.needs_input_grad)      # else no backward: the probabilities are not stored
+    prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
     dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
     vp = L.u64_array(v.data_ptr() for v in values)
     rp = L.u64_array(r.data_ptr() for r in rstds)
     _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
     _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base_c), _p(None), 0.0, _p(cbar_c), n, _p(c0c), n, 1.0,
          _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
-    ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc, *values, *rstds)
+    if grad:
+        ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc, *values, *rstds)
     ctx.n, ctx.q_dtype, ctx.base_shape = n, q.dtype, base.shape
     return out, tc.view(*base.shape[:-1], n)
 
@@ -494,7 +496,8 @@ class FusedDattnReadStk(torch.autograd.Function):
             raise RuntimeError("delta_attnres stacked read: cbar must be (b, t, n) and c0 (n,)")
         out = torch.empty_like(base)
         tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
-        prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+        grad = any(ctx.needs_input_grad)
+        prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
         vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
         rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
         if stack.DOTS is not None and step >= 1 and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
@@ -504,7 +507,8 @@ class FusedDattnReadStk(torch.autograd.Function):
             _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
         _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base), _p(None), 0.0, _p(cbar_c), n, _p(c0c), n, 1.0,
              _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
-        ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc)
+        if grad:
+            ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc)
         ctx.stack, ctx.step, ctx.n, ctx.q_dtype, ctx.base_shape = stack, int(step), n, q.dtype, base.shape
         return out, tc.view(*base.shape[:-1], n)
 
@@ -574,7 +578,8 @@ class FusedCombineStk(torch.autograd.Function):
             raise RuntimeError("delta_attnres fused combine: coeffs must be (b, t, n-1) and prior (n-1,)")
         out = torch.empty_like(proposal)
         tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
-        prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
+        grad = any(ctx.needs_input_grad)      # else no backward: the probabilities are not stored
+        prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
         next_prior = torch.empty(n, device=dev, dtype=torch.float32)
         vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
         rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
@@ -586,7 +591,8 @@ class FusedCombineStk(torch.autograd.Function):
         _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(proposal), _p(h0 if at_boundary else None), float(beta),
              _p(coeffs_c), n - 1, _p(prior_c), n - 1, lam, _inv_sqrt(d), _p(out), _p(tc), _p(prob),
              _p(next_prior), n_tok, d, dt, st)
-        ctx.save_for_backward(qc, coeffs_c, prior_c, prob, dots, tc)
+        if grad:
+            ctx.save_for_backward(qc, coeffs_c, prior_c, prob, dots, tc)
         ctx.stack, ctx.step, ctx.n, ctx.shape = stack, int(step), n, proposal.shape
         ctx.q_shape, ctx.q_dtype = query.shape, query.dtype
         ctx.beta, ctx.at_boundary, ctx.lam = float(beta), bool(at_boundary), lam

@@ -7,7 +7,7 @@ against the oracle chain; mirrors tests/test_dattn_stack.py:68-199 of the refere
      further from the fp64 oracle than the reference read itself is (<= 2 err_ref + 2e-3); 'list' and 'stack' run
      the same read kernels (the stacked write forms the RMS scale itself, summed in another order, so they agree to
      fp32 round-off; bitwise when both take the scales from the same tensors);
-  2. eval (no grad) chains;
+  2. eval (no grad) chains, also with more iterations than trained (remapped queries);
   3. memory: a loss kept after its backward holds no stack.
 """
 import pytest
@@ -157,6 +157,23 @@ def test_eval_chains():
     hr, _ = ref_chain(cfg, None, grad=False)
     for h in (hl, hs, hw):
         assert err_norm(h, hr) <= 1e-2
+
+
+@pytest.mark.parametrize("policy", ["last", "zero"])
+def test_eval_extra_iterations(policy):
+    """Evaluation with more iterations than trained (scripts/eval_extra_visits.py): the queries remapped from a
+    2-iteration cell drive a 4-iteration no-grad chain (no probability stores) that matches the oracle chain run
+    with the same remapped queries."""
+    from loopback_amd.cell import remap_query
+    from loopback_amd.chain import make_inputs, run_chain
+    cfg = chain_cfg(2, 4, torch.bfloat16, backward=False)
+    h0, D, Q, G = make_inputs(cfg, "cpu")
+    Qr = remap_query(Q[:2 * 2 - 1], 2, 2, 4, policy)
+    for mode in ("scores", "stack", "list"):
+        h, _, _ = run_chain(cfg, h0.to(DEV), [x.to(DEV) for x in D], Qr.to(DEV), G.to(DEV), mode, grad=False)
+        torch.cuda.synchronize()
+        states, _, _, _, _ = oracle_chain(cfg.K, cfg.R, h0, D, Qr, G, beta=cfg.beta, eps=cfg.eps, grad=False)
+        assert err_norm(h.cpu(), states[-1]) <= 1e-2
 
 
 @pytest.mark.parametrize("mode", ["stack", "scores"])

@@ -92,3 +92,26 @@ def test_bench_refuses_several_gpus():
                          text=True, timeout=120)
     assert res.returncode != 0
     assert "one GPU" in (res.stdout + res.stderr)
+
+
+def test_remap_query_rows():
+    """Extra iterations at evaluation: trained reads keep their rows; a new read takes the row of the same block
+    position in the last trained iteration ('last') or a zero row ('zero'); R below the trained count truncates."""
+    import torch
+    from loopback_amd.cell import remap_query
+    K, R0 = 4, 2
+    q = torch.arange((K * R0 - 1) * 3, dtype=torch.float32).view(K * R0 - 1, 3)
+    last = remap_query(q, K, R0, 4, "last")
+    zero = remap_query(q, K, R0, 4, "zero")
+    assert last.shape == zero.shape == (K * 4 - 1, 3)
+    assert torch.equal(last[:K * R0 - 1], q) and torch.equal(zero[:K * R0 - 1], q)
+    for s in range(K * R0, K * 4):                      # destination read s uses row s - 1
+        assert torch.equal(last[s - 1], q[(R0 - 1) * K + s % K - 1])
+        assert not zero[s - 1].any()
+    # K = 1: the first new read's source row is the last trained read (row R0 - 1 - 1 + 0)
+    q1 = torch.randn(2, 5)
+    r1 = remap_query(q1, 1, 3, 5, "last")
+    assert torch.equal(r1[2], q1[1]) and torch.equal(r1[3], q1[1])
+    assert torch.equal(remap_query(q, K, R0, 1, "last"), q[:K - 1])
+    with pytest.raises(ValueError):
+        remap_query(q, K, R0, 4, "first")
