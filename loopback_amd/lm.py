@@ -78,7 +78,8 @@ CONFIG5 = LMConfig()   # d=768, 12 heads, SwiGLU 8/3 (2048), 
 
 class Rotary(nn.Module):
     """Non-interleaved RoPE: the two halves of each head rotate as pairs; cos / sin from fp32 positions and inverse
-    frequencies, cached in the activation dtype, the rotation computed in fp32 and rounded back."""
+    frequencies, rounded to the activation dtype (as the reference caches them), the rotation computed in fp32 and
+    rounded back. q and k rotate in one pass."""
 
     def __init__(self, head_dim: int, theta: float):
         super().__init__()
@@ -86,22 +87,25 @@ class Rotary(nn.Module):
         self._cache = None
 
     def tables(self, seq: int, device, dtype):
+        """Full-width fp32 (seq, head_dim) cos and sin (each half-table repeated), through `dtype`."""
         c = self._cache
-        if c is None or c[0] < seq or c[1].device != device or c[1].dtype != dtype:
+        if c is None or c[0] < seq or c[1].device != device or c[3] != dtype:
             inv = 1.0 / (self.theta ** (torch.arange(0, self.head_dim, 2, device=device, dtype=torch.float32)
                                         / self.head_dim))
             f = torch.outer(torch.arange(seq, device=device, dtype=torch.float32), inv)
-            self._cache = c = (seq, torch.cos(f).to(dtype), torch.sin(f).to(dtype))
+            cos = torch.cos(f).to(dtype).float()
+            sin = torch.sin(f).to(dtype).float()
+            self._cache = c = (seq, torch.cat((cos, cos), -1), torch.cat((sin, sin), -1), dtype)
         return c[1][:seq], c[2][:seq]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        """x: (B, H, T, D) -> rotated, same dtype."""
-        cos, sin = self.tables(x.shape[2], x.device, x.dtype)
-        cos = torch.cat((cos, cos), -1).float()
-        sin = torch.cat((sin, sin), -1).float()
+        """x: (B, T, ..., head_dim) -> rotated, same dtype."""
+        T, hd = x.shape[1], self.head_dim
+        cos, sin = self.tables(T, x.device, x.dtype)
+        shape = (1, T) + (1,) * (x.dim() - 3) + (hd,)
         xf = x.float()
-        x1, x2 = xf.chunk(2, dim=-1)
-        return (xf * cos + torch.cat((-x2, x1), -1) * sin).to(x.dtype)
+        rot = torch.cat((-xf[..., hd // 2:], xf[..., :hd // 2]), -1)
+        return (xf * cos.view(shape) + rot * sin.view(shape)).to(x.dtype)
 
 
 def attention_kernels(dtype):
@@ -123,8 +127,9 @@ class Attention(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         B, T, D = x.shape
-        q, k, v = self.qkv(x).view(B, T, 3, self.h, self.dh).permute(2, 0, 3, 1, 4).unbind(0)   # (B, H, T, dh)
-        q, k = self.rotary(q), self.rotary(k)
+        qkv = self.qkv(x).view(B, T, 3, self.h, self.dh)
+        q, k = self.rotary(qkv[:, :, :2]).permute(2, 0, 3, 1, 4).unbind(0)   # (B, H, T, dh) views
+        v = qkv[:, :, 2].transpose(1, 2)
         if x.is_cuda:
             with attention_kernels(x.dtype):
                 a = F.scaled_dot_product_attention(q, k, v.contiguous(), is_causal=True)

@@ -9,7 +9,8 @@ known size). Writes the markdown tables kept with the profiles and the per-launc
         --config c4 --mode scores --out profiles
 
 The passes are split at the one k_split_queries launch each chain pass starts with; the last complete pass of the
-trace and the last pass of each counter run are the ones summarized.
+trace and the last pass of each counter run are the ones summarized. `--stats-only NAME` summarizes the --stats
+output of any run (the LM step) into profiles/NAME.md.
 """
 from __future__ import annotations
 
@@ -83,19 +84,46 @@ def calibration(path, counter):
     return (COPY_BYTES / 1024) / kib
 
 
+def stats_table(path, top):
+    """rocprofv3's --stats kernel summary, the `top` kernels by total time, names shortened."""
+    st = sorted(_rows(path), key=lambda r: -float(r["TotalDurationNs"]))
+    total = sum(float(r["TotalDurationNs"]) for r in st)
+    lines = [f"rocprofv3 --stats over the whole run ({total / 1e6:.1f} ms of kernel time in all; names shortened):",
+             "", "| kernel | calls | total ms | average us | % |", "|---|---|---|---|---|"]
+    for r in st[:top]:
+        name = r["Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:80]
+        lines.append(f"| `{name}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.2f} | "
+                     f"{float(r['AverageNs']) / 1e3:.1f} | {r['Percentage']} |")
+    return lines
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("--trace", required=True)
+    ap.add_argument("--trace", default=None)
     ap.add_argument("--stats", default=None, help="the --stats kernel summary of the same trace run")
-    ap.add_argument("--fetch", required=True)
-    ap.add_argument("--write", required=True)
-    ap.add_argument("--calib-fetch", required=True)
-    ap.add_argument("--calib-write", required=True)
+    ap.add_argument("--fetch", default=None)
+    ap.add_argument("--write", default=None)
+    ap.add_argument("--calib-fetch", default=None)
+    ap.add_argument("--calib-write", default=None)
+    ap.add_argument("--stats-only", default=None, metavar="NAME",
+                    help="write only the --stats table, as profiles/NAME.md (any program, e.g. the LM step)")
+    ap.add_argument("--title", default="", help="heading of a --stats-only summary")
     ap.add_argument("--config", default="c4")
     ap.add_argument("--mode", default="scores")
     ap.add_argument("--out", default="profiles")
     ap.add_argument("--commands", default="", help="the commands that produced the inputs (quoted into the summaries)")
     a = ap.parse_args(argv)
+    if a.stats_only:
+        lines = [f"# {a.title or a.stats_only}", ""]
+        if a.commands:
+            lines += ["Commands:", "", *["    " + c for c in a.commands.split(";;")], ""]
+        lines += stats_table(a.stats, 20)
+        with open(os.path.join(a.out, f"{a.stats_only}.md"), "w") as f:
+            f.write("\n".join(lines) + "\n")
+        return
+    for need in ("trace", "fetch", "write", "calib_fetch", "calib_write"):
+        if getattr(a, need) is None:
+            ap.error(f"--{need.replace('_', '-')} is required")
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     sys.path.insert(0, root)
@@ -124,13 +152,7 @@ def main(argv=None):
         lines.append(f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | "
                      f"{ab / 1e9:.2f} | {gbs} |" if ab else f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | - | - |")
     if a.stats:   # rocprofv3's own per-kernel summary over the whole run (warm-up and timed passes)
-        st = sorted(_rows(a.stats), key=lambda r: -float(r["TotalDurationNs"]))[:12]
-        lines += ["", "rocprofv3 --stats over the whole run (all passes; names shortened):", "",
-                  "| kernel | calls | total ms | average us | % |", "|---|---|---|---|---|"]
-        for r in st:
-            name = r["Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:80]
-            lines.append(f"| `{name}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.2f} | "
-                         f"{float(r['AverageNs']) / 1e3:.1f} | {r['Percentage']} |")
+        lines += [""] + stats_table(a.stats, 12)
     with open(os.path.join(a.out, f"kernels_chain_{a.config}.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
 
