@@ -46,6 +46,12 @@
 #ifndef LDR_B1_WAVE_ROWS
 #define LDR_B1_WAVE_ROWS 1   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
+#ifndef LDR_B1_GPACK
+#define LDR_B1_GPACK 1       // backward pass 1: keep g packed in registers, unpacked where used
+#endif
+#ifndef LDR_B1_PIPE
+#define LDR_B1_PIPE 1        // backward pass 1: the next chunk's loads in flight while one is reduced
+#endif
 #ifndef LDR_NT
 #define LDR_NT 1             // non-temporal loads for the streamed sources
 #endif
@@ -811,6 +817,15 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
       const int64_t tok = t0 + rr;
       const bool valid = tok < n_tok;
       const int64_t roff = (valid ? tok : n_tok - 1) * (int64_t)d;
+#if LDR_B1_GPACK
+      typename IO<T>::Raw gq[VPT];   // g kept packed, unpacked where used
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        gq[v] = IO<T>::raw_nt(g + roff + R.off(v));
+        if (!R.act(v)) gq[v] = IO<T>::zero();
+      }
+#define LDR_GV(v, arr) float arr[8]; IO<T>::unpack(gq[v], arr);
+#else
       float gv[VPT][8];
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
@@ -820,16 +835,19 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
           for (int k = 0; k < 8; ++k) gv[v][k] = 0.f;
         }
       }
+#define LDR_GV(v, arr) const float (&arr)[8] = gv[v];
+#endif
       if (g_prop && valid) {   // the blend's gradients: beta g to h0, g - beta g to the proposal (rounded as autograd)
 #pragma clang fp contract(off)   // a product and a difference, each rounded (no fused multiply-add)
 #pragma unroll
         for (int v = 0; v < VPT; ++v) {
           if (!R.act(v)) continue;
           float gb[8], gpv[8];
+          LDR_GV(v, gvv)
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
-            gb[k] = IO<T>::round(beta * gv[v][k]);
-            gpv[k] = gv[v][k] - gb[k];
+            gb[k] = IO<T>::round(beta * gvv[k]);
+            gpv[k] = gvv[k] - gb[k];
           }
           IO<T>::store(g_h0 + roff + R.c8(v) * 8, gb);
           IO<T>::store(g_prop + roff + R.c8(v) * 8, gpv);
@@ -862,43 +880,64 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
         }
         if (R.lr == 0) s_gd[rr * SP + i] = gd;
       };
-      int i0 = 0;
-      for (; i0 + C <= n; i0 += C) {
-        typename IO<T>::Raw raw[C][VPT];
+      auto dotc = [&](const typename IO<T>::Raw (&rw)[VPT]) {
+        float acc = 0.f;
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          float e[8];
+          IO<T>::unpack(rw[v], e);
+          LDR_GV(v, gvv)
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc += gvv[k] * e[k];
+        }
+        return acc;
+      };
+      auto load_chunk = [&](int i0, typename IO<T>::Raw (&rw)[C][VPT]) {
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
-          for (int v = 0; v < VPT; ++v) raw[c][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0 + c]) + roff + R.off(v));
+          for (int v = 0; v < VPT; ++v) rw[c][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0 + c]) + roff + R.off(v));
+      };
+      int i0 = 0;
+#if LDR_B1_PIPE
+      const int nfull = n - n % C;
+      typename IO<T>::Raw cur[C][VPT];
+      if (nfull > 0) load_chunk(0, cur);
+      for (; i0 < nfull; i0 += C) {   // the next chunk's loads in flight while this one is reduced
+        typename IO<T>::Raw nxt[C][VPT];
+        if (i0 + C < nfull) load_chunk(i0 + C, nxt);
         float pd[C];
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-          pd[c] = 0.f;
+        for (int c = 0; c < C; ++c) pd[c] = dotc(cur[c]);
+        row_sum<C>(pd, tpr, red);
+        if (valid) {
 #pragma unroll
-          for (int v = 0; v < VPT; ++v) {
-            float e[8];
-            IO<T>::unpack(raw[c][v], e);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) pd[c] += gv[v][k] * e[k];
-          }
+          for (int c = 0; c < C; ++c) take(i0 + c, pd[c], cur[c]);
         }
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) cur[c][v] = nxt[c][v];
+      }
+#else
+      for (; i0 + C <= n; i0 += C) {
+        typename IO<T>::Raw raw[C][VPT];
+        load_chunk(i0, raw);
+        float pd[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) pd[c] = dotc(raw[c]);
         row_sum<C>(pd, tpr, red);
         if (valid) {
 #pragma unroll
           for (int c = 0; c < C; ++c) take(i0 + c, pd[c], raw[c]);
         }
       }
+#endif
       for (; i0 < n; ++i0) {
         typename IO<T>::Raw raw[1][VPT];
 #pragma unroll
         for (int v = 0; v < VPT; ++v) raw[0][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0]) + roff + R.off(v));
-        float pd[1] = {0.f};
-#pragma unroll
-        for (int v = 0; v < VPT; ++v) {
-          float e[8];
-          IO<T>::unpack(raw[0][v], e);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) pd[0] += gv[v][k] * e[k];
-        }
+        float pd[1] = {dotc(raw[0])};
         row_sum<1>(pd, tpr, red);
         if (valid) take(i0, pd[0], raw[0]);
       }
@@ -1188,7 +1227,7 @@ int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n) {
 
 template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
 // backward pass 1: sources per row reduction (one LDS exchange per chunk when a row spans two waves)
-template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_B1_C : (VPT == 1 ? 8 : VPT == 2 ? 4 : 2); };
+template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_B1_C : (VPT == 1 ? 8 : VPT == 2 ? 4 : 1); };
 
 }  // namespace
 
