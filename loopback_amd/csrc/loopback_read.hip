@@ -1476,6 +1476,7 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
     if (j < m && (!al16(t.g[j]) || !al16(t.q[j]) || (reinterpret_cast<uintptr_t>(t.wz[j]) & 7u))) return LDR_E_ALIGN;
   }
   int vpt, tpr, e = row_layout(d, &vpt, &tpr, LDR_AS_MAX_VPT, false, LDR_AS_VPT, true);
+  if (e == LDR_E_SHAPE && !LDR_AS_VPT) e = row_layout(d, &vpt, &tpr, 4, false, 0, true);   // rows past 3 x 256 x 8
   if (e) return e;
   if (n_tok == 0) return LDR_OK;
   const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * as_rb(vpt)), 65535);

@@ -11,7 +11,8 @@ LoopDeltaAttnRes.combine -- on the same seeded inputs; mirrors tests/test_fused_
      than the reference read's own bf16 error (<= 2 err_ref + 2e-3) -- dproposal / dh0 come from the caller's
      bf16 torch glue, the same ops as the reference's; against the bf16 reference read itself (whose gradients
      round every per-source term to bf16): norm-relative <= 1e-2 for outputs and all gradients;
-  3. zero query, cbar == prior: out == base and tc == c0 bitwise, fp32 and bf16.
+  3. zero query, cbar == prior: out == base and tc == c0 bitwise, fp32 and bf16;
+  4. the layout's extremes in fp32: one token, d = 8, 40, 2056, 8192, 64 sources.
 """
 import pytest
 import torch
@@ -82,6 +83,19 @@ def test_fp32_matches_reference_read(b, t, d, n, boundary):
     e32 = compare(hip, ref, err_rms)
     assert max(e64.values()) <= 1e-5, e64
     assert max(e32.values()) <= 2e-5, e32
+
+
+@pytest.mark.parametrize("b,t,d,n", [(1, 1, 8, 2), (1, 3, 40, 5), (1, 17, 8192, 3), (2, 5, 64, 64), (1, 33, 2056, 7)])
+@pytest.mark.parametrize("boundary", [False, True])
+def test_fp32_edge_shapes(b, t, d, n, boundary):
+    """The extremes of the layout: one token, the narrowest row (d = 8), rows that are no power of two of vectors
+    (d = 40, 2056), the widest row (d = 8192: 256 lanes x 4 vectors), the most sources a read takes (64)."""
+    args = make(b, t, d, n, torch.float32, seed=31 * n + d + int(boundary))
+    print(f"case fp32 edge b{b} t{t} d{d} n{n} boundary={boundary}", flush=True)
+    hip = run_hip(d, n, args, boundary)
+    ref64 = run_oracle(d, n, args, boundary, dtype=torch.float64)
+    e64 = compare(hip, ref64, err_rms)
+    assert max(e64.values()) <= 1e-5, e64
 
 
 @pytest.mark.parametrize("b,t,d", [(2, 256, 1024), (2, 128, 1536), (4, 128, 768)])

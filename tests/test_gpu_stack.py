@@ -64,6 +64,21 @@ def test_chain_matches_oracle(K, R, dtype, mode):
             assert err_norm(a, c) <= 2 * err_norm(b, c) + 2e-3
 
 
+@pytest.mark.parametrize("K,R,d,t", [(8, 8, 64, 33), (2, 2, 8192, 20), (1, 3, 8, 5)])
+def test_stack_extremes_match_oracle(K, R, d, t):
+    """The stacked layout at its limits in fp32: 64 steps (the most a stack holds; reads of up to 64 sources),
+    the widest row, the narrowest row with one token per tile row."""
+    from loopback_amd.chain import ChainConfig
+    cfg = ChainConfig(f"edge-K{K}R{R}d{d}", d, K, R, 1, t, torch.float32, True, q_std=0.5)
+    print(f"case stack edge K{K} R{R} d{d} t{t}", flush=True)
+    for mode in ("scores", "stack"):
+        h, g = hip_chain(cfg, mode)
+        hr, gr = ref_chain(cfg, torch.float64)
+        assert err_norm(h, hr) <= 1e-5
+        worst = max(err_norm(a, b) for a, b in zip(grad_list(g), grad_list(gr)))
+        assert worst <= 1e-5, (mode, worst)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_layouts_agree(dtype):
     cfg = chain_cfg(3, 3, dtype)

@@ -100,5 +100,11 @@ def test_argument_checks_before_launch(lib):
     two = lib.u64_array([4096, 4096])
     assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 3, p, 2, 1.0, 0.125, p, p, p, null, 16, 64, 1,
                           null) == -1
+    # the widest row (8192) is a shape every stacked entry point takes (no tokens: checked, nothing launched)
+    assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, p, null, 0, 8192, 1, null) == 0
+    assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.01, p, p, p, null, 0, 8192, 1,
+                          null) == 0
+    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.01, p, 1, one, 0, p, 16, p, null,
+                           null, 0.0, 0, 8192, 1, null) == 0
     # zero tokens: accepted, nothing launched
     assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 0, 64, 1e-6, 1, null) == 0
