@@ -89,9 +89,10 @@ def family_bytes(cfg, mode):
     write 3 rows per token (h, x in; V out), read (n+2) (n sources, base in; out), scores online n, backward pass 1
     (n+1) (n sources, g), update gradient (m+3) (the m output gradients of the reads holding the update, the update,
     the result and its negation for the write's x) -- in rows of e * d bytes; per-(token, source) fp32 scalars left
-    out (< 1 %). With the caller's glue in the stacked read, a read at an iteration end also reads h0 and its
-    backward pass 1 writes the blend's two gradients, and the update gradient of each update a read took as its
-    proposal also reads that read's proposal gradient (the add autograd would otherwise run).
+    out (< 1 %). With the caller's glue in the stacked read, a read at an iteration end also reads h0, the update
+    gradient of each update a read took as its proposal also reads that read's output gradient (and adds the
+    proposal's share, the add autograd would otherwise run), and the iteration ends' shares of h0's gradient are
+    summed once (blend_sum: one output gradient per iteration end in, one row out).
     Also the reference dataflow's total (the formula of the survey), which moves more in its backward."""
     from loopback_amd.cell import fuse_glue
     from loopback_amd.chain import algorithmic_bytes_per_token
@@ -105,8 +106,10 @@ def family_bytes(cfg, mode):
     if mode != "scores":
         fam["dots_online"] = S2 * row
     if cfg.backward:
-        fam["read_bwd1"] = (S2 + N - 1 + 2 * ends) * row
+        fam["read_bwd1"] = (S2 + N - 1) * row
         fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 3 * N + (N - 1 if fused else 0)) * row
+        if ends:
+            fam["blend_sum"] = (ends + 1) * row
     ref_total = algorithmic_bytes_per_token(N, cfg.d, e, backward=cfg.backward, dots=(mode == "scores"))["total"] * T
     return fam, ref_total
 

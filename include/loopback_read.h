@@ -110,7 +110,7 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
  *   dr_i[tok] (+)= dz_i dots_i inv_sqrt_d   (= dz_i z_i / r_i; added when dr_accum != 0)
  *   wz[(i * wz_stride + tok) * 2 + {0,1}] = (tc_i - cbar_i, dz_i r_i inv_sqrt_d)   (the pass-2 scalars)
  *   dq_part[p, :] = per-workgroup partial of sum_tok sum_i dz_i r_i v_i inv_sqrt_d  (ldr_read_bwd1_parts rows)
- *   with g_prop / g_h0 (both or neither): the iteration-end blend's gradients g_h0 = round(beta g),
+ *   with g_prop and / or g_h0 (each may be NULL): the iteration-end blend's gradients g_h0 = round(beta g),
  *     g_prop = round(g - g_h0), rounded as autograd rounds them
  * Replaces _dattn_bwd1_stk_kernel (fused_dattn.py:459-493, launched at 777-779) and pass 1 of _dattn_bwd_kernel
  * (111-151); dr is also the dR update of _dattn_bwd2_stk_kernel (532-535). */
@@ -136,13 +136,21 @@ int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, 
  * over the m reads e that hold update i: g_e that read's output gradient, (w_e, dzr_e) its wz pair for source i
  * (float2 per token), q_e its query (fp32, d). One fp32 sum, one rounding; gr may be NULL (no scale gradient).
  * dv_neg (may be NULL) receives -dv, the write's gradient to x (fused_dattn.py:694-695). With add != NULL (another
- * gradient of the write's h, e.g. the read that took h as its proposal) dv holds round(dv + add) instead, the sum
- * autograd would form; dv_neg stays -dv.
+ * gradient of the write's h, e.g. the read that took h as its proposal) dv holds round(dv + a) instead, the sum
+ * autograd would form, with a = add, or, when add_beta != 0 (add being the output gradient g of a read whose base
+ * was the iteration-end blend), the blend's share of it a = round(add - round(add_beta * add)); dv_neg stays -dv.
  * Replaces the dV read-modify-write of _dattn_bwd2_stk_kernel (fused_dattn.py:496-536, launched at 781-784) and
  * _rstd_bwd_acc_kernel (539-552, launched at 717-719). */
 int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                    const float* r, const float* gr, const void* add, void* dv, void* dv_neg, int64_t n_tok, int64_t d,
-                    int dtype, void* stream);
+                    const float* r, const float* gr, const void* add, float add_beta, void* dv, void* dv_neg,
+                    int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* out = round( sum_j round(beta * g_j) ) over m update-shaped tensors (fp32 sum): the gradient of h0 from the m
+ * iteration-end blends of a pass (looped_transformer.py:380-381, base = proposal + beta (h0 - proposal)), formed
+ * once from the reads' output gradients instead of one tensor per blend added up by autograd. No reference
+ * counterpart (the reference leaves these adds to autograd). */
+int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
+                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -837,8 +837,8 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
       }
 #define LDR_GV(v, arr) const float (&arr)[8] = gv[v];
 #endif
-      if (g_prop && valid) {   // the blend's gradients: beta g to h0, g - beta g to the proposal (rounded as autograd)
-#pragma clang fp contract(off)   // a product and a difference, each rounded (no fused multiply-add)
+      if ((g_prop || g_h0) && valid) {   // the blend's gradients: beta g to h0, g - beta g to the proposal
+#pragma clang fp contract(off)   // a product and a difference, each rounded as autograd rounds them (no fma)
 #pragma unroll
         for (int v = 0; v < VPT; ++v) {
           if (!R.act(v)) continue;
@@ -849,8 +849,8 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
             gb[k] = IO<T>::round(beta * gvv[k]);
             gpv[k] = gvv[k] - gb[k];
           }
-          IO<T>::store(g_h0 + roff + R.c8(v) * 8, gb);
-          IO<T>::store(g_prop + roff + R.c8(v) * 8, gpv);
+          if (g_h0) IO<T>::store(g_h0 + roff + R.c8(v) * 8, gb);
+          if (g_prop) IO<T>::store(g_prop + roff + R.c8(v) * 8, gpv);
         }
       }
       // dq of the row is sum_i p_i r_i (gp_i - Sacc) v_i: the gp part goes straight into the running dq, the
@@ -999,6 +999,38 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
 }
 
 // out[c] = sum_p part[p][c]: 16 columns per workgroup, 16 row groups (rows p = group mod 16) added in a fixed order
+// out = round(sum_j round(beta * g_j)): the iteration-end blends' shares of h0's gradient, summed once in fp32
+template <typename T, int VPT>
+__global__ __launch_bounds__(WG) void k_blend_sum(PtrTab g, int m, float beta, T* __restrict__ out, int64_t n_tok,
+                                                  int d, int tpr) {
+#pragma clang fp contract(off)
+  const Rows R(d, tpr);
+  const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
+  for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
+    const int64_t tok = gi * R.rpw + R.rs;
+    const int64_t roff = (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
+    float acc[VPT][8];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v)
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[v][x] = 0.f;
+    for (int j = 0; j < m; ++j) {
+      float e[VPT][8];
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) IO<T>::unpack(IO<T>::raw_nt(static_cast<const T*>(g.p[j]) + roff + R.off(v)), e[v]);
+#pragma unroll
+      for (int v = 0; v < VPT; ++v)
+#pragma unroll
+        for (int x = 0; x < 8; ++x) acc[v][x] += IO<T>::round(beta * e[v][x]);
+    }
+    if (tok < n_tok) {
+#pragma unroll
+      for (int v = 0; v < VPT; ++v)
+        if (R.act(v)) IO<T>::store(out + roff + R.c8(v) * 8, acc[v]);
+    }
+  }
+}
+
 __global__ __launch_bounds__(WG) void k_reduce_rows(const float* __restrict__ part, int64_t rows, int d,
                                                     float* __restrict__ out) {
   __shared__ float s[WG];
@@ -1077,8 +1109,8 @@ constexpr int AS_JB = LDR_AS_JB;   // reads per batch of loads
 template <typename T, int VPT>
 __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* __restrict__ vsrc,
                                                     const float* __restrict__ r, const float* __restrict__ gr,
-                                                    const T* __restrict__ add, T* __restrict__ dv,
-                                                    T* __restrict__ dv_neg, int64_t n_tok, int d,
+                                                    const T* __restrict__ add, float add_beta,
+                                                    T* __restrict__ dv, T* __restrict__ dv_neg, int64_t n_tok, int d,
                                                     int tpr) {
   constexpr int AS_RB = as_rb(VPT);
   const Rows R(d, tpr);
@@ -1142,6 +1174,13 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
       if (add) {   // a gradient of the write's h from elsewhere, added as autograd would add it
 #pragma unroll
         for (int v = 0; v < VPT; ++v) IO<T>::load(add + roff[k] + R.off(v), a[v]);
+        if (add_beta != 0.f) {   // add is the output gradient g of an iteration-end blend: its proposal's share
+#pragma clang fp contract(off)
+#pragma unroll
+          for (int v = 0; v < VPT; ++v)
+#pragma unroll
+            for (int x = 0; x < 8; ++x) a[v][x] = IO<T>::round(a[v][x] - IO<T>::round(add_beta * a[v][x]));
+        }
       }
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
@@ -1236,7 +1275,7 @@ template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 5; }
+int ldr_abi_version(void) { return 6; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -1399,12 +1438,12 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (!src_r || n_tok < 0 || !g || !p || !dots || dots_stride < n_tok || !tc || !cbar || !c0 || !dcbar || !dr ||
       !wz || !dq_part ||
-      wz_stride < n_tok || (dr_accum != 0 && dr_accum != 1) || (!g_prop) != (!g_h0))
+      wz_stride < n_tok || (dr_accum != 0 && dr_accum != 1))
     return LDR_E_ARG;
   if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1) || dcbar_cols < 0 ||
       dcbar_cols > n)
     return LDR_E_ARG;
-  if (!al16(g) || (g_prop && (!al16(g_prop) || !al16(g_h0)))) return LDR_E_ALIGN;
+  if (!al16(g) || (g_prop && !al16(g_prop)) || (g_h0 && !al16(g_h0))) return LDR_E_ALIGN;
   SrcTab s;
   int e = fill_src(s, src_v, src_r, n);
   if (e) return e;
@@ -1438,6 +1477,29 @@ int ldr_reduce_rows(const float* part, int64_t rows, int64_t d, float* out, void
   return launched();
 }
 
+int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
+                  void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (m < 1 || m > MAXS) return LDR_E_SHAPE;
+  if (!g || !out || n_tok < 0) return LDR_E_ARG;
+  if (!al16(out)) return LDR_E_ALIGN;
+  PtrTab t;
+  for (int64_t j = 0; j < MAXS; ++j) {
+    t.p[j] = j < m ? reinterpret_cast<void*>(g[j]) : nullptr;
+    if (j < m && !t.p[j]) return LDR_E_ARG;
+    if (j < m && !al16(t.p[j])) return LDR_E_ALIGN;
+  }
+  int vpt, tpr, e = row_layout(d, &vpt, &tpr);
+  if (e) return e;
+  if (n_tok == 0) return LDR_OK;
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 4096);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_blend_sum<T, VPT>), dim3(grid), dim3(WG), 0, st,
+                                                                  t, (int)m, beta, static_cast<T*>(out), n_tok,
+                                                                  (int)d, tpr)))
+  return launched();
+}
+
 int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, const float* q, const float* wz,
                        int64_t wz_stride, int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
@@ -1461,8 +1523,8 @@ int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, 
 }
 
 int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                    const float* r, const float* gr, const void* add, void* dv, void* dv_neg, int64_t n_tok, int64_t d,
-                    int dtype, void* stream) {
+                    const float* r, const float* gr, const void* add, float add_beta, void* dv, void* dv_neg,
+                    int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (m < 0 || m > MAXS) return LDR_E_SHAPE;
   if ((m > 0 && (!g || !wz || !q)) || !v || !r || !dv || n_tok < 0) return LDR_E_ARG;
@@ -1483,7 +1545,8 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT>), dim3(grid), dim3(WG), 0, st,
                                                                   t, (int)m, static_cast<const T*>(v), r, gr,
-                                                                  static_cast<const T*>(add), static_cast<T*>(dv),
+                                                                  static_cast<const T*>(add), add_beta,
+                                                                  static_cast<T*>(dv),
                                                                   static_cast<T*>(dv_neg), n_tok,
                                                                   (int)d, tpr)))
   return launched();

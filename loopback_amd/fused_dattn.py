@@ -328,7 +328,7 @@ class DattnStack:
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
     transposed operand for its tensor-core product; the HIP write reads Q directly)."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
-                 "assembled", "neg", "dQ", "wh", "gadd")
+                 "assembled", "neg", "dQ", "wh", "gadd", "h0_ref", "h0_steps", "h0_g")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
@@ -349,7 +349,10 @@ class DattnStack:
         self.neg = {}         # s -> (gradient of update s, its negation), handed from _RstdStk to _WriteDelta
         self.dQ = None        # the query gradient rows of the fused combines' backwards (fp32)
         self.wh = {}          # s -> weak reference to the write's h (a fused combine that takes it as its proposal
-        self.gadd = {}        # hands its proposal gradient, gadd[s], to the update's gradient kernel)
+        self.gadd = {}        # hands its proposal gradient, gadd[s] = (g, beta), to the update's gradient kernel)
+        self.h0_ref = None    # the fused iteration-end reads: a weak reference to their h0, their steps, and the
+        self.h0_steps = []    # output gradients {step: g} of those whose backward ran -- h0's gradient from the
+        self.h0_g = {}        # blends is summed once, by the first of them (the last to run backward)
         self.eps = float(eps)
         self.r_done = [False] * self.n_steps      # R[s] (and the scores of update s) written by the write of s
         self.Q = self.QT = self.QB = self.DOTS = None
@@ -381,6 +384,14 @@ class DattnStack:
             self.WZ = torch.empty((max(1, pairs), self.n_tok, 2), dtype=torch.float32, device=self.V.device)
             return False
         return True
+
+
+def _proposal_grad(added):
+    """The proposal gradient a fused combine handed over as (g, beta): g itself, or for an iteration-end blend its
+    share round(g - round(beta g)) -- the value the update-gradient kernel adds (torch ops, for the rare paths where
+    that kernel did not take it)."""
+    g, beta = added
+    return g - (g * beta).to(g.dtype) if beta else g
 
 
 class _WriteDelta(torch.autograd.Function):
@@ -427,8 +438,8 @@ class _WriteDelta(torch.autograd.Function):
                     and g.dtype == dh.dtype):
                 return None, None, g, dx
             # other consumers of the update added to its gradient: h takes all of it, x all but the proposal's
-            return None, None, g, -(g - added) if added is not None else -g
-        return None, None, (g if left is None else g + left), -g
+            return None, None, g, -(g - _proposal_grad(added)) if added is not None else -g
+        return None, None, (g if left is None else g + _proposal_grad(left)), -g
 
 
 class _RstdStk(torch.autograd.Function):
@@ -457,13 +468,15 @@ class _RstdStk(torch.autograd.Function):
         dv = torch.empty_like(xc)
         dv_neg = torch.empty_like(xc)
         grc = None if gr is None else gr.float().contiguous()
-        added = stack.gadd.pop(s, None)       # the gradient of the write's h from the combine that took it
-        if added is not None and (added.shape != x.shape or added.dtype != xc.dtype or not added.is_contiguous()):
-            added = added.to(xc.dtype).contiguous().view(x.shape)
+        added = stack.gadd.pop(s, None)       # (g, beta): the combine that took the write's h as its proposal
+        if added is not None and (added[0].shape != x.shape or added[0].dtype != xc.dtype
+                                  or not added[0].is_contiguous()):
+            added = (added[0].to(xc.dtype).contiguous().view(x.shape), added[1])
         g_ptrs = L.u64_array(stack.bwd[k][0].data_ptr() for k in reads)
         wz_ptrs = L.u64_array(stack.WZ[_pair(k, s)].data_ptr() for k in reads)
         q_ptrs = L.u64_array(stack.bwd[k][1].data_ptr() for k in reads)
-        _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc), _p(added), _p(dv),
+        _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc),
+             _p(None if added is None else added[0]), 0.0 if added is None else float(added[1]), _p(dv),
              _p(dv_neg), stack.n_tok, stack.d, _dtype_code(xc.dtype), _stream(xc.device))
         stack.assembled.add(s)
         for k in [k for k in stack.bwd if all(j in stack.assembled for j in range(k + 1))]:
@@ -602,6 +615,13 @@ class FusedCombineStk(torch.autograd.Function):
         scale = srcs[n + step]
         ctx.linked = (proposal.requires_grad and wr is not None and wr() is proposal and scale.grad_fn is not None
                       and type(scale.grad_fn).__name__ == "_RstdStkBackward")
+        # an iteration end with the pass's h0: its share of h0's gradient is summed with the other ends' at the
+        # first of them (the last to run backward) instead of being written here and added by autograd
+        ctx.h0_sum = False
+        if at_boundary and h0.requires_grad and (stack.h0_ref is None or stack.h0_ref() is h0):
+            stack.h0_ref = weakref.ref(h0)
+            stack.h0_steps.append(int(step))
+            ctx.h0_sum = True
         ctx.mark_non_differentiable(next_prior)
         ctx.set_materialize_grads(False)
         return out, tc.view(*proposal.shape[:-1], n), next_prior
@@ -615,9 +635,9 @@ class FusedCombineStk(torch.autograd.Function):
         if stack.dQ is None or stack.dQ.shape != ctx.q_shape:
             stack.dQ = torch.zeros(ctx.q_shape, device=dev, dtype=torch.float32)
         g = torch.zeros(ctx.shape, device=dev, dtype=stack.V.dtype) if g is None else g.to(stack.V.dtype).contiguous()
-        g_prop = g_h0 = None
-        if ctx.at_boundary:
-            g_prop, g_h0 = torch.empty_like(g), torch.empty_like(g)
+        # the blend's gradients are written only where no later kernel forms them from g
+        g_prop = torch.empty_like(g) if ctx.at_boundary and not ctx.linked else None
+        g_h0 = torch.empty_like(g) if ctx.at_boundary and not ctx.h0_sum else None
         vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
         rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
         drp = L.u64_array(stack.dR[i].data_ptr() for i in range(n))
@@ -630,9 +650,19 @@ class FusedCombineStk(torch.autograd.Function):
         dquery = stack.dQ.to(ctx.q_dtype) if step == 1 else None   # read 1's backward is the pass's last
         dprop = g_prop if ctx.at_boundary else g
         if ctx.linked:
-            stack.gadd[step] = dprop
+            stack.gadd[step] = (g, ctx.beta if ctx.at_boundary else 0.0)
             dprop = None
-        grads = (None, None, dquery, dprop, g_h0,
+        dh0 = g_h0
+        if ctx.h0_sum:
+            stack.h0_g[step] = g
+            if step == min(stack.h0_steps):   # every other iteration end ran its backward: their sum, once
+                gs = [stack.h0_g[k] for k in sorted(stack.h0_g)]
+                dh0 = torch.empty_like(g)
+                _run("blend_sum", L.u64_array(x.data_ptr() for x in gs), len(gs), ctx.beta, _p(dh0), n_tok, d,
+                     _dtype_code(stack.V.dtype), _stream(dev))
+                stack.h0_g, stack.h0_steps = {}, []
+                dh0 = dh0.view(ctx.shape)
+        grads = (None, None, dquery, dprop, dh0,
                  dcoeffs.view(*ctx.shape[:-1], n - 1), None, None, None,
                  *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
         ctx.stack = None

@@ -83,16 +83,18 @@ def test_argument_checks_before_launch(lib):
                             16, 1e-6, 1, null) == -1
     assert L.ldr_split_queries(null, 8, ctypes.c_void_p(4096), null) == -1
     assert L.ldr_dv_assemble(too_many, too_many, too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), null,
-                             null, ctypes.c_void_p(4096), null, 16, 64, 1, null) == -2
+                             null, 0.0, ctypes.c_void_p(4096), null, 16, 64, 1, null) == -2
     # a misaligned added gradient
     assert L.ldr_dv_assemble(one_src := lib.u64_array([4096]), one_src, one_src, 1, ctypes.c_void_p(4096),
-                             ctypes.c_void_p(4096), null, ctypes.c_void_p(4100), ctypes.c_void_p(4096), null, 16, 64,
-                             1, null) == -3
-    # a blend needs both gradient outputs
+                             ctypes.c_void_p(4096), null, ctypes.c_void_p(4100), 0.0, ctypes.c_void_p(4096), null, 16,
+                             64, 1, null) == -3
+    # a misaligned blend-gradient output
     one = lib.u64_array([4096])
     p = ctypes.c_void_p(4096)
-    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, p,
-                           null, 0.5, 16, 64, 1, null) == -1
+    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p,
+                           ctypes.c_void_p(4104), null, 0.5, 16, 64, 1, null) == -3
+    assert L.ldr_blend_sum(too_many, 65, 0.5, p, 16, 64, 1, null) == -2
+    assert L.ldr_blend_sum(one, 1, 0.5, ctypes.c_void_p(4100), 16, 64, 1, null) == -3
     # the raw scores' row stride covers the tokens
     assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 8, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, null,
                            null, 0.0, 16, 64, 1, null) == -1
@@ -101,7 +103,8 @@ def test_argument_checks_before_launch(lib):
     assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 3, p, 2, 1.0, 0.125, p, p, p, null, 16, 64, 1,
                           null) == -1
     # the widest row (8192) is a shape every stacked entry point takes (no tokens: checked, nothing launched)
-    assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, p, null, 0, 8192, 1, null) == 0
+    assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, p, null, 0, 8192, 1, null) == 0
+    assert L.ldr_blend_sum(one, 1, 0.5, p, 0, 8192, 1, null) == 0
     assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.01, p, p, p, null, 0, 8192, 1,
                           null) == 0
     assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.01, p, 1, one, 0, p, 16, p, null,
