@@ -403,7 +403,11 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int WM_TT = 32;   // tokens per workgroup
+#ifndef LDR_WM_MB
+#define LDR_WM_MB 4           // write: 16-token blocks per workgroup (each query-part load serves all of them)
+#endif
+constexpr int WM_MB = LDR_WM_MB;   // 16-token blocks per workgroup
+constexpr int WM_TT = 16 * WM_MB;   // tokens per workgroup
 constexpr int WM_KC = 64;   // columns per chunk
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
@@ -415,20 +419,22 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
                                                    float* __restrict__ dots, int64_t n_tok, int d, int nq,
                                                    int64_t dots_jstride, float eps) {
   constexpr int NBA = NB > 0 ? NB : 1;   // array extents
-  __shared__ f32x4_t s_part[4][2][NBA][64];
-  __shared__ float s_ss[4][2][16];
+  __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
+  __shared__ float s_ss[4][WM_MB][16];
   const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
   const int64_t t0 = (int64_t)blockIdx.x * WM_TT;
-  f32x4_t acc[2][NBA];
+  f32x4_t acc[WM_MB][NBA];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
+  for (int mb = 0; mb < WM_MB; ++mb)
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float ss[2] = {0.f, 0.f};
-  int64_t roff[2];
-  bool tok_ok[2];
+  float ss[WM_MB];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+  for (int mb = 0; mb < WM_MB; ++mb) ss[mb] = 0.f;
+  int64_t roff[WM_MB];
+  bool tok_ok[WM_MB];
+#pragma unroll
+  for (int mb = 0; mb < WM_MB; ++mb) {
     const int64_t tok = t0 + 16 * mb + row;
     tok_ok[mb] = tok < n_tok;
     roff[mb] = (tok_ok[mb] ? tok : n_tok - 1) * (int64_t)d;
@@ -439,10 +445,10 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
   for (int b = 0; b < NBA; ++b) qrow[b] = min(16 * b + row, nq > 0 ? nq - 1 : 0);
   const int nchunks = (d + WM_KC - 1) / WM_KC;
   // a chunk's h and x rows: both 16-token blocks, the lane's two 8-column halves (clamped in bounds)
-  auto load_hx = [&](int c, uint4 (&hr)[2][2], uint4 (&xr)[2][2]) {
+  auto load_hx = [&](int c, uint4 (&hr)[WM_MB][2], uint4 (&xr)[WM_MB][2]) {
     const int col = c * WM_KC + quad * 16;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < WM_MB; ++mb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const int cc = col + 8 * hf < d ? col + 8 * hf : 0;
@@ -450,7 +456,7 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
         xr[mb][hf] = *reinterpret_cast<const uint4*>(x + roff[mb] + cc);
       }
   };
-  uint4 hr[2][2], xr[2][2];
+  uint4 hr[WM_MB][2], xr[WM_MB][2];
   if (w < nchunks) load_hx(w, hr, xr);
   for (int c = w; c < nchunks; c += 4) {   // wave-uniform trip count
     const int col = c * WM_KC + quad * 16;
@@ -470,12 +476,10 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
           qv[p][b][hf] = *reinterpret_cast<const uint4*>(qb + p * qb_part_stride + (int64_t)qrow[b] * d + cc[hf]);
-    // the next chunk's rows in flight while this one is computed
-    uint4 hn[2][2], xn[2][2];
-    if (c + 4 < nchunks) load_hx(c + 4, hn, xn);
-    uint4 va[2][2];
+
+    uint4 va[WM_MB][2];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < WM_MB; ++mb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         float hv[8], xv[8], vv[8];
@@ -501,20 +505,14 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
         for (int hf = 0; hf < 2; ++hf) {
           const uint4 qh = col_ok[hf] ? qv[p][b][hf] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-          for (int mb = 0; mb < 2; ++mb)
+          for (int mb = 0; mb < WM_MB; ++mb)
             acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qh), acc[mb][b],
                                                                  0, 0, 0);
         }
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        hr[mb][hf] = hn[mb][hf];
-        xr[mb][hf] = xn[mb][hf];
-      }
+    if (c + 4 < nchunks) load_hx(c + 4, hr, xr);   // the next chunk's rows (uniform branch)
   }
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+  for (int mb = 0; mb < WM_MB; ++mb) {
     ss[mb] += __shfl_xor(ss[mb], 16, 64);
     ss[mb] += __shfl_xor(ss[mb], 32, 64);
     if (quad == 0) s_ss[w][mb][row] = ss[mb];
@@ -522,13 +520,13 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
     for (int b = 0; b < NB; ++b) s_part[w][mb][b][l] = acc[mb][b];
   }
   __syncthreads();
-  if (tid < 32) {
+  if (tid < 16 * WM_MB) {
     const int mb = tid >> 4, rr = tid & 15;
     const float tot = ((s_ss[0][mb][rr] + s_ss[1][mb][rr]) + s_ss[2][mb][rr]) + s_ss[3][mb][rr];
     const int64_t tok = t0 + tid;
     if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
   }
-  for (int e = tid; e < 2 * NB * 64; e += WG) {
+  for (int e = tid; e < WM_MB * NB * 64; e += WG) {
     const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
     const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
     const int jj = 16 * b + (ll & 15);

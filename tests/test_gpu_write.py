@@ -37,3 +37,22 @@ def test_write_scores(dtype, T, d, N):
         j_lo = max(0, s - 1)
         if j_lo < N - 1:
             assert err_rms(got[j_lo:, s], ref[j_lo:, s]) <= 1e-5, s
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,T,d", [(1, 5, 64), (8, 77, 768), (3, 16, 8192)])
+def test_blend_sum_bitwise(dtype, m, T, d):
+    """ldr_blend_sum: round(sum_j round(beta g_j)) in fp32, j in order -- bitwise the same sequence in torch."""
+    from loopback_amd import _lib as L
+    gen = torch.Generator().manual_seed(m * 1000 + d)
+    gs = [torch.randn(T, d, generator=gen).to(dtype).to(DEV) for _ in range(m)]
+    out = torch.empty(T, d, dtype=dtype, device=DEV)
+    code = L.LIB.ldr_blend_sum(L.u64_array(g.data_ptr() for g in gs), m, 0.75, out.data_ptr(), T, d,
+                               L.BF16 if dtype == torch.bfloat16 else L.F32,
+                               torch.cuda.current_stream().cuda_stream)
+    L.check(code, "blend_sum")
+    torch.cuda.synchronize()
+    acc = torch.zeros(T, d, dtype=torch.float32, device=DEV)
+    for g in gs:
+        acc = acc + (g * 0.75).to(dtype).float()
+    assert torch.equal(out, acc.to(dtype))
