@@ -1237,6 +1237,11 @@ inline int launched() { return (int)hipGetLastError(); }
 // tokens per tile of the tiled kernels: at least one row per row slot
 inline int tile_tokens(int tpr) { const int rpw = WG / tpr; return rpw > 16 ? rpw : 16; }
 
+#ifndef LDR_B1_TT
+#define LDR_B1_TT 32          // backward pass 1: tokens per tile (at least one row per row slot)
+#endif
+inline int b1_tile(int tpr) { const int t = tile_tokens(tpr); return t > LDR_B1_TT ? t : LDR_B1_TT; }
+
 int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n) {
   if (!v || n < 1 || n > MAXS) return LDR_E_ARG;
   for (int64_t i = 0; i < n; ++i) {
@@ -1294,7 +1299,7 @@ int ldr_row_layout(int64_t d, int* vpt, int* tpr) {
 int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d) {
   int vpt, tpr;
   if (n_tok < 1 || row_layout(d, &vpt, &tpr, B1_MAX_VPT, LDR_B1_WAVE_ROWS, LDR_B1_VPT, true) != LDR_OK) return 0;
-  return grid_of(cdiv(n_tok, tile_tokens(tpr)), B1_GRID);
+  return grid_of(cdiv(n_tok, b1_tile(tpr)), B1_GRID);
 }
 
 int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream) {
@@ -1454,7 +1459,7 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
   if ((e = row_layout(d, &vpt, &tpr, B1_MAX_VPT, LDR_B1_WAVE_ROWS, LDR_B1_VPT, true))) return e;
   if (n_tok == 0) return LDR_OK;
   const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
-  const int tt = tile_tokens(tpr);
+  const int tt = b1_tile(tpr);
   const unsigned grid = grid_of(cdiv(n_tok, tt), B1_GRID);
   hipStream_t st = static_cast<hipStream_t>(stream);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_bwd1<T, VPT, B1Chunk<VPT>::C>), dim3(grid),

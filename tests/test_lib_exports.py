@@ -61,7 +61,8 @@ def test_row_layout_rejects(lib, d):
 
 def test_bwd1_parts(lib):
     assert lib.bwd1_parts(16384, 2048) == 512
-    assert lib.bwd1_parts(20, 2048) == 2          # 16-token tiles
+    assert lib.bwd1_parts(20, 2048) == 1          # 32-token tiles
+    assert lib.bwd1_parts(65, 2048) == 3
     assert lib.bwd1_parts(0, 2048) == 0
 
 
