@@ -37,6 +37,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=["c2", "c3", "c4"])
     ap.add_argument("--mode", default="scores", choices=["scores", "stack", "list"])
+    ap.add_argument("--graph", action="store_true",
+                    help="forward-only configs: time replays of the pass captured in a HIP graph (no host work)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the CPU baseline sample")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -155,12 +157,33 @@ def main():
         copy_calibration()
         return
     from loopback_amd import fused_dattn as FD
-    from loopback_amd.chain import CONFIGS, make_inputs, run_chain
+    from loopback_amd.chain import CONFIGS, capture_forward, make_inputs, run_chain
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
     h0, D, Q, G = make_inputs(cfg, dev)
     torch.cuda.synchronize()
+    if args.graph:   # the forward pass as one HIP graph: no Python or launch work per pass
+        if cfg.backward:
+            print("bench.py: --graph times forward-only configurations (c2)", file=sys.stderr)
+            sys.exit(2)
+        graph, _ = capture_forward(cfg, h0, D, Q, args.mode)
+        for _ in range(max(1, args.warmup)):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        _, ref_bytes = family_bytes(cfg, args.mode)
+        print(json.dumps({"metric": f"depth-read tokens/sec (fwd), {cfg.name}, HIP graph replay",
+                          "value": cfg.n_tok * args.steps / elapsed, "unit": "read-tokens/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup, "ms_per_step": 1e3 * elapsed / args.steps,
+                          "higher_is_better": True, "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
+                          "formula_wall_gbs": ref_bytes * args.steps / elapsed / 1e9,
+                          "config": {"workload": cfg.name, "mode": args.mode, "graph": True}}), flush=True)
+        return
 
     for _ in range(args.warmup):
         run_chain(cfg, h0, D, Q, G, args.mode)

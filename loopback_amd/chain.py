@@ -87,6 +87,37 @@ def make_inputs(cfg: ChainConfig, device, n_tok: int | None = None, q_std: float
     return h0, D, Q, G
 
 
+def chain_forward(cell, h0, D, K: int, mode: str):
+    """The chain's forward through `cell` (blocks x -> x + D_s, the stacked write in the stacked modes)."""
+    stack = cell.new_stack(h0.shape, h0.dtype, h0.device, mode=mode)
+    h, deltas, keys, coeffs, prior = h0, [], [], None, None
+    for s in range(len(D)):
+        l, blk = divmod(s, K)
+        x = h
+        hs = x + D[s]
+        deltas.append(stack.write(s, hs, x) if stack is not None else hs - x)
+        h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
+    return h
+
+
+def capture_forward(cfg: ChainConfig, h0, D, Q, mode: str):
+    """A HIP graph of the no-grad chain forward on the static inputs h0, D (their contents may change between
+    replays, not their storage). Returns (graph, out): graph.replay() recomputes out."""
+    cell = LoopDeltaAttnRes(cfg.d, cfg.R, cfg.K, beta=cfg.beta, eps=cfg.eps).to(h0.device)
+    with torch.no_grad():
+        cell.query.copy_(Q)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            chain_forward(cell, h0, D, cfg.K, mode)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = chain_forward(cell, h0, D, cfg.K, mode)
+    graph.cell = cell   # keeps the query alive with the graph
+    return graph, out
+
+
 def run_chain(cfg: ChainConfig, h0, D, Q, G, mode: str, grad: bool | None = None):
     """One pass of the chain through the HIP read in `mode` ('scores', 'stack' or 'list'). Returns
     (h_final, loss, grads) with grads = {'h0', 'D': [...], 'query'} when grad (default cfg.backward)."""
@@ -97,14 +128,7 @@ def run_chain(cfg: ChainConfig, h0, D, Q, G, mode: str, grad: bool | None = None
     h0 = h0.detach().requires_grad_(grad)
     D = [x.detach().requires_grad_(grad) for x in D]
     with torch.set_grad_enabled(grad):
-        stack = cell.new_stack(h0.shape, h0.dtype, h0.device, mode=mode)
-        h, deltas, keys, coeffs, prior = h0, [], [], None, None
-        for s in range(cfg.N):
-            l, blk = divmod(s, cfg.K)
-            x = h
-            hs = x + D[s]
-            deltas.append(stack.write(s, hs, x) if stack is not None else hs - x)
-            h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
+        h = chain_forward(cell, h0, D, cfg.K, mode)
         loss = (h.float() * G).sum()
         grads = None
         if grad:

@@ -1,0 +1,58 @@
+"""The no-grad (prefill / evaluation) chain forward captured in a HIP graph: every library launch takes its
+addresses and sizes by value and allocates nothing, and torch's allocations come from the graph's pool, so the
+whole pass replays without host work. Replays are checked bitwise against eager passes, with eager work and
+synchronization between them, and after the inputs' contents change (the graph reads its static inputs)."""
+import pytest
+import torch
+
+from gpu_helpers import DEV
+
+pytestmark = pytest.mark.gpu
+
+
+def _chain_forward(cell, h0, D, K, mode):
+    stack = cell.new_stack(h0.shape, h0.dtype, h0.device, mode=mode)
+    h, deltas, keys, coeffs, prior = h0, [], [], None, None
+    for s in range(len(D)):
+        l, blk = divmod(s, K)
+        hs = h + D[s]
+        deltas.append(stack.write(s, hs, h) if stack is not None else hs - h)
+        h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
+    return h
+
+
+@pytest.mark.parametrize("mode", ["scores", "stack", "list"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_forward_chain_replays_in_a_graph(mode, dtype):
+    from loopback_amd.cell import LoopDeltaAttnRes
+    K, R, d, t = 2, 4, 256, 300
+    gen = torch.Generator().manual_seed(5)
+    cell = LoopDeltaAttnRes(d, R, K).to(DEV)
+    with torch.no_grad():
+        cell.query.copy_((torch.randn(K * R - 1, d, generator=gen) * 0.5).to(DEV))
+    h0 = torch.randn(2, t, d, generator=gen).to(dtype).to(DEV)
+    D = [torch.randn(2, t, d, generator=gen).to(dtype).to(DEV) for _ in range(K * R)]
+    print(f"case graph {mode} {dtype}", flush=True)
+    with torch.no_grad():
+        ref = _chain_forward(cell, h0, D, K, mode).clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            _chain_forward(cell, h0, D, K, mode)                    # warm-up on a side stream
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = _chain_forward(cell, h0, D, K, mode)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)
+            eager = _chain_forward(cell, h0, D, K, mode)           # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(eager, ref)
+        D[3].mul_(-0.5)
+        h0.add_(0.25)
+        ref2 = _chain_forward(cell, h0, D, K, mode).clone()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref2) and not torch.equal(ref2, ref)
