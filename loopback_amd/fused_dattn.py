@@ -636,8 +636,9 @@ class FusedCombineStk(torch.autograd.Function):
             stack.dQ = torch.zeros(ctx.q_shape, device=dev, dtype=torch.float32)
         g = torch.zeros(ctx.shape, device=dev, dtype=stack.V.dtype) if g is None else g.to(stack.V.dtype).contiguous()
         # the blend's gradients are written only where no later kernel forms them from g
-        g_prop = torch.empty_like(g) if ctx.at_boundary and not ctx.linked else None
-        g_h0 = torch.empty_like(g) if ctx.at_boundary and not ctx.h0_sum else None
+        need_prop, need_h0 = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
+        g_prop = torch.empty_like(g) if ctx.at_boundary and not ctx.linked and need_prop else None
+        g_h0 = torch.empty_like(g) if ctx.at_boundary and not ctx.h0_sum and need_h0 else None
         vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
         rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
         drp = L.u64_array(stack.dR[i].data_ptr() for i in range(n))
@@ -648,7 +649,7 @@ class FusedCombineStk(torch.autograd.Function):
         stack.bwd[step] = (g, qc)
         final = [i == step or (step == 1 and i == 0) for i in range(n)]
         dquery = stack.dQ.to(ctx.q_dtype) if step == 1 else None   # read 1's backward is the pass's last
-        dprop = g_prop if ctx.at_boundary else g
+        dprop = (g_prop if ctx.at_boundary else g) if need_prop else None
         if ctx.linked:
             stack.gadd[step] = (g, ctx.beta if ctx.at_boundary else 0.0)
             dprop = None
