@@ -4,8 +4,9 @@ CPU (no GPU): the model's wiring with the oracle read in fp64 -- topology and sh
 Loopback at beta = 0 with zero queries (the reference audit's C6: every coefficient is then 1, so the read is the
 plain residual sum), and a loss near log(vocab) at init.
 GPU: the model with the HIP read against the same weights on the CPU with the oracle read in fp64 -- loss and every
-parameter gradient (fp32: norm-relative 1e-4; bf16: loss within 1e-2 relative) -- and a few training steps that
-lower the loss on a fixed batch.
+parameter gradient (fp32: norm-relative 1e-4; bf16: loss within 1e-2 relative) -- the model through every read
+path (stored / online scores, list layout, torch glue) agreeing, and a few training steps that lower the loss on a
+fixed batch. CPU also: the meta-device init path leaves the queries at zero.
 """
 import copy
 import math
@@ -120,3 +121,49 @@ def test_lm_training_lowers_loss():
     torch.cuda.synchronize()
     assert last < first - 0.5, (first, last)
     assert model.read.query.abs().sum().item() > 0            # the read's query is trained
+
+
+def test_meta_device_init_gives_zero_queries():
+    """The reference's init guard (check_equivalence_init.py:109-156): a model built on the meta device and
+    materialized with reset_parameters has the read's query (K R - 1, d) at zero and the decay-only read."""
+    cfg = LMConfig(**TINY)
+    with torch.device("meta"):
+        m = LoopbackLM(cfg)
+    assert m.read.query.is_meta
+    m = m.to_empty(device="cpu")
+    m.reset_parameters()
+    assert m.read.query.shape == (cfg.loop_blocks * cfg.loops - 1, cfg.hidden_size)
+    assert not m.read.query.any()
+    assert all(torch.isfinite(p).all() for p in m.parameters())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lm_read_modes_agree(monkeypatch, dtype):
+    """The whole model through every path of the read (tests/test_dattn_stack.py:120-159): stacked with stored
+    scores, stacked with online scores, the list layout, and the stacked layout with the caller's glue as torch ops.
+    Loss and every parameter gradient agree (fp32: norm-relative 1e-6; bf16: 1e-2)."""
+    torch.manual_seed(3)
+    cfg = LMConfig(**TINY)
+    model = LoopbackLM(cfg)
+    with torch.no_grad():
+        model.read.query.normal_(0, 0.5)
+    ids = ids_for(cfg, b=2, t=40).cuda()
+    runs = {}
+    for name, env in {"scores": ("1", "1", "1"), "stack": ("1", "0", "1"), "list": ("0", "1", "1"),
+                      "torch-glue": ("1", "1", "0")}.items():
+        monkeypatch.setenv("LOOP_DATTN_STACK", env[0])
+        monkeypatch.setenv("LOOP_DATTN_DOTS", env[1])
+        monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", env[2])
+        m = copy.deepcopy(model).to(device="cuda", dtype=dtype)
+        loss = m(ids)
+        loss.backward()
+        torch.cuda.synchronize()
+        runs[name] = (loss.item(), _grads(m))
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    l0, g0 = runs["scores"]
+    for name, (l, g) in runs.items():
+        assert abs(l - l0) <= tol * abs(l0), (name, l, l0)
+        for k in g0:
+            err = ((g[k] - g0[k]).norm() / g0[k].norm().clamp_min(1e-30)).item()
+            assert err <= tol, (name, k, err)
