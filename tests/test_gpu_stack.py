@@ -64,10 +64,11 @@ def test_chain_matches_oracle(K, R, dtype, mode):
             assert err_norm(a, c) <= 2 * err_norm(b, c) + 2e-3
 
 
-@pytest.mark.parametrize("K,R,d,t", [(8, 8, 64, 33), (2, 2, 8192, 20), (1, 3, 8, 5)])
+@pytest.mark.parametrize("K,R,d,t", [(8, 8, 64, 33), (2, 2, 8192, 20), (1, 3, 8, 5), (2, 2, 64, 40001)])
 def test_stack_extremes_match_oracle(K, R, d, t):
     """The stacked layout at its limits in fp32: 64 steps (the most a stack holds; reads of up to 64 sources),
-    the widest row, the narrowest row with one token per tile row."""
+    the widest row, the narrowest row with one token per tile row, and a ragged 40001 tokens (several tiles per
+    workgroup of the grid-capped kernels)."""
     from loopback_amd.chain import ChainConfig
     cfg = ChainConfig(f"edge-K{K}R{R}d{d}", d, K, R, 1, t, torch.float32, True, q_std=0.5)
     print(f"case stack edge K{K} R{R} d{d} t{t}", flush=True)
