@@ -223,8 +223,8 @@ def main():
             traffic = tr["hbm_bytes_per_launch"].get(dom)
 
     line = {
-        "metric": "depth-read tokens/sec (fwd+bwd), d=2048, N=32 stack" if cfg.backward else
-                  f"depth-read tokens/sec (fwd), {cfg.name}",
+        "metric": ("depth-read tokens/sec (fwd+bwd), d=2048, N=32 stack" if args.config == "c4" else
+                   f"depth-read tokens/sec ({'fwd+bwd' if cfg.backward else 'fwd'}), {cfg.name}"),
         "value": cfg.n_tok * args.steps / elapsed,
         "unit": "read-tokens/s",
         "n_gpus": 1,

@@ -328,7 +328,7 @@ class DattnStack:
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
     transposed operand for its tensor-core product; the HIP write reads Q directly)."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
-                 "assembled", "neg", "dQ", "wh", "gadd", "h0_ref", "h0_steps", "h0_g")
+                 "assembled", "neg", "dQ", "wh", "gadd", "h0_ref", "h0_steps", "h0_g", "vptr", "rptr", "drptr")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
@@ -342,6 +342,10 @@ class DattnStack:
         self.V = torch.empty((n_steps, b, t, d), dtype=dtype, device=device)
         self.R = torch.empty((n_steps, b, t, 1), dtype=torch.float32, device=device)
         _require_gpu(self.V, "the stack")
+        # the slices' addresses, once: a read over sources 0..n-1 passes these tables (the kernels take n entries)
+        self.vptr = _slice_table(self.V)
+        self.rptr = _slice_table(self.R)
+        self.drptr = None
         self.dV = self.dR = None
         self.WZ = None
         self.bwd = {}
@@ -380,10 +384,17 @@ class DattnStack:
         """Allocate the backward state on the first backward of the pass; False then, True afterwards."""
         if self.dR is None:
             self.dR = torch.zeros_like(self.R)
+            self.drptr = _slice_table(self.dR)
             pairs = self.n_steps * (self.n_steps + 1) // 2 - 1
             self.WZ = torch.empty((max(1, pairs), self.n_tok, 2), dtype=torch.float32, device=self.V.device)
             return False
         return True
+
+
+def _slice_table(t: torch.Tensor):
+    """Device addresses of t[0], t[1], ... (a stack's slices), as the kernels' per-source tables."""
+    step = t.stride(0) * t.element_size()
+    return L.u64_array(t.data_ptr() + i * step for i in range(t.shape[0]))
 
 
 def _proposal_grad(added):
@@ -511,8 +522,7 @@ class FusedDattnReadStk(torch.autograd.Function):
         tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
         grad = any(ctx.needs_input_grad)
         prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
-        vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
-        rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
+        vp, rp = stack.vptr, stack.rptr
         if stack.DOTS is not None and step >= 1 and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
             dots = stack.DOTS[step - 1]          # the stored scores of query step - 1, [source, token]
         else:
@@ -532,9 +542,7 @@ class FusedDattnReadStk(torch.autograd.Function):
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         stack.grads()
         g = g.to(stack.V.dtype).contiguous()
-        vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
-        rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
-        drp = L.u64_array(stack.dR[i].data_ptr() for i in range(n))
+        vp, rp, drp = stack.vptr, stack.rptr, stack.drptr
         wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
         dq, dcbar = _bwd1(vp, rp, n, g, gt, prob, dots, tc, cbar_c, c0c, drp, True, wz, n_tok, n_tok, d,
                           _dtype_code(stack.V.dtype), dev)
@@ -594,8 +602,7 @@ class FusedCombineStk(torch.autograd.Function):
         grad = any(ctx.needs_input_grad)      # else no backward: the probabilities are not stored
         prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
         next_prior = torch.empty(n, device=dev, dtype=torch.float32)
-        vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
-        rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
+        vp, rp = stack.vptr, stack.rptr
         if stack.DOTS is not None and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
             dots = stack.DOTS[step - 1]
         else:
@@ -639,9 +646,7 @@ class FusedCombineStk(torch.autograd.Function):
         need_prop, need_h0 = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
         g_prop = torch.empty_like(g) if ctx.at_boundary and not ctx.linked and need_prop else None
         g_h0 = torch.empty_like(g) if ctx.at_boundary and not ctx.h0_sum and need_h0 else None
-        vp = L.u64_array(stack.V[i].data_ptr() for i in range(n))
-        rp = L.u64_array(stack.R[i].data_ptr() for i in range(n))
-        drp = L.u64_array(stack.dR[i].data_ptr() for i in range(n))
+        vp, rp, drp = stack.vptr, stack.rptr, stack.drptr
         wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
         _, dcoeffs = _bwd1(vp, rp, n, g, gt, prob, dots, tc, coeffs_c, prior_c, drp, True, wz, n_tok, n_tok, d,
                            _dtype_code(stack.V.dtype), dev, cols=n - 1, lam=ctx.lam, g_prop=g_prop, g_h0=g_h0,
