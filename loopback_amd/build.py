@@ -1,9 +1,10 @@
-"""Build libloopback_read.so in-tree with hipcc for gfx950 (MI355X).
+"""Build libloopback_read.so (the read's kernels and C ABI) and libloopback_probe.so (the streaming-ceiling probes of
+stream_probe.py) in-tree with hipcc for gfx950 (MI355X).
 
-    python -m loopback_amd.build            # compile, print the command
+    python -m loopback_amd.build            # compile, print the commands
 
-The library lands next to this file (loopback_amd/libloopback_read.so), so it travels with the source tree to the
-GPU box; nothing is installed. Compiling needs hipcc only, not a GPU.
+The libraries land next to this file, so they travel with the source tree to the GPU box; nothing is installed.
+Compiling needs hipcc only, not a GPU.
 """
 from __future__ import annotations
 
@@ -17,6 +18,8 @@ ROOT = os.path.dirname(HERE)
 SRC = os.path.join(HERE, "csrc", "loopback_read.hip")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libloopback_read.so")
+PROBE_SRC = os.path.join(HERE, "csrc", "stream_probe.hip")
+PROBE_LIB = os.path.join(HERE, "libloopback_probe.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code (plain fp32 VALU instead).
@@ -31,16 +34,21 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = True) -> str:
-    """Compile the library (always; a stale build never survives a call) and return its path."""
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *FLAGS, f"-I{INCLUDE}", "-o", tmp, SRC]
+def _compile(src: str, lib: str, verbose: bool) -> None:
+    tmp = lib + ".tmp"
+    cmd = [hipcc(), *FLAGS, f"-I{INCLUDE}", "-o", tmp, src]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = True) -> str:
+    """Compile both libraries (always; a stale build never survives a call); returns the read library's path."""
+    _compile(SRC, LIB, verbose)
+    _compile(PROBE_SRC, PROBE_LIB, verbose)
     return LIB
 
 

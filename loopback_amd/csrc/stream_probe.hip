@@ -1,0 +1,69 @@
+// stream_probe.hip -- what HBM streaming the box sustains for the read kernels' access patterns.
+//
+// The read kernels stream n sources row by row (one 16-byte vector per lane, rows of 4 KiB) and write at most a few
+// rows per row set. These probes do the same with no arithmetic: read the n sources (XOR-folded so the loads are
+// not dead), optionally write one row per row set; and a plain device copy. bench-side code (stream_probe.py) times
+// them to give the practical ceiling each kernel's read/write mix allows, next to the 8 TB/s peak.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int MAXP = 64;
+constexpr int ROWV = 256;   // 16-byte vectors per row: 4 KiB rows, one vector per lane of a 256-lane workgroup
+struct Tab { const u32x4* p[MAXP]; };
+
+// n sources of `rows` rows; with out != nullptr one row written per row set (the read forward's mix)
+__global__ __launch_bounds__(256) void k_probe_read(Tab t, int n, int64_t rows, u32x4* __restrict__ out,
+                                                    unsigned* __restrict__ sink) {
+  const int lane = (int)threadIdx.x;
+  unsigned s = 0;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+      u32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(t.p[i + u] + row * ROWV + lane);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc ^= v[u];
+    }
+    for (; i < n; ++i) acc ^= __builtin_nontemporal_load(t.p[i] + row * ROWV + lane);
+    if (out) out[row * ROWV + lane] = acc;
+    s ^= acc.x ^ acc.y ^ acc.z ^ acc.w;
+  }
+  if (s == 0x9e3779b9u) sink[0] = s;   // never true for the probe's data; keeps the loads live
+}
+
+__global__ __launch_bounds__(256) void k_probe_copy(const u32x4* __restrict__ a, u32x4* __restrict__ b, int64_t n) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    b[i] = __builtin_nontemporal_load(a + i);
+}
+
+}  // namespace
+
+extern "C" {
+
+// Read n sources (host array of n device addresses, each `rows` rows of 4 KiB, 16-byte aligned), writing one row
+// per row set to out when out != NULL; grid workgroups of 256 lanes. Returns 0 or a hipError_t / -1 on bad input.
+int ldp_read(const uint64_t* src, int n, int64_t rows, void* out, void* sink, int grid, void* stream) {
+  if (!src || n < 1 || n > MAXP || rows < 1 || !sink || grid < 1) return -1;
+  Tab t;
+  for (int i = 0; i < MAXP; ++i) t.p[i] = i < n ? reinterpret_cast<const u32x4*>(src[i]) : nullptr;
+  for (int i = 0; i < n; ++i)
+    if (!t.p[i] || (reinterpret_cast<uintptr_t>(t.p[i]) & 15u)) return -1;
+  hipLaunchKernelGGL(k_probe_read, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), t, n, rows,
+                     static_cast<u32x4*>(out), static_cast<unsigned*>(sink));
+  return (int)hipGetLastError();
+}
+
+// b[0:bytes] = a[0:bytes] (bytes a multiple of 16).
+int ldp_copy(const void* a, void* b, int64_t bytes, int grid, void* stream) {
+  if (!a || !b || bytes < 16 || (bytes & 15) || grid < 1) return -1;
+  hipLaunchKernelGGL(k_probe_copy, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(a), static_cast<u32x4*>(b), bytes / 16);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"
