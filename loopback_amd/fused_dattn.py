@@ -25,7 +25,11 @@ Layouts:
     backward keeps its output gradient g_s and its per-(source, token) scalars (w, dz r / sqrt(d)); the gradient of
     update i is formed once, when its scale's backward runs (after every read of it), as
     sum_s (w_si g_s + dzr_si q_s) + the scale's term, in fp32 with one rounding. Same gradients, at least as
-    accurate as the per-read bf16 adds, and about a quarter less HBM traffic over a pass.
+    accurate as the per-read bf16 adds, and about a quarter less HBM traffic over a pass;
+  * FusedCombineStk (this module's extension, no reference counterpart): the stacked read with the caller's glue
+    (LoopDeltaAttnRes.combine's iteration-end blend and coefficient bookkeeping) inside the kernels, and the
+    gradient hand-offs that spare autograd's own glue (one query gradient per pass, the proposal's gradient added
+    by the update-gradient kernel, h0's blend gradients summed once).
 """
 from __future__ import annotations
 
@@ -38,7 +42,7 @@ import torch
 from . import _lib as L
 
 __all__ = ["rstd_ref", "rstd", "fused_read_supported", "FusedDattnRead", "DattnGradAccum", "FusedDattnReadAcc",
-           "DattnStack", "FusedDattnReadStk", "_alias"]
+           "DattnStack", "FusedDattnReadStk", "FusedCombineStk", "_alias"]
 
 _LIB = L.LIB
 MAX_SOURCES = L.MAX_SOURCES
@@ -350,7 +354,8 @@ class DattnStack:
         self.WZ = None
         self.bwd = {}
         self.assembled = set()
-        self.neg = {}         # s -> (gradient of update s, its negation), handed from _RstdStk to _WriteDelta
+        self.neg = {}         # s -> (gradient of the write's h, of its x, the added proposal gradient or None),
+                              # handed from _RstdStk to _WriteDelta
         self.dQ = None        # the query gradient rows of the fused combines' backwards (fp32)
         self.wh = {}          # s -> weak reference to the write's h (a fused combine that takes it as its proposal
         self.gadd = {}        # hands its proposal gradient, gadd[s] = (g, beta), to the update's gradient kernel)
