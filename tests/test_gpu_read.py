@@ -12,7 +12,8 @@ LoopDeltaAttnRes.combine -- on the same seeded inputs; mirrors tests/test_fused_
      bf16 torch glue, the same ops as the reference's; against the bf16 reference read itself (whose gradients
      round every per-source term to bf16): norm-relative <= 1e-2 for outputs and all gradients;
   3. zero query, cbar == prior: out == base and tc == c0 bitwise, fp32 and bf16;
-  4. the layout's extremes in fp32: one token, d = 8, 40, 2056, 8192, 64 sources.
+  4. the layout's extremes in fp32: one token, d = 8, 40, 2056, 8192, 64 sources; extreme values (a saturated
+     softmax, priors under the clamp, large updates beside an all-zero one).
 """
 import pytest
 import torch
@@ -96,6 +97,32 @@ def test_fp32_edge_shapes(b, t, d, n, boundary):
     ref64 = run_oracle(d, n, args, boundary, dtype=torch.float64)
     e64 = compare(hip, ref64, err_rms)
     assert max(e64.values()) <= 1e-5, e64
+
+
+@pytest.mark.parametrize("boundary", [False, True])
+def test_fp32_extreme_inputs(boundary):
+    """Conditions the reference read meets at the edges of training: a query large enough to saturate the softmax
+    (logits ~ +-50), priors below the 1e-8 clamp, updates of magnitude 1e3 next to an all-zero update (its scale is
+    rsqrt(eps) = 1000 and its score 0). No inf / nan, and against the exact read the 1e-5 x RMS fp32 bar -- or, where
+    the problem's conditioning puts the reference read itself in fp32 above it (the updates' gradients here, ~5e-5),
+    no worse than that reference read."""
+    b, t, d, n = 2, 33, 512, 6
+    deltas, proposal, h0, q, prior, coeffs, up, up2 = make(b, t, d, n, torch.float32, seed=77)
+    deltas = [x * 1e3 for x in deltas[:-2]] + [torch.zeros_like(deltas[-2]), deltas[-1]]
+    q = q * 60.0
+    prior = prior.clone()
+    prior[0], prior[2] = 1e-12, 3e-9
+    coeffs = prior.view(1, 1, -1) + 0.2 * torch.randn(b, t, n - 1, generator=torch.Generator().manual_seed(78))
+    args = (deltas, proposal, h0, q, prior, coeffs, up, up2)
+    print(f"case fp32 extreme boundary={boundary}", flush=True)
+    hip = run_hip(d, n, args, boundary)
+    for k, v in hip.items():
+        for x in (v if isinstance(v, list) else [v]):
+            assert x is None or torch.isfinite(x).all(), k
+    ref64 = run_oracle(d, n, args, boundary, dtype=torch.float64)
+    e64 = compare(hip, ref64, err_rms)
+    er = compare(run_oracle(d, n, args, boundary), ref64, err_rms)
+    assert all(e64[k] <= max(1e-5, er[k]) for k in e64), (e64, er)
 
 
 @pytest.mark.parametrize("b,t,d", [(2, 256, 1024), (2, 128, 1536), (4, 128, 768)])
