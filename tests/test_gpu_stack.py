@@ -81,6 +81,26 @@ def test_stack_extremes_match_oracle(K, R, d, t):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["scores", "stack"])
+def test_chain_with_saturated_reads(dtype, mode):
+    """Queries large enough to saturate every read's softmax (q ~ N(0, 20^2): logits in the tens), through the
+    stacked write's matrix-core scores and the reads: no worse against the exact chain than the reference chain in
+    the same dtype (+ 1e-6 in fp32, + 2e-3 in bf16, the reference test's own slack)."""
+    from loopback_amd.chain import ChainConfig
+    cfg = ChainConfig("sat-K3R3", 256, 3, 3, 1, 200, dtype, True, q_std=20.0)
+    print(f"case saturated {dtype} {mode}", flush=True)
+    h, g = hip_chain(cfg, mode)
+    hr, gr = ref_chain(cfg, None)
+    h64, g64 = ref_chain(cfg, torch.float64)
+    slack = 1e-6 if dtype == torch.float32 else 2e-3
+    assert torch.isfinite(h).all()
+    assert err_norm(h, h64) <= 2 * err_norm(hr, h64) + slack
+    for a, b, c in zip(grad_list(g), grad_list(gr), grad_list(g64)):
+        assert torch.isfinite(a).all()
+        assert err_norm(a, c) <= 2 * err_norm(b, c) + slack
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_layouts_agree(dtype):
     cfg = chain_cfg(3, 3, dtype)
     hl, gl = hip_chain(cfg, "list")
