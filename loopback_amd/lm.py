@@ -15,6 +15,7 @@ memory-efficient kernels in 16-bit (never the math path's batched products in bf
 
     python -m loopback_amd.lm --steps 10 --warmup 3            # config 5: the Loopback LM step, tokens/s
     python -m loopback_amd.lm --residual none                  # the same model as Plain Loop
+    python -m loopback_amd.lm --prefill --batch 8 --seq 4096 [--graph]   # no-grad forward, tokens/s
 """
 from __future__ import annotations
 
@@ -253,6 +254,10 @@ def bench(argv=None):
     ap.add_argument("--batch", type=int, default=8)
     ap.add_argument("--seq", type=int, default=2048)
     ap.add_argument("--residual", default="delta_attnres", choices=["delta_attnres", "none"])
+    ap.add_argument("--prefill", action="store_true",
+                    help="time the no-grad forward (logits) instead of the training step; with --graph replayed as "
+                         "one HIP graph")
+    ap.add_argument("--graph", action="store_true")
     a = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("lm: no GPU visible", file=sys.stderr)
@@ -261,9 +266,11 @@ def bench(argv=None):
     cfg = LMConfig(residual=None if a.residual == "none" else "delta_attnres")
     torch.manual_seed(0)
     model = LoopbackLM(cfg).to(device=dev, dtype=torch.bfloat16)
-    opt = make_optimizer(model)
     gen = torch.Generator(device=dev).manual_seed(1)
     ids = torch.randint(0, cfg.vocab_size, (a.batch, a.seq), device=dev, generator=gen)
+    if a.prefill:
+        return _prefill(model, cfg, ids, a)
+    opt = make_optimizer(model)
     for _ in range(a.warmup):
         train_step(model, opt, ids)
     torch.cuda.synchronize()
@@ -281,6 +288,47 @@ def bench(argv=None):
                       "data": "uniform random token ids", "optimizer": "AdamW (foreach)",
                       "config": {"topology": cfg.topology(), **asdict(cfg), "batch": a.batch, "seq": a.seq}}),
           flush=True)
+
+
+def _prefill(model: LoopbackLM, cfg: LMConfig, ids: torch.Tensor, a) -> None:
+    """No-grad forward to the logits (the reference's prefill measurement, results/README.md:163-177), eagerly or
+    replayed from one HIP graph (the read records nothing for a backward and allocates nothing itself)."""
+    model.eval()
+
+    def fwd():
+        return model.head(model.hidden(ids))
+
+    with torch.no_grad():
+        for _ in range(a.warmup):
+            fwd()
+        torch.cuda.synchronize()
+        if a.graph:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                fwd()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                fwd()
+            run = graph.replay
+        else:
+            run = fwd
+        run()
+        torch.cuda.synchronize()
+        gc.collect()
+        gc.freeze()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            run()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    tokens = a.batch * a.seq
+    print(json.dumps({"metric": "LM prefill tokens/sec (no-grad forward to logits)", "value": tokens * a.steps / dt,
+                      "unit": "tokens/s", "ms_per_pass": 1e3 * dt / a.steps, "steps": a.steps, "graph": a.graph,
+                      "dtype": "bf16", "data": "uniform random token ids",
+                      "config": {"topology": cfg.topology(), "residual": cfg.residual, "batch": a.batch,
+                                 "seq": a.seq}}), flush=True)
 
 
 if __name__ == "__main__":
