@@ -1,0 +1,84 @@
+"""Chains through linear blocks, as the reference's stacked-layout test builds them (tests/test_dattn_stack.py:68-127):
+hs = (h.float() @ W_s).to(dtype) + h, so the state reaches the next block both through the residual and through a
+matrix product, and the loss mean(h.float()^2) sends gradients into every W_s, h0 and the query. The HIP read in
+each layout ('list', 'stack', 'scores') against the oracle cell on the CPU with the same weights: norm-relative 1e-5
+in fp32 and 1e-2 in bf16 (outputs and every gradient), and in bf16 no further from the fp64 oracle than the
+reference read in bf16 is (<= 2 err_ref + 2e-3, tests/test_fused_dattn.py:104-109).
+"""
+import pytest
+import torch
+
+from gpu_helpers import DEV, err_norm
+from oracle.reference_read import OracleCell
+
+pytestmark = pytest.mark.gpu
+
+BETA, EPS = 0.75, 1e-6
+
+
+def make(K, R, d, n_tok, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    Ws = [torch.randn(d, d, generator=g) * 0.03 for _ in range(K * R)]
+    h0 = torch.randn(1, n_tok, d, generator=g) * 0.5
+    q = torch.randn(K * R - 1, d, generator=g) * 0.5
+    return Ws, h0, q
+
+
+def hip_chain(K, R, dtype, mode, Ws, h0, q):
+    from loopback_amd.cell import LoopDeltaAttnRes
+    d = h0.shape[-1]
+    cell = LoopDeltaAttnRes(d, R, K, beta=BETA, eps=EPS).to(DEV)
+    with torch.no_grad():
+        cell.query.copy_(q)
+    Ws = [w.detach().to(DEV).requires_grad_() for w in Ws]
+    h0 = h0.detach().to(DEV, dtype).requires_grad_()
+    stack = cell.new_stack(h0.shape, dtype, h0.device, mode=mode)
+    h, deltas, keys, coeffs, prior = h0, [], [], None, None
+    for s in range(K * R):
+        l, blk = divmod(s, K)
+        x = h
+        hs = (h.float() @ Ws[s]).to(dtype) + h
+        deltas.append(stack.write(s, hs, x) if stack is not None else hs - x)
+        h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
+    (h.float() ** 2).mean().backward()
+    torch.cuda.synchronize()
+    return h.detach().cpu(), [w.grad.cpu() for w in Ws] + [h0.grad.cpu(), cell.query.grad.cpu()]
+
+
+def oracle_chain(K, R, dtype, Ws, h0, q):
+    """The same chain through the oracle cell on the CPU; fp64 runs the blocks in fp64 as well."""
+    wide = torch.float64 if dtype == torch.float64 else torch.float32
+    Ws = [w.detach().to(wide).clone().requires_grad_() for w in Ws]
+    h0 = h0.detach().to(dtype).clone().requires_grad_()
+    query = q.detach().to(wide).clone().requires_grad_()
+    cell = OracleCell(h0.shape[-1], R, K, BETA, EPS, query)
+    h, deltas, keys, coeffs, prior = h0, [], [], None, None
+    for s in range(K * R):
+        l, blk = divmod(s, K)
+        x = h
+        hs = (h.to(wide) @ Ws[s]).to(dtype) + h
+        deltas.append(hs - x)
+        h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys)
+    (h.to(wide) ** 2).mean().backward()
+    return h.detach(), [w.grad for w in Ws] + [h0.grad, query.grad]
+
+
+@pytest.mark.parametrize("K,R,dtype", [(2, 4, torch.bfloat16), (3, 3, torch.bfloat16), (2, 4, torch.float32),
+                                       (3, 3, torch.float32)])
+@pytest.mark.parametrize("mode", ["list", "stack", "scores"])
+def test_linear_block_chain_matches_oracle(K, R, dtype, mode):
+    print(f"case linear blocks K{K} R{R} {dtype} {mode}", flush=True)
+    Ws, h0, q = make(K, R, 256, 2048)
+    h0 = h0.to(dtype).float()   # every run starts from the same (rounded) state
+    h, g = hip_chain(K, R, dtype, mode, Ws, h0, q)
+    hr, gr = oracle_chain(K, R, dtype, Ws, h0, q)
+    assert torch.isfinite(h).all() and all(torch.isfinite(x).all() for x in g)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert err_norm(h, hr) <= tol
+    worst = max(err_norm(a, b) for a, b in zip(g, gr))
+    assert worst <= tol, worst
+    if dtype == torch.bfloat16:
+        h64, g64 = oracle_chain(K, R, torch.float64, Ws, h0, q)
+        assert err_norm(h, h64) <= 2 * err_norm(hr, h64) + 2e-3
+        for a, b, c in zip(g, gr, g64):
+            assert err_norm(a, c) <= 2 * err_norm(b, c) + 2e-3
