@@ -395,10 +395,12 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
 // write step on the matrix cores (bf16 updates): the scores are a (tokens x d) . (d x queries) product. Each fp32
 // query row is held as three bf16 parts q = hi + mid + lo (the split is exact to ~2^-24 relative); the update is
 // exactly bf16 after its rounding, so three bf16 MFMAs with fp32 accumulation give fp32-accurate scores.
-// A workgroup takes 32 tokens (two 16-row blocks); its 4 waves split d into 64-column chunks (lane quad g holds
-// 16 contiguous columns of its row, i.e. two 8-element k-groups, one per MFMA); the wave partials meet in LDS in a
-// fixed order. v_mfma_f32_16x16x32_bf16 operands: lane l holds row (l % 16) of A and column (l % 16) of B over the
-// k-group of its quad (l / 16); the result holds rows 4 (l / 16) + i, i < 4, of column l % 16.
+// A workgroup takes WM_TT tokens (WM_MB 16-row blocks); its 4 waves split d into 64-column chunks. In a chunk, lane
+// quad g holds columns [8g, 8g + 8) and [32 + 8g, 40 + 8g) of its row (one 8-element k-group per MFMA), so each
+// load and store instruction covers 64 contiguous bytes of every row it touches; the wave partials meet in LDS in a
+// fixed order. A wave requests the next chunk's rows before it works on the current one.
+// v_mfma_f32_16x16x32_bf16 operands: lane l holds row (l % 16) of A and column (l % 16) of B over the k-group of its
+// quad (l / 16); the result holds rows 4 (l / 16) + i, i < 4, of column l % 16.
 // ---------------------------------------------------------------------------------------------------------------
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -409,6 +411,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int WM_MB = LDR_WM_MB;   // 16-token blocks per workgroup
 constexpr int WM_TT = 16 * WM_MB;   // tokens per workgroup
 constexpr int WM_KC = 64;   // columns per chunk
+constexpr int WM_QS = 8;    // column step between the quads of a wave
+constexpr int WM_HS = 32;   // column step between a lane's two k-groups
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
@@ -444,14 +448,14 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
 #pragma unroll
   for (int b = 0; b < NBA; ++b) qrow[b] = min(16 * b + row, nq > 0 ? nq - 1 : 0);
   const int nchunks = (d + WM_KC - 1) / WM_KC;
-  // a chunk's h and x rows: both 16-token blocks, the lane's two 8-column halves (clamped in bounds)
+  // a chunk's h and x rows: every 16-token block, the lane's two 8-column k-groups (clamped in bounds)
   auto load_hx = [&](int c, uint4 (&hr)[WM_MB][2], uint4 (&xr)[WM_MB][2]) {
-    const int col = c * WM_KC + quad * 16;
+    const int col = c * WM_KC + quad * WM_QS;
 #pragma unroll
     for (int mb = 0; mb < WM_MB; ++mb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        const int cc = col + 8 * hf < d ? col + 8 * hf : 0;
+        const int cc = col + WM_HS * hf < d ? col + WM_HS * hf : 0;
         hr[mb][hf] = *reinterpret_cast<const uint4*>(h + roff[mb] + cc);
         xr[mb][hf] = *reinterpret_cast<const uint4*>(x + roff[mb] + cc);
       }
@@ -459,13 +463,13 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
   uint4 hr[WM_MB][2], xr[WM_MB][2];
   if (w < nchunks) load_hx(w, hr, xr);
   for (int c = w; c < nchunks; c += 4) {   // wave-uniform trip count
-    const int col = c * WM_KC + quad * 16;
+    const int col = c * WM_KC + quad * WM_QS;
     bool col_ok[2];
     int cc[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      col_ok[hf] = col + 8 * hf < d;
-      cc[hf] = col_ok[hf] ? col + 8 * hf : 0;
+      col_ok[hf] = col + WM_HS * hf < d;
+      cc[hf] = col_ok[hf] ? col + WM_HS * hf : 0;
     }
     // the chunk's query parts (cache-resident), requested before the data is touched
     uint4 qv[3][NBA][2];
@@ -477,14 +481,20 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
         for (int hf = 0; hf < 2; ++hf)
           qv[p][b][hf] = *reinterpret_cast<const uint4*>(qb + p * qb_part_stride + (int64_t)qrow[b] * d + cc[hf]);
 
+    uint4 hc[WM_MB][2], xc[WM_MB][2];   // this chunk's rows; the next chunk's are requested now
+#pragma unroll
+    for (int mb = 0; mb < WM_MB; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) { hc[mb][hf] = hr[mb][hf]; xc[mb][hf] = xr[mb][hf]; }
+    if (c + 4 < nchunks) load_hx(c + 4, hr, xr);   // uniform branch
     uint4 va[WM_MB][2];
 #pragma unroll
     for (int mb = 0; mb < WM_MB; ++mb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         float hv[8], xv[8], vv[8];
-        IO<bf16_t>::unpack(IO<bf16_t>::Raw{hr[mb][hf]}, hv);
-        IO<bf16_t>::unpack(IO<bf16_t>::Raw{xr[mb][hf]}, xv);
+        IO<bf16_t>::unpack(IO<bf16_t>::Raw{hc[mb][hf]}, hv);
+        IO<bf16_t>::unpack(IO<bf16_t>::Raw{xc[mb][hf]}, xv);
         const bool ok = tok_ok[mb] && col_ok[hf];
 #pragma unroll
         for (int k = 0; k < 8; ++k) vv[k] = ok ? hv[k] - xv[k] : 0.f;
@@ -509,7 +519,6 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
             acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qh), acc[mb][b],
                                                                  0, 0, 0);
         }
-    if (c + 4 < nchunks) load_hx(c + 4, hr, xr);   // the next chunk's rows (uniform branch)
   }
 #pragma unroll
   for (int mb = 0; mb < WM_MB; ++mb) {
