@@ -88,7 +88,7 @@ class KernelTimer:
 
 def family_bytes(cfg, mode):
     """Compulsory HBM bytes per pass (T tokens) of each kernel family of this build -- what each kernel must move:
-    write 3 rows per token (h, x in; V out), read (n+2) (n sources, base in; out), scores online n, backward pass 1
+    write 3 rows per token (h, x in; V out), read (n+2) (n sources, base in; out; with online scores the same, in one pass), backward pass 1
     (n+1) (n sources, g), update gradient (m+3) (the m output gradients of the reads holding the update, the update,
     the result and its negation for the write's x) -- in rows of e * d bytes; per-(token, source) fp32 scalars left
     out (< 1 %). With the caller's glue in the stacked read, a read at an iteration end also reads h0, the update
@@ -104,9 +104,8 @@ def family_bytes(cfg, mode):
     row = e * cfg.d * T
     fused = mode != "list" and fuse_glue()
     ends = sum(1 for s in range(1, N) if s % cfg.K == cfg.K - 1) if fused else 0
-    fam = {"write_dots": 3 * N * row, "read_fwd": (S2 + 2 * (N - 1) + ends) * row}
-    if mode != "scores":
-        fam["dots_online"] = S2 * row
+    read = "read_fwd" if mode == "scores" else "read_fwd_online"   # online scores: formed in the same pass
+    fam = {"write_dots": 3 * N * row, read: (S2 + 2 * (N - 1) + ends) * row}
     if cfg.backward:
         fam["read_bwd1"] = (S2 + N - 1) * row
         fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 3 * N + (N - 1 if fused else 0)) * row

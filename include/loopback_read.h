@@ -102,6 +102,19 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
                  int64_t c0_cols, float lam, float inv_sqrt_d, void* out, float* tc, float* p, float* next_prior,
                  int64_t n_tok, int64_t d, int dtype, void* stream);
 
+/* The read step without stored scores, in one pass over the sources: the raw scores q . v_i are formed as the
+ * sources stream and stored into dots[i * dots_stride + tok] (for the backward; required), and the outputs are
+ * those of ldr_read_fwd on those scores (out up to fp32 summation order: the weighted sum runs as an online softmax
+ * against a running maximum; tc and p from the same softmax as ldr_read_fwd, so a zero query with cbar == c0 gives
+ * tc == c0 and out == base bitwise). q is the read's query, fp32 [d]. Rows wider than one wave (d > 2048 for bf16)
+ * take two passes inside the call (ldr_dots_online, then ldr_read_fwd). Replaces _dattn_fwd_stk_kernel
+ * (fused_dattn.py:410-456, the stacked read with LOOP_DATTN_DOTS=0) and the list layout's _dattn_fwd_kernel
+ * (55-108), each one pass over the sources. */
+int ldr_read_fwd_online(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* q, float* dots,
+                        int64_t dots_stride, const void* base, const void* h0, float beta, const float* cbar,
+                        int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, void* out,
+                        float* tc, float* p, float* next_prior, int64_t n_tok, int64_t d, int dtype, void* stream);
+
 /* Backward pass 1 of a read (the only re-read of the sources), with g = dL/dout, gt = dL/dtc (NULL = zeros), and
  * the forward's p and raw scores dots (as ldr_read_fwd took them):
  *   gd_i = g . v_i,  gp_i = M (gd_i + gt_i),  Sacc = sum_i p_i gp_i,  dz_i = p_i (gp_i - Sacc)

@@ -763,6 +763,213 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// read forward with online scores in one pass over the sources (rows inside one wave, tpr <= 64). Per token row and
+// source i: the raw score q . v_i (row sum), the logit l_i = score r_i inv + lc_i, and an online softmax against a
+// reference maximum m that moves only when a logit passes it by more than RF_LAZY (the running sums are then
+// rescaled): S = sum_i e_i and P = sum_i e_i v_i with e_i = exp(l_i - m), beside
+// acc = base + sum_i (c0_i - cbar_i - M p0_i) v_i (p0 = softmax(lc) is a per-read constant); at the row's end
+// out = acc + (M / S) P = base + sum_i (tc_i - cbar_i) v_i. A zero query is the exact case p = p0: the weights are
+// then c0_i - cbar_i and P is not formed, so a zero query with cbar == c0 gives out == base bitwise. tc and p come
+// from the row's logits at its end (the softmax of the stored-score read, so equal logits give tc == c0 bitwise);
+// the raw scores are stored for the backward.
+// ---------------------------------------------------------------------------------------------------------------
+#ifndef LDR_ON_WAVES
+#define LDR_ON_WAVES 2        // one-pass online read: waves per SIMD the registers must allow
+#endif
+constexpr float RF_LAZY = 8.f;   // e^8 < 3000: the running sums stay far from overflow between rescales
+
+// LDS written by some lanes of a wave and read by others of the same wave: complete the writes, keep the order
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <typename T, int VPT, bool BLEND, int PD>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LDR_ON_WAVES))) void k_read_online(SrcTab src, int n, const float* __restrict__ q,
+                                                    float* __restrict__ dots, int64_t dots_stride,
+                                                    const T* __restrict__ base, const T* __restrict__ h0, float beta,
+                                                    Coef cf, float inv, T* __restrict__ out, float* __restrict__ tc,
+                                                    float* __restrict__ prob, float* __restrict__ next_prior,
+                                                    int64_t n_tok, int d, int tpr) {
+  __shared__ float s_lg[WG / 8][MAXS];   // each row's logits (rows have at least 8 lanes)
+  __shared__ float s_wt[WG / 8][MAXS];   // each row's fixed weights
+  __shared__ float s_rs[WG / 8][MAXS];   // each row's source scales
+  __shared__ float s_c0[MAXS], s_lc[MAXS], s_p0[MAXS], s_M;
+  __shared__ __align__(16) float s_q[64 * 4 * 8];   // the query, zero past d (rows of <= 64 lanes x 4 vectors)
+  __shared__ int s_qnz;
+  using Raw = typename IO<T>::Raw;
+  const Rows R(d, tpr);
+  const int tid = (int)threadIdx.x;
+  if (tid == 0) s_qnz = 0;
+  load_prior(cf, n, s_c0, s_lc, &s_M);   // barriers inside: s_qnz is cleared before anyone sets it
+  const float M = s_M;
+  if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
+  bool nz = false;
+  for (int k = tid; k < 64 * 4 * 8; k += WG) {
+    const float x = k < d ? q[k] : 0.f;
+    s_q[k] = x;
+    nz |= x != 0.f;
+  }
+  if (nz) s_qnz = 1;   // every writer stores the same value
+  if (R.rs == 0) {     // p0 = softmax(lc), once per workgroup, by the row softmax
+    float p0[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int i = R.lr + m * tpr;
+      p0[m] = i < n ? s_lc[i] : -INFINITY;
+    }
+    softmax_lanes(p0, tpr);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int i = R.lr + m * tpr;
+      if (i < n) s_p0[i] = p0[m];
+    }
+  }
+  __syncthreads();
+  const bool qz = s_qnz == 0;   // workgroup-uniform
+  float* lg = s_lg[R.rs];
+  float* wt = s_wt[R.rs];
+  float* rsc = s_rs[R.rs];
+  const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
+  for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
+    const int64_t tok = gi * R.rpw + R.rs;
+    const bool valid = tok < n_tok;
+    const int64_t tk = valid ? tok : n_tok - 1;   // rows past the end recompute the last token, store nothing
+    const int64_t roff = tk * (int64_t)d;
+    for (int i = R.lr; i < n; i += tpr) {           // the row's per-source scalars, spread over its lanes
+      const float cb = coef_cbar(cf, tk, i);
+      wt[i] = qz ? s_c0[i] - cb : (s_c0[i] - cb) - M * s_p0[i];
+      rsc[i] = src.r[i][tk];
+    }
+    auto load_src = [&](int i, Raw (&rw)[VPT]) {
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) rw[v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i]) + roff + R.off(v));
+    };
+    Raw buf[PD][VPT];   // a ring of PD sources in flight: source i lives in buf[i % PD]
+#pragma unroll
+    for (int j = 0; j < PD; ++j)
+      if (j < n) load_src(j, buf[j]);
+    float acc[VPT][8], P[VPT][8];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) IO<T>::load(base + roff + R.off(v), acc[v]);
+    if (BLEND) {   // iteration end: base = proposal + beta (h0 - proposal), each step rounded as the caller's ops
+#pragma clang fp contract(off)   // three separately rounded operations, as torch runs them (no fused multiply-add)
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        float hv[8];
+        IO<T>::load(h0 + roff + R.off(v), hv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          acc[v][k] = IO<T>::round(acc[v][k] + IO<T>::round(beta * IO<T>::round(hv[k] - acc[v][k])));
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < VPT; ++v)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) P[v][k] = 0.f;
+    float S = 0.f, mref = -INFINITY;
+    wave_lds_sync();
+    auto dotq = [&](const Raw (&rw)[VPT]) {   // the query slice comes from LDS (no registers held for it)
+      asm volatile("" ::: "memory");           // read here, not hoisted out of the source loop into registers
+      float a = 0.f;
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        float e[8], qx[8];
+        IO<T>::unpack(rw[v], e);
+        const float4* qp = reinterpret_cast<const float4*>(s_q + R.c8(v) * 8);
+        const float4 q0 = qp[0], q1 = qp[1];
+        qx[0] = q0.x; qx[1] = q0.y; qx[2] = q0.z; qx[3] = q0.w;
+        qx[4] = q1.x; qx[5] = q1.y; qx[6] = q1.z; qx[7] = q1.w;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a += qx[k] * e[k];
+      }
+      return a;
+    };
+    // one source once its raw score is known: the logit, the online sums, the fixed-weight sum
+    auto take = [&](int i, float score, const Raw (&rw)[VPT]) {
+      const float l = score * rsc[i] * inv + s_lc[i];
+      if (R.lr == 0) {
+        lg[i] = l;
+        if (valid) dots[(int64_t)i * dots_stride + tok] = score;
+      }
+      float ex = 0.f;
+      if (!qz) {
+        if (l > mref + RF_LAZY) {   // first source (mref = -inf: a = 0 on zero sums), or a far larger logit
+          const float a = expf(mref - l);
+          S *= a;
+#pragma unroll
+          for (int v = 0; v < VPT; ++v)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) P[v][k] *= a;
+          mref = l;
+        }
+        ex = expf(l - mref);
+        S += ex;
+      }
+      const float w = wt[i];
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) {
+        float e[8];
+        IO<T>::unpack(rw[v], e);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (!qz) P[v][k] += ex * e[k];
+          acc[v][k] += w * e[k];
+        }
+      }
+    };
+    auto one = [&](int i, Raw (&rw)[VPT]) {   // source i, then its slot refilled with source i + PD
+      float pd[1] = {dotq(rw)};
+      row_sum<1>(pd, tpr, nullptr);
+      take(i, pd[0], rw);
+      if (i + PD < n) load_src(i + PD, rw);
+    };
+    int i0 = 0;
+    for (; i0 + PD <= n; i0 += PD) {
+#pragma unroll
+      for (int j = 0; j < PD; ++j) one(i0 + j, buf[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < PD; ++j)
+      if (i0 + j < n) one(i0 + j, buf[j]);
+    if (!qz) {
+      const float f = M / S;
+#pragma unroll
+      for (int v = 0; v < VPT; ++v)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[v][k] += f * P[v][k];
+    }
+    if (valid) {
+#pragma unroll
+      for (int v = 0; v < VPT; ++v)
+        if (R.act(v)) IO<T>::store(out + roff + R.c8(v) * 8, acc[v]);
+    }
+    wave_lds_sync();
+    float ps[8], p0[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int i = R.lr + m * tpr;
+      ps[m] = i < n ? lg[i] : -INFINITY;
+      p0[m] = i < n ? s_lc[i] : -INFINITY;
+    }
+    softmax_lanes(ps, tpr);
+    softmax_lanes(p0, tpr);
+    if (valid) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const int i = R.lr + m * tpr;
+        if (i < n) {
+          tc[tok * n + i] = s_c0[i] + M * (ps[m] - p0[m]);
+          if (prob) prob[tok * n + i] = ps[m];   // for the backward only
+        }
+      }
+    }
+    wave_lds_sync();   // this row's scalars are read before the next row overwrites them
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // backward pass 1: the only re-read of the sources
 // ---------------------------------------------------------------------------------------------------------------
 constexpr int B1_GRID = 512;
@@ -1277,6 +1484,11 @@ int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n) {
   else { typedef float T; __VA_ARGS__; }
 
 template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
+// one-pass online read: sources in flight per row (enough bytes in flight to cover the HBM latency)
+#ifndef LDR_ON_PD
+#define LDR_ON_PD 2           // one-pass online read: sources in flight per row at 3-4 vectors per lane
+#endif
+template <int VPT> struct OnlineDepth { static constexpr int PD = VPT <= 2 ? 2 * LDR_ON_PD : LDR_ON_PD; };
 // backward pass 1: sources per row reduction (one LDS exchange per chunk when a row spans two waves)
 template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_B1_C : (VPT == 1 ? 8 : VPT == 2 ? 4 : 1); };
 
@@ -1287,7 +1499,7 @@ template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 6; }
+int ldr_abi_version(void) { return 7; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -1437,6 +1649,46 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
                                                                     static_cast<const T*>(base), nullptr, beta, cf,
                                                                     inv_sqrt_d, static_cast<T*>(out), tc, p,
                                                                     next_prior, n_tok, (int)d, tpr, tt)))
+  }
+  return launched();
+}
+
+int ldr_read_fwd_online(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* q, float* dots,
+                        int64_t dots_stride, const void* base, const void* h0, float beta, const float* cbar,
+                        int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, void* out,
+                        float* tc, float* p, float* next_prior, int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (!src_r || !q || n_tok < 0 || !dots || dots_stride < n_tok || !base || !cbar || !c0 || !out || !tc)
+    return LDR_E_ARG;
+  if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1)) return LDR_E_ARG;
+  if (!al16(q) || !al16(base) || !al16(out) || (h0 && !al16(h0))) return LDR_E_ALIGN;
+  SrcTab s;
+  int e = fill_src(s, src_v, src_r, n);
+  if (e) return e;
+  int vpt, tpr;
+  if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, true, LDR_RF_VPT))) return e;
+  if (tpr > 64) {   // rows across waves: the scores first, then the stored-score read (two passes)
+    if ((e = ldr_dots_online(src_v, n, q, dots, dots_stride, n_tok, d, dtype, stream))) return e;
+    return ldr_read_fwd(src_v, src_r, n, dots, dots_stride, base, h0, beta, cbar, cbar_cols, c0, c0_cols, lam,
+                        inv_sqrt_d, out, tc, p, next_prior, n_tok, d, dtype, stream);
+  }
+  if (n_tok == 0) return LDR_OK;
+  const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 4096);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (h0) {
+    LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_online<T, VPT, true, OnlineDepth<VPT>::PD>),
+                                                                    dim3(grid), dim3(WG), 0, st, s, (int)n, q, dots,
+                                                                    dots_stride, static_cast<const T*>(base),
+                                                                    static_cast<const T*>(h0), beta, cf, inv_sqrt_d,
+                                                                    static_cast<T*>(out), tc, p, next_prior, n_tok,
+                                                                    (int)d, tpr)))
+  } else {
+    LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_online<T, VPT, false, OnlineDepth<VPT>::PD>),
+                                                                    dim3(grid), dim3(WG), 0, st, s, (int)n, q, dots,
+                                                                    dots_stride, static_cast<const T*>(base), nullptr,
+                                                                    beta, cf, inv_sqrt_d, static_cast<T*>(out), tc, p,
+                                                                    next_prior, n_tok, (int)d, tpr)))
   }
   return launched();
 }

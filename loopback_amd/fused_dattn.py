@@ -188,9 +188,8 @@ def _forward_impl(ctx, q, base, cbar, c0, srcs):
     dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
     vp = L.u64_array(v.data_ptr() for v in values)
     rp = L.u64_array(r.data_ptr() for r in rstds)
-    _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
-    _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base_c), _p(None), 0.0, _p(cbar_c), n, _p(c0c), n, 1.0,
-         _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
+    _run("read_fwd_online", vp, rp, n, _p(qc), _p(dots), n_tok, _p(base_c), _p(None), 0.0, _p(cbar_c), n, _p(c0c),
+         n, 1.0, _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
     if grad:
         ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc, *values, *rstds)
     ctx.n, ctx.q_dtype, ctx.base_shape = n, q.dtype, base.shape
@@ -530,11 +529,12 @@ class FusedDattnReadStk(torch.autograd.Function):
         vp, rp = stack.vptr, stack.rptr
         if stack.DOTS is not None and step >= 1 and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
             dots = stack.DOTS[step - 1]          # the stored scores of query step - 1, [source, token]
-        else:
+            _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base), _p(None), 0.0, _p(cbar_c), n, _p(c0c), n, 1.0,
+                 _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
+        else:                                    # online scores, formed (and kept for the backward) as it reads
             dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
-            _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
-        _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base), _p(None), 0.0, _p(cbar_c), n, _p(c0c), n, 1.0,
-             _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
+            _run("read_fwd_online", vp, rp, n, _p(qc), _p(dots), n_tok, _p(base), _p(None), 0.0, _p(cbar_c), n,
+                 _p(c0c), n, 1.0, _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
         if grad:
             ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc)
         ctx.stack, ctx.step, ctx.n, ctx.q_dtype, ctx.base_shape = stack, int(step), n, q.dtype, base.shape
@@ -608,14 +608,14 @@ class FusedCombineStk(torch.autograd.Function):
         prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
         next_prior = torch.empty(n, device=dev, dtype=torch.float32)
         vp, rp = stack.vptr, stack.rptr
+        blend = (_p(proposal), _p(h0 if at_boundary else None), float(beta), _p(coeffs_c), n - 1, _p(prior_c), n - 1,
+                 lam, _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(next_prior), n_tok, d, dt, st)
         if stack.DOTS is not None and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
             dots = stack.DOTS[step - 1]
+            _run("read_fwd", vp, rp, n, _p(dots), n_tok, *blend)
         else:
             dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
-            _run("dots_online", vp, n, _p(qc), _p(dots), n_tok, n_tok, d, dt, st)
-        _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(proposal), _p(h0 if at_boundary else None), float(beta),
-             _p(coeffs_c), n - 1, _p(prior_c), n - 1, lam, _inv_sqrt(d), _p(out), _p(tc), _p(prob),
-             _p(next_prior), n_tok, d, dt, st)
+            _run("read_fwd_online", vp, rp, n, _p(qc), _p(dots), n_tok, *blend)
         if grad:
             ctx.save_for_backward(qc, coeffs_c, prior_c, prob, dots, tc)
         ctx.stack, ctx.step, ctx.n, ctx.shape = stack, int(step), n, proposal.shape

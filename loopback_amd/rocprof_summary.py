@@ -20,7 +20,7 @@ import json
 import os
 import sys
 
-FAMILIES = [("k_read_fwd", "read_fwd"), ("k_bwd1", "read_bwd1"), ("k_dv_assemble", "dv_assemble"),
+FAMILIES = [("k_read_fwd", "read_fwd"), ("k_read_online", "read_fwd_online"), ("k_bwd1", "read_bwd1"), ("k_dv_assemble", "dv_assemble"),
             ("k_write_mfma", "write_dots"), ("k_write_dots", "write_dots"), ("k_dots", "dots_online"),
             ("k_reduce_rows", "reduce_rows"), ("k_split_queries", "split_queries"), ("k_rstd", "rstd"),
             ("k_bwd2_list", "read_bwd2_list"), ("k_blend_sum", "blend_sum")]

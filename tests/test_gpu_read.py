@@ -211,3 +211,61 @@ def test_accumulating_list_layout_matches_plain():
         results.append([v.grad.float().cpu() for v in vs])
     for a, b_ in zip(*results):
         assert err_max(a, b_) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,d,n", [(300, 2048, 31), (77, 768, 9), (41, 64, 64), (50, 1024, 3), (33, 3072, 5)])
+@pytest.mark.parametrize("boundary", [False, True])
+@pytest.mark.parametrize("q_std", [0.0, 0.05, 30.0])
+def test_one_pass_online_read_matches_two_passes(dtype, T, d, n, boundary, q_std):
+    """ldr_read_fwd_online (scores formed as the sources stream, an online softmax against a running maximum) against
+    ldr_dots_online + ldr_read_fwd on the same inputs, through the C ABI: the stored raw scores bitwise; tc and p to
+    fp32 round-off (their softmax is the same function over the same logits, spread over other lanes); out to the
+    fp32 bar (1e-5 x RMS; bf16: one rounding of an fp32 sum, so within 1 ulp of bf16 at |out|); a zero query gives
+    the two-pass out and tc bitwise (no online sum is formed; tc == c0). q_std 30 saturates the softmax (rescales of the running
+    sums); d = 3072 takes two passes inside the call (rows wider than a wave)."""
+    from loopback_amd import _lib as L
+    gen = torch.Generator().manual_seed(T * 7 + d + n + int(boundary) + int(q_std))
+    dt = L.BF16 if dtype == torch.bfloat16 else L.F32
+    vs = [torch.randn(T, d, generator=gen).to(dtype).to(DEV) for _ in range(n)]
+    rs = [torch.rsqrt(v.float().pow(2).mean(-1) + 1e-6).contiguous() for v in vs]
+    q = (torch.randn(d, generator=gen) * q_std).to(DEV)
+    base = torch.randn(T, d, generator=gen).to(dtype).to(DEV)
+    h0 = torch.randn(T, d, generator=gen).to(dtype).to(DEV) if boundary else None
+    cols = n - 1 if boundary else n
+    cbar = (torch.rand(T, cols, generator=gen) + 0.1).to(DEV)
+    c0 = (torch.rand(cols, generator=gen) + 0.1).to(DEV)
+    lam = 0.25 if boundary else 1.0
+    vp = L.u64_array(v.data_ptr() for v in vs)
+    rp = L.u64_array(r.data_ptr() for r in rs)
+    st = torch.cuda.current_stream().cuda_stream
+    res = []
+    for one_pass in (True, False):
+        out = torch.empty(T, d, dtype=dtype, device=DEV)
+        tc = torch.empty(T, n, device=DEV)
+        p = torch.empty(T, n, device=DEV)
+        npr = torch.empty(n, device=DEV)
+        dots = torch.full((n, T), float("nan"), device=DEV)
+        tail = (base.data_ptr(), h0.data_ptr() if boundary else None, 0.75, cbar.data_ptr(), cols, c0.data_ptr(),
+                cols, lam, d ** -0.5, out.data_ptr(), tc.data_ptr(), p.data_ptr(), npr.data_ptr(), T, d, dt, st)
+        if one_pass:
+            L.check(L.LIB.ldr_read_fwd_online(vp, rp, n, q.data_ptr(), dots.data_ptr(), T, *tail), "read_fwd_online")
+        else:
+            L.check(L.LIB.ldr_dots_online(vp, n, q.data_ptr(), dots.data_ptr(), T, T, d, dt, st), "dots_online")
+            L.check(L.LIB.ldr_read_fwd(vp, rp, n, dots.data_ptr(), T, *tail), "read_fwd")
+        torch.cuda.synchronize()
+        res.append((out, tc, p, npr, dots))
+    (o1, tc1, p1, np1, d1), (o2, tc2, p2, np2, d2) = res
+    assert torch.equal(d1, d2) and torch.equal(np1, np2)
+    assert torch.isfinite(o1.float()).all() and torch.isfinite(tc1).all()
+    assert (p1 - p2).abs().max().item() <= 1e-6
+    if q_std == 0.0:
+        assert torch.equal(o1, o2) and torch.equal(tc1, tc2)
+        return
+    assert (tc1 - tc2).abs().max().item() <= 1e-6 * tc2.abs().max().item()
+    if dtype == torch.float32:
+        assert err_rms(o1, o2) <= 1e-5
+    else:
+        a, b = o1.float(), o2.float()
+        scale = b.pow(2).mean().sqrt().item()
+        assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 2e-5 * scale).all()

@@ -103,6 +103,16 @@ def test_argument_checks_before_launch(lib):
     two = lib.u64_array([4096, 4096])
     assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 3, p, 2, 1.0, 0.125, p, p, p, null, 16, 64, 1,
                           null) == -1
+    # the one-pass online read needs the query and the score output (the backward's raw scores), both aligned
+    assert L.ldr_read_fwd_online(two, two, 2, null, p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.125, p, p, p, null, 16,
+                                 64, 1, null) == -1
+    assert L.ldr_read_fwd_online(two, two, 2, p, null, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.125, p, p, p, null, 16,
+                                 64, 1, null) == -1
+    assert L.ldr_read_fwd_online(two, two, 2, ctypes.c_void_p(4100), p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.125, p,
+                                 p, p, null, 16, 64, 1, null) == -3
+    for width in (2048, 8192):   # one pass (rows in one wave) and two (wider rows)
+        assert L.ldr_read_fwd_online(two, two, 2, p, p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.01, p, p, p, null, 0,
+                                     width, 1, null) == 0
     # the widest row (8192) is a shape every stacked entry point takes (no tokens: checked, nothing launched)
     assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, p, null, 0, 8192, 1, null) == 0
     assert L.ldr_blend_sum(one, 1, 0.5, p, 0, 8192, 1, null) == 0
