@@ -172,6 +172,36 @@ struct Rows {
   __device__ __forceinline__ int off(int v) const { const int c = c8(v); return (c < d8 ? c : d8 - 1) * 8; }
 };
 
+// Reduction over an aligned group of g lanes of a wave (g a power of two <= 64) in registers, without the LDS
+// crossbar: DPP (xor 1 and xor 2 inside quads, the 8- and 16-lane mirrors) and gfx950's row swaps
+// (v_permlane16_swap, v_permlane32_swap), the smallest level first. At each level both operands already hold equal
+// values across their halves, so every lane of the group ends with the same bits. All lanes of the wave must be
+// active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+template <typename Op>
+__device__ __forceinline__ float lanes_reduce(float x, int g, Op op) {
+  if (g >= 2) x = op(x, dpp_f<0xB1>(x));    // quad_perm [1, 0, 3, 2]
+  if (g >= 4) x = op(x, dpp_f<0x4E>(x));    // quad_perm [2, 3, 0, 1]
+  if (g >= 8) x = op(x, dpp_f<0x141>(x));   // row_half_mirror
+  if (g >= 16) x = op(x, dpp_f<0x140>(x));  // row_mirror
+  if (g >= 32) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto sw = __builtin_amdgcn_permlane16_swap(u, u, false, false);   // rows (0, 0, 2, 2) and (1, 1, 3, 3)
+    x = op(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
+  }
+  if (g >= 64) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);   // lower half twice, upper half twice
+    x = op(__builtin_bit_cast(float, (unsigned)sw[0]), __builtin_bit_cast(float, (unsigned)sw[1]));
+  }
+  return x;
+}
+struct AddOp { __device__ __forceinline__ float operator()(float a, float b) const { return a + b; } };
+struct MaxOp { __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+
 // Sum NV values over the tpr lanes of a row (tpr a power of two); every lane of the row ends with the totals,
 // bitwise equal on all of them. tpr <= 64: the row is an aligned lane group of one wave. tpr > 64: the row spans
 // tpr/64 waves and the wave totals meet in `red` (4 * NV floats of LDS); the whole workgroup must then call
@@ -179,10 +209,8 @@ struct Rows {
 template <int NV>
 __device__ __forceinline__ void row_sum(float (&x)[NV], int tpr, float* red) {
   const int w = tpr < 64 ? tpr : 64;
-  for (int off = w >> 1; off > 0; off >>= 1) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) x[j] += __shfl_xor(x[j], off, 64);
-  }
+  for (int j = 0; j < NV; ++j) x[j] = lanes_reduce(x[j], w, AddOp());
   if (tpr > 64) {
     const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
     __syncthreads();
@@ -201,25 +229,28 @@ __device__ __forceinline__ void row_sum(float (&x)[NV], int tpr, float* red) {
   }
 }
 
-// logsumexp of a token's n logits held by `lpt` aligned lanes (up to 8 each; unused slots are -inf): every lane
-// returns the same value. One code path for the scored and the prior-only logits, so equal inputs give bitwise
-// equal results (the zero-query identity tc == c0, out == base).
-// softmax over a token's logits spread over lpt lanes (8 each, -inf past n), in place: p = exp(l - max) / sum.
-// The division form (not exp(l - logsumexp)) keeps p within a few ulp, as torch's softmax computes it.
-__device__ __forceinline__ void softmax_lanes(float (&l)[8], int lpt) {
+// Softmax over a token's logits spread over lpt aligned lanes (slot m of lane j holds logit j + m lpt; -inf past n),
+// in place: p = exp(l - max) / sum. Only the first ns = ceil(n / lpt) slots can hold logits; the others are left 0
+// without work. The division form (not exp(l - logsumexp)) keeps p within a few ulp, as torch's softmax computes
+// it. One code path for the scored and the prior-only logits, so equal inputs give bitwise equal results (the
+// zero-query identity tc == c0, out == base).
+__device__ __forceinline__ void softmax_lanes(float (&l)[8], int lpt, int ns) {
   float mx = l[0];
 #pragma unroll
-  for (int m = 1; m < 8; ++m) mx = fmaxf(mx, l[m]);
-  for (int off = lpt >> 1; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  for (int m = 1; m < 8; ++m)
+    if (m < ns) mx = fmaxf(mx, l[m]);
+  mx = lanes_reduce(mx, lpt, MaxOp());
   float s = 0.f;
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    l[m] = (l[m] == -INFINITY) ? 0.f : expf(l[m] - mx);
-    s += l[m];
+    if (m < ns) {
+      l[m] = (l[m] == -INFINITY) ? 0.f : expf(l[m] - mx);
+      s += l[m];
+    }
   }
-  for (int off = lpt >> 1; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  s = lanes_reduce(s, lpt, AddOp());
 #pragma unroll
-  for (int m = 0; m < 8; ++m) l[m] = l[m] / s;
+  for (int m = 0; m < 8; ++m) l[m] = m < ns ? l[m] / s : 0.f;
 }
 
 // The coefficient inputs of a read. Either as the read takes them (cbar [tok][n], c0 [n], lam = 1), or -- fused
@@ -637,13 +668,28 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
                                                  int tt) {
   __shared__ float s_l[MAXS * (TT_MAX + 1)];   // logits [i][t]
   __shared__ float s_w[TT_MAX * SP];           // cbar, then the weights [t][i]
-  __shared__ float s_c0[MAXS], s_lc[MAXS], s_M;
+  __shared__ float s_c0[MAXS], s_lc[MAXS], s_p0[MAXS], s_M;
   const Rows R(d, tpr);
   const int tid = (int)threadIdx.x;
   load_prior(cf, n, s_c0, s_lc, &s_M);
   const float M = s_M;
   if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
   const int lpt = WG / tt;   // lanes per token in the softmax
+  const int ns = (n + lpt - 1) / lpt;
+  if (tid < lpt) {   // p0 = softmax(lc), a per-read constant: once, by the lanes of one token
+    float p0[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int i = tid + m * lpt;
+      p0[m] = (i < n) ? s_lc[i] : -INFINITY;
+    }
+    softmax_lanes(p0, lpt, ns);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int i = tid + m * lpt;
+      if (i < n) s_p0[i] = p0[m];
+    }
+  }
   const int64_t tiles = (n_tok + tt - 1) / tt;
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int64_t t0 = tile * tt;
@@ -663,20 +709,18 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
     {
       const int t = tid / lpt, j = tid - t * lpt;
       const int64_t tok = t0 + t;
-      float ps[8], p0[8];
+      float ps[8];
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int i = j + m * lpt;
         ps[m] = (i < n) ? s_l[i * (TT_MAX + 1) + t] : -INFINITY;
-        p0[m] = (i < n) ? s_lc[i] : -INFINITY;
       }
-      softmax_lanes(ps, lpt);
-      softmax_lanes(p0, lpt);
+      softmax_lanes(ps, lpt, ns);
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int i = j + m * lpt;
         if (i < n) {
-          const float tcv = s_c0[i] + M * (ps[m] - p0[m]);
+          const float tcv = s_c0[i] + M * (ps[m] - s_p0[i]);
           s_w[t * SP + i] = tcv - s_w[t * SP + i];
           if (tok < n_tok) {
             tc[tok * n + i] = tcv;
@@ -773,6 +817,12 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
 // from the row's logits at its end (the softmax of the stored-score read, so equal logits give tc == c0 bitwise);
 // the raw scores are stored for the backward.
 // ---------------------------------------------------------------------------------------------------------------
+#ifndef LDR_RF_GRID
+#define LDR_RF_GRID 512       // read forward: workgroups (2 per CU: all resident, each takes token tiles in turn)
+#endif
+#ifndef LDR_ON_GRID
+#define LDR_ON_GRID 512       // one-pass online read: workgroups (2 per CU: all resident, each takes rows in turn)
+#endif
 #ifndef LDR_ON_WAVES
 #define LDR_ON_WAVES 2        // one-pass online read: waves per SIMD the registers must allow
 #endif
@@ -812,14 +862,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LDR_ON_WAVES
     nz |= x != 0.f;
   }
   if (nz) s_qnz = 1;   // every writer stores the same value
-  if (R.rs == 0) {     // p0 = softmax(lc), once per workgroup, by the row softmax
+  const int ns = (n + tpr - 1) / tpr;
+  if (R.rs == 0) {     // p0 = softmax(lc), a per-read constant: once, by the lanes of one row
     float p0[8];
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       const int i = R.lr + m * tpr;
       p0[m] = i < n ? s_lc[i] : -INFINITY;
     }
-    softmax_lanes(p0, tpr);
+    softmax_lanes(p0, tpr, ns);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       const int i = R.lr + m * tpr;
@@ -946,21 +997,19 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LDR_ON_WAVES
         if (R.act(v)) IO<T>::store(out + roff + R.c8(v) * 8, acc[v]);
     }
     wave_lds_sync();
-    float ps[8], p0[8];
+    float ps[8];
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       const int i = R.lr + m * tpr;
       ps[m] = i < n ? lg[i] : -INFINITY;
-      p0[m] = i < n ? s_lc[i] : -INFINITY;
     }
-    softmax_lanes(ps, tpr);
-    softmax_lanes(p0, tpr);
+    softmax_lanes(ps, tpr, ns);
     if (valid) {
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int i = R.lr + m * tpr;
         if (i < n) {
-          tc[tok * n + i] = s_c0[i] + M * (ps[m] - p0[m]);
+          tc[tok * n + i] = s_c0[i] + M * (ps[m] - s_p0[i]);
           if (prob) prob[tok * n + i] = ps[m];   // for the backward only
         }
       }
@@ -1634,7 +1683,7 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
   if (n_tok == 0) return LDR_OK;
   const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
   const int tt = tile_tokens(tpr);
-  const unsigned grid = grid_of(cdiv(n_tok, tt), 65535);
+  const unsigned grid = grid_of(cdiv(n_tok, tt), LDR_RF_GRID);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (h0) {
     LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_fwd<T, VPT, true>), dim3(grid), dim3(WG), 0,
@@ -1674,7 +1723,7 @@ int ldr_read_fwd_online(const uint64_t* src_v, const uint64_t* src_r, int64_t n,
   }
   if (n_tok == 0) return LDR_OK;
   const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
-  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 4096);
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), LDR_ON_GRID);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (h0) {
     LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_online<T, VPT, true, OnlineDepth<VPT>::PD>),
