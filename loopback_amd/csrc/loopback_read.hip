@@ -817,6 +817,9 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
 // from the row's logits at its end (the softmax of the stored-score read, so equal logits give tc == c0 bitwise);
 // the raw scores are stored for the backward.
 // ---------------------------------------------------------------------------------------------------------------
+#ifndef LDR_AS_GRID
+#define LDR_AS_GRID 65535     // update gradient: most workgroups
+#endif
 #ifndef LDR_RF_GRID
 #define LDR_RF_GRID 512       // read forward: workgroups (2 per CU: all resident, each takes token tiles in turn)
 #endif
@@ -1021,7 +1024,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LDR_ON_WAVES
 // ---------------------------------------------------------------------------------------------------------------
 // backward pass 1: the only re-read of the sources
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int B1_GRID = 512;
+#ifndef LDR_B1_GRID
+#define LDR_B1_GRID 512
+#endif
+constexpr int B1_GRID = LDR_B1_GRID;
 constexpr int B1_MAX_VPT = LDR_B1_MAX_VPT;
 
 template <typename T, int VPT, int C>
@@ -1854,7 +1860,7 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
   if (e == LDR_E_SHAPE && !LDR_AS_VPT) e = row_layout(d, &vpt, &tpr, 4, false, 0, true);   // rows past 3 x 256 x 8
   if (e) return e;
   if (n_tok == 0) return LDR_OK;
-  const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * as_rb(vpt)), 65535);
+  const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * as_rb(vpt)), LDR_AS_GRID);
   hipStream_t st = static_cast<hipStream_t>(stream);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT>), dim3(grid), dim3(WG), 0, st,
                                                                   t, (int)m, static_cast<const T*>(v), r, gr,
