@@ -39,10 +39,23 @@ def _rows(path):
         return list(csv.DictReader(f))
 
 
+FWD_KERNELS = ("k_split_queries", "k_write_mfma", "k_write_dots", "k_rstd_fwd", "k_read_fwd", "k_read_online", "k_dots")
+BWD_KERNELS = ("k_bwd1", "k_dv_assemble", "k_reduce_rows", "k_blend_sum", "k_bwd2_list", "k_rstd_bwd")
+
+
 def _passes(rows, key="Start_Timestamp"):
-    """The rows of each chain pass, in launch order (a pass starts at its k_split_queries launch)."""
+    """The rows of each chain pass, in launch order. With stored scores a pass starts at its k_split_queries launch
+    (the stack's queries); otherwise at the first forward kernel of the library after a backward one."""
     rows = sorted(rows, key=lambda r: int(r[key]))
     starts = [i for i, r in enumerate(rows) if "k_split_queries" in r["Kernel_Name"]]
+    if not starts:
+        prev = None
+        for i, r in enumerate(rows):
+            name = r["Kernel_Name"]
+            kind = "f" if any(k in name for k in FWD_KERNELS) else "b" if any(k in name for k in BWD_KERNELS) else None
+            if kind == "f" and prev != "f":
+                starts.append(i)
+            prev = kind or prev
     return [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
 
 
@@ -138,6 +151,7 @@ def main(argv=None):
     fs = calibration(a.calib_fetch, "FETCH_SIZE")
     ws = calibration(a.calib_write, "WRITE_SIZE")
 
+    tag = a.config if a.mode == "scores" else f"{a.config}_{a.mode}"   # the headline mode keeps the plain name
     busy = sum(v[1] for v in kt.values()) / 1e3
     lines = [f"# Kernel time per chain pass: config {a.config} ({cfg.name}), mode {a.mode}", ""]
     if a.commands:
@@ -153,7 +167,7 @@ def main(argv=None):
                      f"{ab / 1e9:.2f} | {gbs} |" if ab else f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | - | - |")
     if a.stats:   # rocprofv3's own per-kernel summary over the whole run (warm-up and timed passes)
         lines += [""] + stats_table(a.stats, 12)
-    with open(os.path.join(a.out, f"kernels_chain_{a.config}.md"), "w") as f:
+    with open(os.path.join(a.out, f"kernels_chain_{tag}.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
 
     per_launch = {}
@@ -176,11 +190,11 @@ def main(argv=None):
                      f"{(fb + wb) / fam_bytes[famname]:.3f} | {per_launch[famname]:.0f} |")
     lines += ["", "Algorithmic bytes: the compulsory rows of each kernel family (bench.py `family_bytes`); per-(token, "
               "source) fp32 scalars are not counted, which is most of the excess."]
-    with open(os.path.join(a.out, f"traffic_chain_{a.config}.md"), "w") as f:
+    with open(os.path.join(a.out, f"traffic_chain_{tag}.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
-    with open(os.path.join(a.out, f"traffic_chain_{a.config}.txt"), "w") as f:
+    with open(os.path.join(a.out, f"traffic_chain_{tag}.txt"), "w") as f:
         json.dump({"config": a.config, "mode": a.mode,
-                   "source": f"profiles/traffic_chain_{a.config}.md (commands and calibration there)",
+                   "source": f"profiles/traffic_chain_{tag}.md (commands and calibration there)",
                    "fetch_scale": fs, "write_scale": ws, "hbm_bytes_per_launch": per_launch}, f, indent=1)
         f.write("\n")
 
