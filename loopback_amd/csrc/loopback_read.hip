@@ -119,12 +119,17 @@ template <> struct IO<bf16_t> {
     u.x = pack2(o[0], o[1]); u.y = pack2(o[2], o[3]); u.z = pack2(o[4], o[5]); u.w = pack2(o[6], o[7]);
     *reinterpret_cast<uint4*>(p) = u;
   }
-  // stores -o (rounded): the sign bits of the rounded values flipped, exact
-  static __device__ __forceinline__ void store_neg(bf16_t* p, const float (&o)[8]) {
-    uint4 u;
-    u.x = pack2(o[0], o[1]) ^ 0x80008000u; u.y = pack2(o[2], o[3]) ^ 0x80008000u;
-    u.z = pack2(o[4], o[5]) ^ 0x80008000u; u.w = pack2(o[6], o[7]) ^ 0x80008000u;
-    *reinterpret_cast<uint4*>(p) = u;
+  // non-temporal stores, for results not read again soon (the update gradients): they stream to HBM instead of
+  // displacing the rows the next launches re-read from the caches
+  static __device__ __forceinline__ void store_nt(bf16_t* p, const float (&o)[8]) {
+    const u32x4 u{pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7])};
+    __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(p));
+  }
+  // stores -o (rounded), non-temporal: the sign bits of the rounded values flipped, exact
+  static __device__ __forceinline__ void store_neg_nt(bf16_t* p, const float (&o)[8]) {
+    const u32x4 u{pack2(o[0], o[1]) ^ 0x80008000u, pack2(o[2], o[3]) ^ 0x80008000u,
+                  pack2(o[4], o[5]) ^ 0x80008000u, pack2(o[6], o[7]) ^ 0x80008000u};
+    __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(p));
   }
   static __device__ __forceinline__ float round(float x) { return (float)(__bf16)x; }
 };
@@ -144,14 +149,19 @@ template <> struct IO<float> {
     reinterpret_cast<float4*>(p)[0] = make_float4(o[0], o[1], o[2], o[3]);
     reinterpret_cast<float4*>(p)[1] = make_float4(o[4], o[5], o[6], o[7]);
   }
-  static __device__ __forceinline__ void store_neg(float* p, const float (&o)[8]) {
-    uint4 a, b;
-    a.x = __float_as_uint(o[0]) ^ 0x80000000u; a.y = __float_as_uint(o[1]) ^ 0x80000000u;
-    a.z = __float_as_uint(o[2]) ^ 0x80000000u; a.w = __float_as_uint(o[3]) ^ 0x80000000u;
-    b.x = __float_as_uint(o[4]) ^ 0x80000000u; b.y = __float_as_uint(o[5]) ^ 0x80000000u;
-    b.z = __float_as_uint(o[6]) ^ 0x80000000u; b.w = __float_as_uint(o[7]) ^ 0x80000000u;
-    reinterpret_cast<uint4*>(p)[0] = a;
-    reinterpret_cast<uint4*>(p)[1] = b;
+  static __device__ __forceinline__ void store_nt(float* p, const float (&o)[8]) {
+    __builtin_nontemporal_store(u32x4{__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                      __float_as_uint(o[3])}, reinterpret_cast<u32x4*>(p));
+    __builtin_nontemporal_store(u32x4{__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]),
+                                      __float_as_uint(o[7])}, reinterpret_cast<u32x4*>(p) + 1);
+  }
+  static __device__ __forceinline__ void store_neg_nt(float* p, const float (&o)[8]) {
+    __builtin_nontemporal_store(u32x4{__float_as_uint(o[0]) ^ 0x80000000u, __float_as_uint(o[1]) ^ 0x80000000u,
+                                      __float_as_uint(o[2]) ^ 0x80000000u, __float_as_uint(o[3]) ^ 0x80000000u},
+                                reinterpret_cast<u32x4*>(p));
+    __builtin_nontemporal_store(u32x4{__float_as_uint(o[4]) ^ 0x80000000u, __float_as_uint(o[5]) ^ 0x80000000u,
+                                      __float_as_uint(o[6]) ^ 0x80000000u, __float_as_uint(o[7]) ^ 0x80000000u},
+                                reinterpret_cast<u32x4*>(p) + 1);
   }
   static __device__ __forceinline__ float round(float x) { return x; }
 };
@@ -1456,12 +1466,12 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 #pragma unroll
         for (int x = 0; x < 8; ++x) acc[k][v][x] += c * e[v][x];
         if (tok[k] < n_tok && R.act(v)) {
-          if (dv_neg) IO<T>::store_neg(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
+          if (dv_neg) IO<T>::store_neg_nt(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
           if (add) {
 #pragma unroll
             for (int x = 0; x < 8; ++x) acc[k][v][x] = IO<T>::round(acc[k][v][x]) + a[v][x];
           }
-          IO<T>::store(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
+          IO<T>::store_nt(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
         }
       }
     }
