@@ -1422,7 +1422,7 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 #pragma unroll
         for (int k = 0; k < AS_RB; ++k)
 #pragma unroll
-          for (int v = 0; v < VPT; ++v) raw[b][k][v] = IO<T>::raw(gj + roff[k] + R.off(v));
+          for (int v = 0; v < VPT; ++v) raw[b][k][v] = IO<T>::raw_nt(gj + roff[k] + R.off(v));
 #pragma unroll
         for (int k = 0; k < AS_RB; ++k) sc[b][k] = *reinterpret_cast<const float2*>(tab.wz[j0 + b] + 2 * tokc[k]);
 #pragma unroll
