@@ -55,6 +55,24 @@
 #ifndef LDR_NT
 #define LDR_NT 1             // non-temporal loads for the streamed sources
 #endif
+#ifndef LDR_AS_GRID
+#define LDR_AS_GRID 65535    // update gradient: most workgroups
+#endif
+#ifndef LDR_RF_GRID
+#define LDR_RF_GRID 512      // read forward: workgroups (2 per CU: all resident, each takes token tiles in turn)
+#endif
+#ifndef LDR_ON_GRID
+#define LDR_ON_GRID 512      // one-pass online read: workgroups (2 per CU: all resident, each takes rows in turn)
+#endif
+#ifndef LDR_ON_WAVES
+#define LDR_ON_WAVES 2       // one-pass online read: waves per SIMD the registers must allow
+#endif
+#ifndef LDR_ON_PD
+#define LDR_ON_PD 2          // one-pass online read: sources in flight per row at 3-4 vectors per lane
+#endif
+#ifndef LDR_B1_GRID
+#define LDR_B1_GRID 512      // backward pass 1: workgroups (each takes token tiles in turn)
+#endif
 #ifndef LDR_RF_VPT
 #define LDR_RF_VPT 0         // fixed vectors per lane (0 = chosen from d) for the read forward,
 #endif
@@ -827,18 +845,6 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
 // from the row's logits at its end (the softmax of the stored-score read, so equal logits give tc == c0 bitwise);
 // the raw scores are stored for the backward.
 // ---------------------------------------------------------------------------------------------------------------
-#ifndef LDR_AS_GRID
-#define LDR_AS_GRID 65535     // update gradient: most workgroups
-#endif
-#ifndef LDR_RF_GRID
-#define LDR_RF_GRID 512       // read forward: workgroups (2 per CU: all resident, each takes token tiles in turn)
-#endif
-#ifndef LDR_ON_GRID
-#define LDR_ON_GRID 512       // one-pass online read: workgroups (2 per CU: all resident, each takes rows in turn)
-#endif
-#ifndef LDR_ON_WAVES
-#define LDR_ON_WAVES 2        // one-pass online read: waves per SIMD the registers must allow
-#endif
 constexpr float RF_LAZY = 8.f;   // e^8 < 3000: the running sums stay far from overflow between rescales
 
 // LDS written by some lanes of a wave and read by others of the same wave: complete the writes, keep the order
@@ -1034,9 +1040,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LDR_ON_WAVES
 // ---------------------------------------------------------------------------------------------------------------
 // backward pass 1: the only re-read of the sources
 // ---------------------------------------------------------------------------------------------------------------
-#ifndef LDR_B1_GRID
-#define LDR_B1_GRID 512
-#endif
 constexpr int B1_GRID = LDR_B1_GRID;
 constexpr int B1_MAX_VPT = LDR_B1_MAX_VPT;
 
@@ -1550,9 +1553,6 @@ int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n) {
 
 template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
 // one-pass online read: sources in flight per row (enough bytes in flight to cover the HBM latency)
-#ifndef LDR_ON_PD
-#define LDR_ON_PD 2           // one-pass online read: sources in flight per row at 3-4 vectors per lane
-#endif
 template <int VPT> struct OnlineDepth { static constexpr int PD = VPT <= 2 ? 2 * LDR_ON_PD : LDR_ON_PD; };
 // backward pass 1: sources per row reduction (one LDS exchange per chunk when a row spans two waves)
 template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_B1_C : (VPT == 1 ? 8 : VPT == 2 ? 4 : 1); };
