@@ -107,6 +107,19 @@ def stats_table(path, top):
         name = r["Name"].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:80]
         lines.append(f"| `{name}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.2f} | "
                      f"{float(r['AverageNs']) / 1e3:.1f} | {r['Percentage']} |")
+    fams = {}
+    for r in st:   # this library's kernels, whether or not they made the table
+        fam = family(r["Name"])
+        if fam != "torch / runtime":
+            f = fams.setdefault(fam, [0, 0.0])
+            f[0] += int(r["Calls"])
+            f[1] += float(r["TotalDurationNs"])
+    if fams:
+        lib = sum(v[1] for v in fams.values())
+        lines += ["", f"This library's kernels: {lib / 1e6:.2f} ms of the {total / 1e6:.1f} ms "
+                      f"({100 * lib / total:.1f} %).", "", "| kernel family | calls | total ms |", "|---|---|---|"]
+        for fam, (n, ns) in sorted(fams.items(), key=lambda x: -x[1][1]):
+            lines.append(f"| `{fam}` | {n} | {ns / 1e6:.2f} |")
     return lines
 
 
