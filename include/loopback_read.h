@@ -6,7 +6,9 @@
  * Conventions (every entry point):
  *   - device pointers are plain addresses of device memory; tensors are row-major and contiguous, one row of d
  *     elements per token; every vector pointer (updates, h, x, base, out, g, dv, q rows) is 16-byte aligned;
- *   - n_tok = b * t tokens, d the width (a multiple of 8, at most LDR_MAX_WIDTH);
+ *   - n_tok = b * t tokens, d the width (a multiple of 8, at most LDR_MAX_WIDTH); n_tok = 0 is a valid batch, for
+ *     which the token-sized buffers may be NULL (as empty tensors give them): nothing is read or written but the
+ *     per-read outputs (next_prior);
  *   - dtype is LDR_F32 or LDR_BF16 and applies to the update-shaped tensors (updates, base, out, g, dv, h, x);
  *     every scale, score, coefficient and gradient scalar is fp32;
  *   - per-source arrays (src_v, src_r, ...) are HOST arrays of n device addresses, copied into the kernel

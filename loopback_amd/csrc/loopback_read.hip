@@ -1514,6 +1514,8 @@ int row_layout(int64_t d, int* vpt, int* tpr, int max_vpt = 4, bool wave_rows = 
 
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool dtype_ok(int dt) { return dt == LDR_F32 || dt == LDR_BF16; }
+// a token-sized buffer: required, except that with no tokens it may be NULL (torch's empty tensors are)
+inline bool tok_ptr(const void* p, int64_t n_tok) { return p != nullptr || n_tok == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline unsigned grid_of(int64_t blocks, int64_t cap) { return (unsigned)(blocks < 1 ? 1 : (blocks < cap ? blocks : cap)); }
 inline int launched() { return (int)hipGetLastError(); }
@@ -1526,13 +1528,14 @@ inline int tile_tokens(int tpr) { const int rpw = WG / tpr; return rpw > 16 ? rp
 #endif
 inline int b1_tile(int tpr) { const int t = tile_tokens(tpr); return t > LDR_B1_TT ? t : LDR_B1_TT; }
 
-int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n) {
+int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n, int64_t n_tok) {
   if (!v || n < 1 || n > MAXS) return LDR_E_ARG;
   for (int64_t i = 0; i < n; ++i) {
     s.v[i] = reinterpret_cast<const void*>(v[i]);
-    if (!s.v[i] || !al16(s.v[i])) return s.v[i] ? LDR_E_ALIGN : LDR_E_ARG;
+    if (!tok_ptr(s.v[i], n_tok)) return LDR_E_ARG;
+    if (!al16(s.v[i])) return LDR_E_ALIGN;
     s.r[i] = r ? reinterpret_cast<const float*>(r[i]) : nullptr;
-    if (r && !s.r[i]) return LDR_E_ARG;
+    if (r && !tok_ptr(s.r[i], n_tok)) return LDR_E_ARG;
   }
   for (int64_t i = n; i < MAXS; ++i) { s.v[i] = nullptr; s.r[i] = nullptr; }
   return LDR_OK;
@@ -1590,7 +1593,7 @@ int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d) {
 
 int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (n_tok < 0 || !x || !r) return LDR_E_ARG;
+  if (n_tok < 0 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok)) return LDR_E_ARG;
   if (!al16(x)) return LDR_E_ALIGN;
   int vpt, tpr, e = row_layout(d, &vpt, &tpr);
   if (e) return e;
@@ -1605,7 +1608,8 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
 int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
                  void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (n_tok < 0 || !x || !r || !gr || !gx) return LDR_E_ARG;
+  if (n_tok < 0 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(gr, n_tok) || !tok_ptr(gx, n_tok))
+    return LDR_E_ARG;
   if (!al16(x) || !al16(gx)) return LDR_E_ALIGN;
   int vpt, tpr, e = row_layout(d, &vpt, &tpr);
   if (e) return e;
@@ -1622,9 +1626,11 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
                    int64_t qb_part_stride, float* dots, int64_t n_tok, int64_t d, int64_t nq, int64_t dots_jstride,
                    float eps, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (n_tok < 0 || !h || !x || !v_out || !r_out || nq < 0) return LDR_E_ARG;
+  if (n_tok < 0 || !tok_ptr(h, n_tok) || !tok_ptr(x, n_tok) || !tok_ptr(v_out, n_tok) || !tok_ptr(r_out, n_tok) ||
+      nq < 0)
+    return LDR_E_ARG;
   if (nq > LDR_MAX_QUERIES) return LDR_E_SHAPE;
-  if (nq > 0 && (!dots || dots_jstride < n_tok)) return LDR_E_ARG;
+  if (nq > 0 && (!tok_ptr(dots, n_tok) || dots_jstride < n_tok)) return LDR_E_ARG;
   if (nq > 0 && dtype == LDR_BF16 && (!qb || qb_part_stride < nq * d)) return LDR_E_ARG;
   if (nq > 0 && dtype == LDR_F32 && !q) return LDR_E_ARG;
   if (!al16(h) || !al16(x) || !al16(v_out) || (nq > 0 && q && !al16(q)) ||
@@ -1666,10 +1672,10 @@ int ldr_split_queries(const float* q, int64_t n, void* qb, void* stream) {
 int ldr_dots_online(const uint64_t* src_v, int64_t n, const float* q, float* out, int64_t out_stride,
                     int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (n_tok < 0 || !q || !out || out_stride < n_tok) return LDR_E_ARG;
+  if (n_tok < 0 || !q || !tok_ptr(out, n_tok) || out_stride < n_tok) return LDR_E_ARG;
   if (!al16(q)) return LDR_E_ALIGN;
   SrcTab s;
-  int e = fill_src(s, src_v, nullptr, n);
+  int e = fill_src(s, src_v, nullptr, n, n_tok);
   if (e) return e;
   int vpt, tpr;
   if ((e = row_layout(d, &vpt, &tpr))) return e;
@@ -1687,19 +1693,20 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
                  int64_t c0_cols, float lam, float inv_sqrt_d, void* out, float* tc, float* p, float* next_prior,
                  int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (!src_r || n_tok < 0 || !dots || dots_stride < n_tok || !base || !cbar || !c0 || !out || !tc)
+  if (!src_r || n_tok < 0 || !tok_ptr(dots, n_tok) || dots_stride < n_tok || !tok_ptr(base, n_tok) ||
+      !tok_ptr(cbar, n_tok) || !c0 || !tok_ptr(out, n_tok) || !tok_ptr(tc, n_tok))
     return LDR_E_ARG;
   if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1)) return LDR_E_ARG;
   if (!al16(base) || !al16(out) || (h0 && !al16(h0))) return LDR_E_ALIGN;
   SrcTab s;
-  int e = fill_src(s, src_v, src_r, n);
+  int e = fill_src(s, src_v, src_r, n, n_tok);
   if (e) return e;
   int vpt, tpr;
   if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, true, LDR_RF_VPT))) return e;
-  if (n_tok == 0) return LDR_OK;
+  if (n_tok == 0 && !next_prior) return LDR_OK;
   const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
   const int tt = tile_tokens(tpr);
-  const unsigned grid = grid_of(cdiv(n_tok, tt), LDR_RF_GRID);
+  const unsigned grid = grid_of(cdiv(n_tok, tt), LDR_RF_GRID);   // no tokens: one workgroup writes next_prior
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (h0) {
     LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_fwd<T, VPT, true>), dim3(grid), dim3(WG), 0,
@@ -1723,12 +1730,13 @@ int ldr_read_fwd_online(const uint64_t* src_v, const uint64_t* src_r, int64_t n,
                         int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, void* out,
                         float* tc, float* p, float* next_prior, int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (!src_r || !q || n_tok < 0 || !dots || dots_stride < n_tok || !base || !cbar || !c0 || !out || !tc)
+  if (!src_r || !q || n_tok < 0 || !tok_ptr(dots, n_tok) || dots_stride < n_tok || !tok_ptr(base, n_tok) ||
+      !tok_ptr(cbar, n_tok) || !c0 || !tok_ptr(out, n_tok) || !tok_ptr(tc, n_tok))
     return LDR_E_ARG;
   if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1)) return LDR_E_ARG;
   if (!al16(q) || !al16(base) || !al16(out) || (h0 && !al16(h0))) return LDR_E_ALIGN;
   SrcTab s;
-  int e = fill_src(s, src_v, src_r, n);
+  int e = fill_src(s, src_v, src_r, n, n_tok);
   if (e) return e;
   int vpt, tpr;
   if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, true, LDR_RF_VPT))) return e;
@@ -1737,7 +1745,7 @@ int ldr_read_fwd_online(const uint64_t* src_v, const uint64_t* src_r, int64_t n,
     return ldr_read_fwd(src_v, src_r, n, dots, dots_stride, base, h0, beta, cbar, cbar_cols, c0, c0_cols, lam,
                         inv_sqrt_d, out, tc, p, next_prior, n_tok, d, dtype, stream);
   }
-  if (n_tok == 0) return LDR_OK;
+  if (n_tok == 0 && !next_prior) return LDR_OK;   // no tokens: one workgroup writes next_prior
   const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
   const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), LDR_ON_GRID);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1765,21 +1773,21 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
                   const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride, float* dq_part, void* g_prop,
                   void* g_h0, float beta, int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (!src_r || n_tok < 0 || !g || !p || !dots || dots_stride < n_tok || !tc || !cbar || !c0 || !dcbar || !dr ||
-      !wz || !dq_part ||
-      wz_stride < n_tok || (dr_accum != 0 && dr_accum != 1))
+  if (!src_r || n_tok < 0 || !tok_ptr(g, n_tok) || !tok_ptr(p, n_tok) || !tok_ptr(dots, n_tok) ||
+      dots_stride < n_tok || !tok_ptr(tc, n_tok) || !tok_ptr(cbar, n_tok) || !c0 || !tok_ptr(dcbar, n_tok) || !dr ||
+      !tok_ptr(wz, n_tok) || !dq_part || wz_stride < n_tok || (dr_accum != 0 && dr_accum != 1))
     return LDR_E_ARG;
   if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1) || dcbar_cols < 0 ||
       dcbar_cols > n)
     return LDR_E_ARG;
   if (!al16(g) || (g_prop && !al16(g_prop)) || (g_h0 && !al16(g_h0))) return LDR_E_ALIGN;
   SrcTab s;
-  int e = fill_src(s, src_v, src_r, n);
+  int e = fill_src(s, src_v, src_r, n, n_tok);
   if (e) return e;
   PtrTab drt;
   for (int64_t i = 0; i < MAXS; ++i) {
     drt.p[i] = i < n ? reinterpret_cast<void*>(dr[i]) : nullptr;
-    if (i < n && !drt.p[i]) return LDR_E_ARG;
+    if (i < n && !tok_ptr(drt.p[i], n_tok)) return LDR_E_ARG;
   }
   int vpt, tpr;
   if ((e = row_layout(d, &vpt, &tpr, B1_MAX_VPT, LDR_B1_WAVE_ROWS, LDR_B1_VPT, true))) return e;
@@ -1810,12 +1818,12 @@ int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, void* out, int64_t n
                   void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (m < 1 || m > MAXS) return LDR_E_SHAPE;
-  if (!g || !out || n_tok < 0) return LDR_E_ARG;
+  if (!g || !tok_ptr(out, n_tok) || n_tok < 0) return LDR_E_ARG;
   if (!al16(out)) return LDR_E_ALIGN;
   PtrTab t;
   for (int64_t j = 0; j < MAXS; ++j) {
     t.p[j] = j < m ? reinterpret_cast<void*>(g[j]) : nullptr;
-    if (j < m && !t.p[j]) return LDR_E_ARG;
+    if (j < m && !tok_ptr(t.p[j], n_tok)) return LDR_E_ARG;
     if (j < m && !al16(t.p[j])) return LDR_E_ALIGN;
   }
   int vpt, tpr, e = row_layout(d, &vpt, &tpr);
@@ -1832,13 +1840,15 @@ int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, void* out, int64_t n
 int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, const float* q, const float* wz,
                        int64_t wz_stride, int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (!dv || n < 1 || n > MAXS || !g || !q || !wz || wz_stride < n_tok || n_tok < 0 || (accum != 0 && accum != 1))
+  if (!dv || n < 1 || n > MAXS || !tok_ptr(g, n_tok) || !q || !tok_ptr(wz, n_tok) || wz_stride < n_tok || n_tok < 0 ||
+      (accum != 0 && accum != 1))
     return n > MAXS ? LDR_E_SHAPE : LDR_E_ARG;
   if (!al16(g) || !al16(q)) return LDR_E_ALIGN;
   PtrTab t;
   for (int64_t i = 0; i < MAXS; ++i) {
     t.p[i] = i < n ? reinterpret_cast<void*>(dv[i]) : nullptr;
-    if (i < n && (!t.p[i] || !al16(t.p[i]))) return t.p[i] ? LDR_E_ALIGN : LDR_E_ARG;
+    if (i < n && !tok_ptr(t.p[i], n_tok)) return LDR_E_ARG;
+    if (i < n && !al16(t.p[i])) return LDR_E_ALIGN;
   }
   int vpt, tpr, e = row_layout(d, &vpt, &tpr);
   if (e) return e;
@@ -1856,14 +1866,15 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
                     int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (m < 0 || m > MAXS) return LDR_E_SHAPE;
-  if ((m > 0 && (!g || !wz || !q)) || !v || !r || !dv || n_tok < 0) return LDR_E_ARG;
+  if ((m > 0 && (!g || !wz || !q)) || !tok_ptr(v, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(dv, n_tok) || n_tok < 0)
+    return LDR_E_ARG;
   if (!al16(v) || !al16(dv) || (dv_neg && !al16(dv_neg)) || (add && !al16(add))) return LDR_E_ALIGN;
   AsmTab t;
   for (int64_t j = 0; j < MAXS; ++j) {
     t.g[j] = j < m ? reinterpret_cast<const void*>(g[j]) : nullptr;
     t.wz[j] = j < m ? reinterpret_cast<const float*>(wz[j]) : nullptr;
     t.q[j] = j < m ? reinterpret_cast<const float*>(q[j]) : nullptr;
-    if (j < m && (!t.g[j] || !t.wz[j] || !t.q[j])) return LDR_E_ARG;
+    if (j < m && (!tok_ptr(t.g[j], n_tok) || !tok_ptr(t.wz[j], n_tok) || !t.q[j])) return LDR_E_ARG;
     if (j < m && (!al16(t.g[j]) || !al16(t.q[j]) || (reinterpret_cast<uintptr_t>(t.wz[j]) & 7u))) return LDR_E_ALIGN;
   }
   int vpt, tpr, e = row_layout(d, &vpt, &tpr, LDR_AS_MAX_VPT, false, LDR_AS_VPT, true);

@@ -249,3 +249,52 @@ def test_kept_loss_holds_no_stack(mode):
     held, stack_bytes, kept = once()
     assert held < 0.05 * stack_bytes, (held, stack_bytes)
     del kept
+
+
+@pytest.mark.parametrize("mode", ["list", "stack", "scores"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_empty_token_batch(mode, dtype):
+    """A batch of no tokens ((1, 0, d)) through every layout, forward and backward: empty outputs and gradients of
+    the right shapes, and a zero query gradient (a sum over no tokens); no kernel runs on an empty grid."""
+    from loopback_amd.chain import ChainConfig, run_chain
+    cfg = ChainConfig("empty-K2R2", 64, 2, 2, 1, 0, dtype, True)
+    h0 = torch.zeros(1, 0, 64, dtype=dtype, device=DEV)
+    D = [torch.zeros(1, 0, 64, dtype=dtype, device=DEV) for _ in range(cfg.N)]
+    Q = torch.randn(cfg.N - 1, 64, device=DEV)
+    G = torch.zeros(1, 0, 64, device=DEV)
+    print(f"case empty {mode} {dtype}", flush=True)
+    h, loss, grads = run_chain(cfg, h0, D, Q, G, mode)
+    torch.cuda.synchronize()
+    assert h.shape == (1, 0, 64) and loss.item() == 0.0
+    assert grads["h0"].shape == (1, 0, 64) and all(g.shape == (1, 0, 64) for g in grads["D"])
+    assert torch.equal(grads["query"], torch.zeros_like(Q))
+
+
+@pytest.mark.parametrize("mode", ["list", "stack", "scores"])
+def test_empty_token_batch_priors(mode):
+    """With no tokens the read still hands back the next prior (the fused combine forms it in its kernel): every
+    step's prior equals the oracle cell's."""
+    from loopback_amd.cell import LoopDeltaAttnRes
+    from oracle.reference_read import OracleCell
+    K, R, d = 3, 2, 64
+    Q = torch.randn(K * R - 1, d)
+    cell = LoopDeltaAttnRes(d, R, K, beta=0.75, eps=1e-6).to(DEV)
+    with torch.no_grad():
+        cell.query.copy_(Q)
+    ocell = OracleCell(d, R, K, 0.75, 1e-6, Q.double())
+    h0 = torch.zeros(1, 0, d, device=DEV)
+    stack = cell.new_stack(h0.shape, h0.dtype, h0.device, mode=mode)
+    h, deltas, keys, coeffs, prior = h0, [], [], None, None
+    oh, odeltas, okeys, ocoeffs, oprior = h0.cpu().double(), [], [], None, None
+    with torch.no_grad():
+        for s in range(K * R):
+            l, blk = divmod(s, K)
+            x, ox = h, oh
+            hs, ohs = x + 0.0, ox + 0.0
+            deltas.append(stack.write(s, hs, x) if stack is not None else hs - x)
+            odeltas.append(ohs - ox)
+            h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
+            oh, ocoeffs, oprior = ocell.combine(ohs, h0.cpu().double(), odeltas, ocoeffs, oprior, l, blk, keys=okeys)
+            torch.cuda.synchronize()
+            assert coeffs.shape == (1, 0, s + 1)
+            assert torch.allclose(prior.cpu().double(), oprior, rtol=1e-6, atol=0), (s, prior, oprior)

@@ -122,3 +122,15 @@ def test_argument_checks_before_launch(lib):
                            null, 0.0, 0, 8192, 1, null) == 0
     # zero tokens: accepted, nothing launched
     assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 0, 64, 1e-6, 1, null) == 0
+    # ... also with the token-sized buffers NULL, as torch's empty tensors give them (never with tokens)
+    nulls = lib.u64_array([0, 0])
+    assert L.ldr_rstd_fwd(null, null, 0, 64, 1e-6, 1, null) == 0
+    assert L.ldr_rstd_fwd(null, null, 1, 64, 1e-6, 1, null) == -1
+    assert L.ldr_read_fwd(nulls, nulls, 2, null, 0, null, null, 0.0, null, 2, p, 2, 1.0, 0.125, null, null, null,
+                          null, 0, 64, 1, null) == 0
+    assert L.ldr_read_fwd(nulls, nulls, 2, null, 0, null, null, 0.0, null, 2, p, 2, 1.0, 0.125, null, null, null,
+                          null, 1, 64, 1, null) == -1
+    assert L.ldr_dv_assemble(lib.u64_array([0]), lib.u64_array([0]), one, 1, null, null, null, null, 0.0, null, null,
+                             0, 64, 1, null) == 0
+    assert L.ldr_read_bwd1(nulls, nulls, 2, null, null, null, null, 0, null, null, 2, p, 2, 1.0, 0.125, null, 2,
+                           nulls, 0, null, 0, p, null, null, 0.0, 0, 64, 1, null) == 0
