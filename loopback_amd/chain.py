@@ -118,13 +118,24 @@ def capture_forward(cfg: ChainConfig, h0, D, Q, mode: str):
     return graph, out
 
 
-def run_chain(cfg: ChainConfig, h0, D, Q, G, mode: str, grad: bool | None = None):
-    """One pass of the chain through the HIP read in `mode` ('scores', 'stack' or 'list'). Returns
-    (h_final, loss, grads) with grads = {'h0', 'D': [...], 'query'} when grad (default cfg.backward)."""
-    grad = cfg.backward if grad is None else grad
-    cell = LoopDeltaAttnRes(cfg.d, cfg.R, cfg.K, beta=cfg.beta, eps=cfg.eps).to(h0.device)
+def make_cell(cfg: ChainConfig, Q) -> LoopDeltaAttnRes:
+    """The chain's read cell with its query set to Q (on Q's device)."""
+    cell = LoopDeltaAttnRes(cfg.d, cfg.R, cfg.K, beta=cfg.beta, eps=cfg.eps).to(Q.device)
     with torch.no_grad():
         cell.query.copy_(Q)
+    return cell
+
+
+def run_chain(cfg: ChainConfig, h0, D, Q, G, mode: str, grad: bool | None = None, cell=None):
+    """One pass of the chain through the HIP read in `mode` ('scores', 'stack' or 'list'). Returns
+    (h_final, loss, grads) with grads = {'h0', 'D': [...], 'query'} when grad (default cfg.backward). `cell` (from
+    make_cell) is reused across passes, as a training loop keeps its model: its query gradient is reset each pass;
+    without one, a cell is made from Q."""
+    grad = cfg.backward if grad is None else grad
+    if cell is None:
+        cell = make_cell(cfg, Q)
+    else:
+        cell.query.grad = None
     h0 = h0.detach().requires_grad_(grad)
     D = [x.detach().requires_grad_(grad) for x in D]
     with torch.set_grad_enabled(grad):
