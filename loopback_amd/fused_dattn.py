@@ -21,7 +21,8 @@ Layouts:
   * stacked layout (DattnStack, FusedDattnReadStk): the updates of a pass in V[n_steps, b, t, d]. With the read
     queries, each write also stores the update's scores against every later read query, DOTS[j, i, tok]
     (query-major, then source, then token: coalesced for both the write and the read), and the reads form their
-    softmax from them. The stacked backward does not read-modify-write a gradient stack per read: each read's
+    softmax from them; without them (and in the list layout) a read forms the scores as it streams the sources,
+    with an online softmax, in one pass. The stacked backward does not read-modify-write a gradient stack per read: each read's
     backward keeps its output gradient g_s and its per-(source, token) scalars (w, dz r / sqrt(d)); the gradient of
     update i is formed once, when its scale's backward runs (after every read of it), as
     sum_s (w_si g_s + dzr_si q_s) + the scale's term, in fp32 with one rounding. Same gradients, at least as
@@ -34,7 +35,6 @@ Layouts:
 from __future__ import annotations
 
 import ctypes
-import math
 import weakref
 
 import torch
