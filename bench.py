@@ -92,9 +92,9 @@ def family_bytes(cfg, mode):
     (n+1) (n sources, g), update gradient (m+3) (the m output gradients of the reads holding the update, the update,
     the result and its negation for the write's x) -- in rows of e * d bytes; per-(token, source) fp32 scalars left
     out (< 1 %). With the caller's glue in the stacked read, a read at an iteration end also reads h0, the update
-    gradient of each update a read took as its proposal also reads that read's output gradient (and adds the
-    proposal's share, the add autograd would otherwise run), and the iteration ends' shares of h0's gradient are
-    summed once (blend_sum: one output gradient per iteration end in, one row out).
+    gradient of each update a read took as its proposal adds the proposal's share (the add autograd would otherwise
+    run) from that read's output gradient, which it reads anyway, and the iteration ends' shares of h0's gradient
+    are summed once (blend_sum: one output gradient per iteration end in, one row out).
     Also the reference dataflow's total (the formula of the survey), which moves more in its backward."""
     from loopback_amd.cell import fuse_glue
     from loopback_amd.chain import algorithmic_bytes_per_token
@@ -108,7 +108,7 @@ def family_bytes(cfg, mode):
     fam = {"write_dots": 3 * N * row, read: (S2 + 2 * (N - 1) + ends) * row}
     if cfg.backward:
         fam["read_bwd1"] = (S2 + N - 1) * row
-        fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 3 * N + (N - 1 if fused else 0)) * row
+        fam["dv_assemble"] = ((N - 1) + N * (N - 1) // 2 + 3 * N) * row
         if ends:
             fam["blend_sum"] = (ends + 1) * row
     ref_total = algorithmic_bytes_per_token(N, cfg.d, e, backward=cfg.backward, dots=(mode == "scores"))["total"] * T

@@ -1388,7 +1388,7 @@ __global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, c
 constexpr int as_rb(int vpt) { return vpt >= 3 ? 2 : LDR_AS_RB; }
 constexpr int AS_JB = LDR_AS_JB;   // reads per batch of loads
 
-template <typename T, int VPT>
+template <typename T, int VPT, bool ADD_LAST>   // ADD_LAST: add is the output gradient of the last read in tab
 __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* __restrict__ vsrc,
                                                     const float* __restrict__ r, const float* __restrict__ gr,
                                                     const T* __restrict__ add, float add_beta,
@@ -1413,6 +1413,21 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
       for (int v = 0; v < VPT; ++v)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[k][v][e] = 0.f;
+    // one read's share: w g + dzr q for the tile's rows, as two explicit fused multiply-adds (so every kernel
+    // variant and every read accumulate with the same roundings, whatever the compiler would contract)
+    auto take_row = [&](const typename IO<T>::Raw (&raw)[AS_RB][VPT], const float2 (&sc)[AS_RB],
+                        const float (&qv)[VPT][8]) {
+#pragma unroll
+      for (int k = 0; k < AS_RB; ++k)
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+          float e[8];
+          IO<T>::unpack(raw[k][v], e);
+#pragma unroll
+          for (int x = 0; x < 8; ++x)
+            acc[k][v][x] = __builtin_fmaf(sc[k].y, qv[v][x], __builtin_fmaf(sc[k].x, e[x], acc[k][v][x]));
+        }
+    };
     // JB reads per batch: their g rows (and query columns) are all in flight before the first multiply-add
     auto batch = [&](int j0, auto jb_tag) {
       constexpr int JB = decltype(jb_tag)::value;
@@ -1432,20 +1447,27 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
         for (int v = 0; v < VPT; ++v) load_f32x8(tab.q[j0 + b] + R.off(v), qv[b][v]);
       }
 #pragma unroll
-      for (int b = 0; b < JB; ++b)
-#pragma unroll
-        for (int k = 0; k < AS_RB; ++k)
-#pragma unroll
-          for (int v = 0; v < VPT; ++v) {
-            float e[8];
-            IO<T>::unpack(raw[b][k][v], e);
-#pragma unroll
-            for (int x = 0; x < 8; ++x) acc[k][v][x] += sc[b][k].x * e[x] + sc[b][k].y * qv[b][v][x];
-          }
+      for (int b = 0; b < JB; ++b) take_row(raw[b], sc[b], qv[b]);
     };
+    const int mm = ADD_LAST ? m - 1 : m;
     int j = 0;
-    for (; j + AS_JB <= m; j += AS_JB) batch(j, std::integral_constant<int, AS_JB>());
-    for (; j < m; ++j) batch(j, std::integral_constant<int, 1>());
+    for (; j + AS_JB <= mm; j += AS_JB) batch(j, std::integral_constant<int, AS_JB>());
+    for (; j < mm; ++j) batch(j, std::integral_constant<int, 1>());
+    typename IO<T>::Raw last[AS_RB][VPT];   // ADD_LAST: the last read's rows, kept for the added gradient
+    if (ADD_LAST) {
+      const T* gj = static_cast<const T*>(tab.g[m - 1]);
+      float2 sc[AS_RB];
+      float qv[VPT][8];
+#pragma unroll
+      for (int k = 0; k < AS_RB; ++k)
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) last[k][v] = IO<T>::raw_nt(gj + roff[k] + R.off(v));
+#pragma unroll
+      for (int k = 0; k < AS_RB; ++k) sc[k] = *reinterpret_cast<const float2*>(tab.wz[m - 1] + 2 * tokc[k]);
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) load_f32x8(tab.q[m - 1] + R.off(v), qv[v]);
+      take_row(last, sc, qv);
+    }
 #pragma unroll
     for (int k = 0; k < AS_RB; ++k) {
       const float rv = r[tokc[k]];
@@ -1454,8 +1476,13 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 #pragma unroll
       for (int v = 0; v < VPT; ++v) IO<T>::load(vsrc + roff[k] + R.off(v), e[v]);
       if (add) {   // a gradient of the write's h from elsewhere, added as autograd would add it
+        if (ADD_LAST) {   // the rows already in registers
 #pragma unroll
-        for (int v = 0; v < VPT; ++v) IO<T>::load(add + roff[k] + R.off(v), a[v]);
+          for (int v = 0; v < VPT; ++v) IO<T>::unpack(last[k][v], a[v]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) IO<T>::load(add + roff[k] + R.off(v), a[v]);
+        }
         if (add_beta != 0.f) {   // add is the output gradient g of an iteration-end blend: its proposal's share
 #pragma clang fp contract(off)
 #pragma unroll
@@ -1467,7 +1494,7 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
 #pragma unroll
-        for (int x = 0; x < 8; ++x) acc[k][v][x] += c * e[v][x];
+        for (int x = 0; x < 8; ++x) acc[k][v][x] = __builtin_fmaf(c, e[v][x], acc[k][v][x]);
         if (tok[k] < n_tok && R.act(v)) {
           if (dv_neg) IO<T>::store_neg_nt(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
           if (add) {
@@ -1883,12 +1910,21 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
   if (n_tok == 0) return LDR_OK;
   const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * as_rb(vpt)), LDR_AS_GRID);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT>), dim3(grid), dim3(WG), 0, st,
-                                                                  t, (int)m, static_cast<const T*>(v), r, gr,
-                                                                  static_cast<const T*>(add), add_beta,
-                                                                  static_cast<T*>(dv),
-                                                                  static_cast<T*>(dv_neg), n_tok,
-                                                                  (int)d, tpr)))
+  // the added gradient is often the last read's output gradient itself (the proposal of that read is this write's
+  // h): then its rows are read once
+  const bool add_last = add && m > 0 && add == t.g[m - 1];
+#define LDR_AS_LAUNCH(AL)                                                                                         \
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT, AL>), dim3(grid), dim3(WG), 0, \
+                                                                  st, t, (int)m, static_cast<const T*>(v), r, gr,  \
+                                                                  static_cast<const T*>(add), add_beta,            \
+                                                                  static_cast<T*>(dv), static_cast<T*>(dv_neg),    \
+                                                                  n_tok, (int)d, tpr)))
+  if (add_last) {
+    LDR_AS_LAUNCH(true)
+  } else {
+    LDR_AS_LAUNCH(false)
+  }
+#undef LDR_AS_LAUNCH
   return launched();
 }
 

@@ -480,6 +480,9 @@ class _RstdStk(torch.autograd.Function):
             raise RuntimeError("delta_attnres stacked read: the scale's backward ran before any read's backward")
         xc = x.contiguous()
         reads = sorted(k for k in stack.bwd if k >= max(s, 1))     # the reads of update s whose backward ran
+        if s in reads:   # read s last: when its output gradient is also the added one, the kernel loads it once
+            reads.remove(s)
+            reads.append(s)
         dv = torch.empty_like(xc)
         dv_neg = torch.empty_like(xc)
         grc = None if gr is None else gr.float().contiguous()
