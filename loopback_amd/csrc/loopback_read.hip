@@ -1103,7 +1103,7 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
       typename IO<T>::Raw gq[VPT];   // g kept packed, unpacked where used
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
-        gq[v] = IO<T>::raw_nt(g + roff + R.off(v));
+        gq[v] = IO<T>::raw(g + roff + R.off(v));   // just written by the caller: cached, not streamed
         if (!R.act(v)) gq[v] = IO<T>::zero();
       }
 #define LDR_GV(v, arr) float arr[8]; IO<T>::unpack(gq[v], arr);
@@ -1111,7 +1111,7 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
       float gv[VPT][8];
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
-        IO<T>::unpack(IO<T>::raw_nt(g + roff + R.off(v)), gv[v]);
+        IO<T>::unpack(IO<T>::raw(g + roff + R.off(v)), gv[v]);
         if (!R.act(v)) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) gv[v][k] = 0.f;
@@ -1461,7 +1461,7 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 #pragma unroll
       for (int k = 0; k < AS_RB; ++k)
 #pragma unroll
-        for (int v = 0; v < VPT; ++v) last[k][v] = IO<T>::raw_nt(gj + roff[k] + R.off(v));
+        for (int v = 0; v < VPT; ++v) last[k][v] = IO<T>::raw(gj + roff[k] + R.off(v));   // backward pass 1 just read it
 #pragma unroll
       for (int k = 0; k < AS_RB; ++k) sc[k] = *reinterpret_cast<const float2*>(tab.wz[m - 1] + 2 * tokc[k]);
 #pragma unroll
