@@ -564,7 +564,9 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
         IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);   // the stored (rounded) update
 #pragma unroll
         for (int k = 0; k < 8; ++k) ss[mb] += rv[k] * rv[k];
-        if (ok) *reinterpret_cast<uint4*>(v + roff[mb] + cc[hf]) = u;
+        // non-temporal: the read that follows streams V[s] with its other sources, and dirty cached lines would be
+        // written back in the middle of its stream
+        if (ok) __builtin_nontemporal_store(u32x4{u.x, u.y, u.z, u.w}, reinterpret_cast<u32x4*>(v + roff[mb] + cc[hf]));
       }
 #pragma unroll
     for (int p = 0; p < 3 * (NB > 0); ++p)
