@@ -269,3 +269,62 @@ def test_one_pass_online_read_matches_two_passes(dtype, T, d, n, boundary, q_std
         a, b = o1.float(), o2.float()
         scale = b.pow(2).mean().sqrt().item()
         assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 2e-5 * scale).all()
+
+
+@pytest.mark.parametrize("order", ["rising", "falling", "alternating"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_online_read_rescale_paths(order, dtype):
+    """The one-pass online read against the two-pass read (C ABI) when every source moves the running maximum:
+    sources v_i = cos(t_i) u + sin(t_i) w with u along the query and w orthogonal to it give logits |q| cos(t_i)
+    (the RMS scale removes the magnitude), here spread over [-120, 120] rising, falling or alternating across 31
+    sources, so the reference maximum moves (and the sums are rescaled) at most sources, or never after the first."""
+    from loopback_amd import _lib as L
+    T, d, n = 64, 1024, 31
+    gen = torch.Generator().manual_seed(5)
+    qdir = torch.randn(d, generator=gen)
+    qdir /= qdir.norm()
+    w = torch.randn(T, d, generator=gen)
+    w -= (w @ qdir)[:, None] * qdir[None, :]
+    w /= w.norm(dim=1, keepdim=True)
+    zs = torch.linspace(-0.99, 0.99, n)
+    if order == "falling":
+        zs = zs.flip(0)
+    elif order == "alternating":
+        zs = torch.stack([zs[: (n + 1) // 2], torch.cat([zs[(n + 1) // 2:], zs[:1]])], 1).flatten()[:n]
+    vs = [((c * qdir[None, :] + (1 - c * c) ** 0.5 * w) * (1.0 + 0.1 * i)).to(dtype).to(DEV)
+          for i, c in enumerate(zs.tolist())]
+    rs = [torch.rsqrt(v.float().pow(2).mean(-1) + 1e-6).contiguous() for v in vs]
+    q = (qdir * 120.0).to(DEV)   # r (q . v) / sqrt(d) = |q| cos t_i r |v| / sqrt(d) = 120 cos t_i (r |v| = sqrt(d))
+    base = torch.randn(T, d, generator=gen).to(dtype).to(DEV)
+    cbar = (torch.rand(T, n, generator=gen) + 0.1).to(DEV)
+    c0 = (torch.rand(n, generator=gen) + 0.1).to(DEV)
+    dt = L.BF16 if dtype == torch.bfloat16 else L.F32
+    vp = L.u64_array(v.data_ptr() for v in vs)
+    rp = L.u64_array(r.data_ptr() for r in rs)
+    st = torch.cuda.current_stream().cuda_stream
+    res = []
+    for one_pass in (True, False):
+        out = torch.empty(T, d, dtype=dtype, device=DEV)
+        tc = torch.empty(T, n, device=DEV)
+        p = torch.empty(T, n, device=DEV)
+        dots = torch.empty(n, T, device=DEV)
+        tail = (base.data_ptr(), None, 0.0, cbar.data_ptr(), n, c0.data_ptr(), n, 1.0, d ** -0.5, out.data_ptr(),
+                tc.data_ptr(), p.data_ptr(), None, T, d, dt, st)
+        if one_pass:
+            L.check(L.LIB.ldr_read_fwd_online(vp, rp, n, q.data_ptr(), dots.data_ptr(), T, *tail), "read_fwd_online")
+        else:
+            L.check(L.LIB.ldr_dots_online(vp, n, q.data_ptr(), dots.data_ptr(), T, T, d, dt, st), "dots_online")
+            L.check(L.LIB.ldr_read_fwd(vp, rp, n, dots.data_ptr(), T, *tail), "read_fwd")
+        torch.cuda.synchronize()
+        res.append((out, tc, p, dots))
+    (o1, tc1, p1, d1), (o2, tc2, p2, d2) = res
+    z = d1 * torch.stack(rs) * d ** -0.5
+    assert z.max().item() > 100 and z.min().item() < -100   # the logits do span the range
+    assert torch.equal(d1, d2)
+    assert torch.isfinite(o1.float()).all() and (p1 - p2).abs().max().item() <= 1e-6
+    if dtype == torch.float32:
+        assert err_rms(o1, o2) <= 1e-5
+    else:
+        a, b = o1.float(), o2.float()
+        scale = b.pow(2).mean().sqrt().item()
+        assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 2e-5 * scale).all()
