@@ -124,7 +124,9 @@ int ldr_read_fwd_online(const uint64_t* src_v, const uint64_t* src_r, int64_t n,
  *     previous coefficients through the caller's bookkeeping)
  *   dr_i[tok] (+)= dz_i dots_i inv_sqrt_d   (= dz_i z_i / r_i; added when dr_accum != 0)
  *   wz[(i * wz_stride + tok) * 2 + {0,1}] = (tc_i - cbar_i, dz_i r_i inv_sqrt_d)   (the pass-2 scalars)
- *   dq_part[p, :] = per-workgroup partial of sum_tok sum_i dz_i r_i v_i inv_sqrt_d  (ldr_read_bwd1_parts rows)
+ *   dq_part[p * dq_part_stride + c] = per-workgroup partial of sum_tok sum_i dz_i r_i v_i inv_sqrt_d
+ *     (ldr_read_bwd1_parts rows p; dq_part_stride >= d: with a stride of k d, k reads' partials interleave as
+ *     [p][read][d] and one ldr_reduce_rows over rows of k d sums them all)
  *   with g_prop and / or g_h0 (each may be NULL): the iteration-end blend's gradients g_h0 = round(beta g),
  *     g_prop = round(g - g_h0), rounded as autograd rounds them
  * Replaces _dattn_bwd1_stk_kernel (fused_dattn.py:459-493, launched at 777-779) and pass 1 of _dattn_bwd_kernel
@@ -133,8 +135,8 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
                   const float* p, const float* dots, int64_t dots_stride, const float* tc, const float* cbar,
                   int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, float* dcbar,
                   int64_t dcbar_cols, const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride,
-                  float* dq_part, void* g_prop, void* g_h0, float beta, int64_t n_tok, int64_t d, int dtype,
-                  void* stream);
+                  float* dq_part, int64_t dq_part_stride, void* g_prop, void* g_h0, float beta, int64_t n_tok,
+                  int64_t d, int dtype, void* stream);
 
 /* out[c] = sum_p part[p * d + c] in a fixed order (deterministic).
  * Replaces the torch dq_part.sum(0) (fused_dattn.py:317, 785). */

@@ -857,12 +857,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 template <typename T, int VPT, bool BLEND, int PD>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LDR_ON_WAVES))) void k_read_online(SrcTab src, int n, const float* __restrict__ q,
-                                                    float* __restrict__ dots, int64_t dots_stride,
-                                                    const T* __restrict__ base, const T* __restrict__ h0, float beta,
-                                                    Coef cf, float inv, T* __restrict__ out, float* __restrict__ tc,
-                                                    float* __restrict__ prob, float* __restrict__ next_prior,
-                                                    int64_t n_tok, int d, int tpr) {
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LDR_ON_WAVES)))
+void k_read_online(SrcTab src, int n, const float* __restrict__ q, float* __restrict__ dots, int64_t dots_stride,
+                   const T* __restrict__ base, const T* __restrict__ h0, float beta, Coef cf, float inv,
+                   T* __restrict__ out, float* __restrict__ tc, float* __restrict__ prob,
+                   float* __restrict__ next_prior, int64_t n_tok, int d, int tpr) {
   __shared__ float s_lg[WG / 8][MAXS];   // each row's logits (rows have at least 8 lanes)
   __shared__ float s_wt[WG / 8][MAXS];   // each row's fixed weights
   __shared__ float s_rs[WG / 8][MAXS];   // each row's source scales
@@ -1051,6 +1050,7 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
                                              int64_t dots_stride, const float* __restrict__ tcp, Coef cf, float inv,
                                              float* __restrict__ dcbar, int dcbar_cols, PtrTab dr, int dr_accum,
                                              float* __restrict__ wz, int64_t wz_stride, float* __restrict__ dq_part,
+                                             int64_t dq_stride,
                                              T* __restrict__ g_prop, T* __restrict__ g_h0, float beta, int64_t n_tok,
                                              int d, int tpr, int tt) {
   // LDS: six [TT_MAX][SP] scalar planes (probability, scale, upstream tc gradient, g.v, raw score then dr, and
@@ -1279,7 +1279,7 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
     }
     __syncthreads();
   }
-  for (int c = tid; c < d; c += WG) dq_part[(int64_t)blockIdx.x * d + c] = s_dq[c];
+  for (int c = tid; c < d; c += WG) dq_part[(int64_t)blockIdx.x * dq_stride + c] = s_dq[c];
 }
 
 // out[c] = sum_p part[p][c]: 16 columns per workgroup, 16 row groups (rows p = group mod 16) added in a fixed order
@@ -1596,7 +1596,7 @@ template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 7; }
+int ldr_abi_version(void) { return 8; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -1799,12 +1799,14 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
                   const float* p, const float* dots, int64_t dots_stride, const float* tc, const float* cbar,
                   int64_t cbar_cols,
                   const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, float* dcbar, int64_t dcbar_cols,
-                  const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride, float* dq_part, void* g_prop,
+                  const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride, float* dq_part,
+                  int64_t dq_part_stride, void* g_prop,
                   void* g_h0, float beta, int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (!src_r || n_tok < 0 || !tok_ptr(g, n_tok) || !tok_ptr(p, n_tok) || !tok_ptr(dots, n_tok) ||
       dots_stride < n_tok || !tok_ptr(tc, n_tok) || !tok_ptr(cbar, n_tok) || !c0 || !tok_ptr(dcbar, n_tok) || !dr ||
-      !tok_ptr(wz, n_tok) || !dq_part || wz_stride < n_tok || (dr_accum != 0 && dr_accum != 1))
+      !tok_ptr(wz, n_tok) || !dq_part || wz_stride < n_tok || dq_part_stride < d ||
+      (dr_accum != 0 && dr_accum != 1))
     return LDR_E_ARG;
   if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1) || dcbar_cols < 0 ||
       dcbar_cols > n)
@@ -1829,7 +1831,7 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
                                                                   dim3(WG), 0, st, s, (int)n, static_cast<const T*>(g),
                                                                   gt, p, dots, dots_stride, tc, cf, inv_sqrt_d, dcbar,
                                                                   (int)dcbar_cols, drt, dr_accum, wz, wz_stride,
-                                                                  dq_part, static_cast<T*>(g_prop),
+                                                                  dq_part, dq_part_stride, static_cast<T*>(g_prop),
                                                                   static_cast<T*>(g_h0), beta, n_tok, (int)d, tpr,
                                                                   tt)))
   return launched();

@@ -197,22 +197,26 @@ def _forward_impl(ctx, q, base, cbar, c0, srcs):
 
 
 def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_ptrs, dr_accum, wz, wz_stride, n_tok, d,
-          dtype, dev, cols=None, lam=1.0, g_prop=None, g_h0=None, beta=0.0, dq=None):
+          dtype, dev, cols=None, lam=1.0, g_prop=None, g_h0=None, beta=0.0, dq=None, part=None):
     """Pass 1 of the backward plus the dq reduction; returns (dq fp32, dcbar [n_tok, cols]). prob and dots are the
     forward's probabilities [n_tok, n] and raw scores [n, >= n_tok] (row stride dots.stride(0)). cols = n: cbar_c and c0c
     are the read's own; cols = n - 1: they are the previous read's coefficients and prior (scaled by lam, the newest
     entry implied) and dcbar is the gradient of those coefficients. g_prop / g_h0 receive the iteration-end blend's
-    gradients when given. dq: an fp32 row of d to reduce the query gradient into (else a new one)."""
+    gradients when given. dq: an fp32 row of d to reduce the query gradient into (else a new one). part: a
+    [bwd1_parts, d] view (any row stride) that takes the per-workgroup partials instead, left for the caller to
+    reduce (dq is then None)."""
     st = _stream(dev)
     cols = n if cols is None else cols
     gt_c = None if gt is None else gt.reshape(n_tok, n).float().contiguous()
     dcbar = torch.empty((n_tok, cols), device=dev, dtype=torch.float32)
     parts = L.bwd1_parts(n_tok, d)
-    dq_part = torch.empty((max(1, parts), d), device=dev, dtype=torch.float32)
+    dq_part = torch.empty((max(1, parts), d), device=dev, dtype=torch.float32) if part is None else part
     _run("read_bwd1", values_ptrs, rstd_ptrs, n, _p(g), _p(gt_c), _p(prob), _p(dots), dots.stride(0), _p(tc),
          _p(cbar_c), cols,
          _p(c0c), cols, float(lam), _inv_sqrt(d), _p(dcbar), cols, dr_ptrs, int(dr_accum), _p(wz), wz_stride,
-         _p(dq_part), _p(g_prop), _p(g_h0), float(beta), n_tok, d, dtype, st)
+         _p(dq_part), dq_part.stride(0), _p(g_prop), _p(g_h0), float(beta), n_tok, d, dtype, st)
+    if part is not None:
+        return None, dcbar
     dq = torch.empty(d, device=dev, dtype=torch.float32) if dq is None else dq
     if n_tok > 0:
         _run("reduce_rows", _p(dq_part), parts, d, _p(dq), st)
@@ -331,7 +335,8 @@ class DattnStack:
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
     transposed operand for its tensor-core product; the HIP write reads Q directly)."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
-                 "assembled", "neg", "dQ", "wh", "gadd", "h0_ref", "h0_steps", "h0_g", "vptr", "rptr", "drptr")
+                 "assembled", "neg", "dq_parts", "dq_rows", "wh", "gadd", "h0_ref", "h0_steps", "h0_g", "vptr",
+                 "rptr", "drptr")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
@@ -355,7 +360,8 @@ class DattnStack:
         self.assembled = set()
         self.neg = {}         # s -> (gradient of the write's h, of its x, the added proposal gradient or None),
                               # handed from _RstdStk to _WriteDelta
-        self.dQ = None        # the query gradient rows of the fused combines' backwards (fp32)
+        self.dq_parts = None  # the fused combines' query-gradient partials, [part][read][d] fp32, and the reads
+        self.dq_rows = set()  # whose backward wrote theirs; summed once, by read 1's backward (the pass's last)
         self.wh = {}          # s -> weak reference to the write's h (a fused combine that takes it as its proposal
         self.gadd = {}        # hands its proposal gradient, gadd[s] = (g, beta), to the update's gradient kernel)
         self.h0_ref = None    # the fused iteration-end reads: a weak reference to their h0, their steps, and the
@@ -647,8 +653,12 @@ class FusedCombineStk(torch.autograd.Function):
         stack, step, n = ctx.stack, ctx.step, ctx.n
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         stack.grads()
-        if stack.dQ is None or stack.dQ.shape != ctx.q_shape:
-            stack.dQ = torch.zeros(ctx.q_shape, device=dev, dtype=torch.float32)
+        nq = ctx.q_shape[0]
+        parts = L.bwd1_parts(n_tok, d)
+        if stack.dq_parts is None or stack.dq_parts.shape != (max(1, parts), nq, d):
+            # every read's dq partials, interleaved [part][read][d]: one reduction at the pass's last read
+            stack.dq_parts = torch.empty((max(1, parts), nq, d), device=dev, dtype=torch.float32)
+            stack.dq_rows = set()
         g = torch.zeros(ctx.shape, device=dev, dtype=stack.V.dtype) if g is None else g.to(stack.V.dtype).contiguous()
         # the blend's gradients are written only where no later kernel forms them from g
         need_prop, need_h0 = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
@@ -658,10 +668,21 @@ class FusedCombineStk(torch.autograd.Function):
         wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
         _, dcoeffs = _bwd1(vp, rp, n, g, gt, prob, dots, tc, coeffs_c, prior_c, drp, True, wz, n_tok, n_tok, d,
                            _dtype_code(stack.V.dtype), dev, cols=n - 1, lam=ctx.lam, g_prop=g_prop, g_h0=g_h0,
-                           beta=ctx.beta, dq=stack.dQ[step - 1])
+                           beta=ctx.beta, part=stack.dq_parts[:, step - 1, :])
+        stack.dq_rows.add(step - 1)
         stack.bwd[step] = (g, qc)
         final = [i == step or (step == 1 and i == 0) for i in range(n)]
-        dquery = stack.dQ.to(ctx.q_dtype) if step == 1 else None   # read 1's backward is the pass's last
+        dquery = None
+        if step == 1:   # read 1's backward is the pass's last: every read's partials, summed in one launch
+            for j in set(range(nq)) - stack.dq_rows:   # reads with no backward in this pass (none, normally)
+                stack.dq_parts[:, j, :].zero_()
+            dq = torch.empty((nq, d), device=dev, dtype=torch.float32)
+            if n_tok > 0:
+                _run("reduce_rows", _p(stack.dq_parts), parts, nq * d, _p(dq), _stream(dev))
+            else:
+                dq.zero_()
+            dquery = dq.to(ctx.q_dtype)
+            stack.dq_parts, stack.dq_rows = None, set()
         dprop = (g_prop if ctx.at_boundary else g) if need_prop else None
         if ctx.linked:
             stack.gadd[step] = (g, ctx.beta if ctx.at_boundary else 0.0)

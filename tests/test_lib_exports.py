@@ -92,13 +92,16 @@ def test_argument_checks_before_launch(lib):
     # a misaligned blend-gradient output
     one = lib.u64_array([4096])
     p = ctypes.c_void_p(4096)
-    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p,
+    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, 64,
                            ctypes.c_void_p(4104), null, 0.5, 16, 64, 1, null) == -3
     assert L.ldr_blend_sum(too_many, 65, 0.5, p, 16, 64, 1, null) == -2
     assert L.ldr_blend_sum(one, 1, 0.5, ctypes.c_void_p(4100), 16, 64, 1, null) == -3
     # the raw scores' row stride covers the tokens
-    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 8, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, null,
-                           null, 0.0, 16, 64, 1, null) == -1
+    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 8, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, 64,
+                           null, null, 0.0, 16, 64, 1, null) == -1
+    # ... and the dq partials' row stride covers a row
+    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, 56,
+                           null, null, 0.0, 16, 64, 1, null) == -1
     # coefficient columns: n (as the read takes them) or n - 1 (fused bookkeeping), nothing else
     two = lib.u64_array([4096, 4096])
     assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 3, p, 2, 1.0, 0.125, p, p, p, null, 16, 64, 1,
@@ -118,8 +121,8 @@ def test_argument_checks_before_launch(lib):
     assert L.ldr_blend_sum(one, 1, 0.5, p, 0, 8192, 1, null) == 0
     assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.01, p, p, p, null, 0, 8192, 1,
                           null) == 0
-    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.01, p, 1, one, 0, p, 16, p, null,
-                           null, 0.0, 0, 8192, 1, null) == 0
+    assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.01, p, 1, one, 0, p, 16, p, 8192,
+                           null, null, 0.0, 0, 8192, 1, null) == 0
     # zero tokens: accepted, nothing launched
     assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 0, 64, 1e-6, 1, null) == 0
     # ... also with the token-sized buffers NULL, as torch's empty tensors give them (never with tokens)
@@ -133,4 +136,4 @@ def test_argument_checks_before_launch(lib):
     assert L.ldr_dv_assemble(lib.u64_array([0]), lib.u64_array([0]), one, 1, null, null, null, null, 0.0, null, null,
                              0, 64, 1, null) == 0
     assert L.ldr_read_bwd1(nulls, nulls, 2, null, null, null, null, 0, null, null, 2, p, 2, 1.0, 0.125, null, 2,
-                           nulls, 0, null, 0, p, null, null, 0.0, 0, 64, 1, null) == 0
+                           nulls, 0, null, 0, p, 64, null, null, 0.0, 0, 64, 1, null) == 0
