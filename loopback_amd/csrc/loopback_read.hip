@@ -46,12 +46,6 @@
 #ifndef LDR_B1_WAVE_ROWS
 #define LDR_B1_WAVE_ROWS 1   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
-#ifndef LDR_B1_GPACK
-#define LDR_B1_GPACK 1       // backward pass 1: keep g packed in registers, unpacked where used
-#endif
-#ifndef LDR_B1_PIPE
-#define LDR_B1_PIPE 1        // backward pass 1: the next chunk's loads in flight while one is reduced
-#endif
 #ifndef LDR_NT
 #define LDR_NT 1             // non-temporal loads for the streamed sources
 #endif
@@ -596,16 +590,18 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
     const int64_t tok = t0 + tid;
     if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
   }
-  for (int e = tid; e < WM_MB * NB * 64; e += WG) {
-    const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
-    const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
-    const int jj = 16 * b + (ll & 15);
-    if (jj >= nq) continue;
-    const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
-    float* dst = dots + (int64_t)jj * dots_jstride + tok;
+  if constexpr (NB > 0) {   // the scores (NB = 0 writes none)
+    for (int e = tid; e < WM_MB * NB * 64; e += WG) {
+      const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
+      const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
+      const int jj = 16 * b + (ll & 15);
+      if (jj >= nq) continue;
+      const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
+      float* dst = dots + (int64_t)jj * dots_jstride + tok;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (tok + i < n_tok) dst[i] = sum[i];
+      for (int i = 0; i < 4; ++i)
+        if (tok + i < n_tok) dst[i] = sum[i];
+    }
   }
 }
 
@@ -1101,33 +1097,20 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
       const int64_t tok = t0 + rr;
       const bool valid = tok < n_tok;
       const int64_t roff = (valid ? tok : n_tok - 1) * (int64_t)d;
-#if LDR_B1_GPACK
-      typename IO<T>::Raw gq[VPT];   // g kept packed, unpacked where used
+      typename IO<T>::Raw gq[VPT];   // g kept packed (fewer registers), unpacked where used
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
         gq[v] = IO<T>::raw(g + roff + R.off(v));   // just written by the caller: cached, not streamed
         if (!R.act(v)) gq[v] = IO<T>::zero();
       }
-#define LDR_GV(v, arr) float arr[8]; IO<T>::unpack(gq[v], arr);
-#else
-      float gv[VPT][8];
-#pragma unroll
-      for (int v = 0; v < VPT; ++v) {
-        IO<T>::unpack(IO<T>::raw(g + roff + R.off(v)), gv[v]);
-        if (!R.act(v)) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) gv[v][k] = 0.f;
-        }
-      }
-#define LDR_GV(v, arr) const float (&arr)[8] = gv[v];
-#endif
       if ((g_prop || g_h0) && valid) {   // the blend's gradients: beta g to h0, g - beta g to the proposal
 #pragma clang fp contract(off)   // a product and a difference, each rounded as autograd rounds them (no fma)
 #pragma unroll
         for (int v = 0; v < VPT; ++v) {
           if (!R.act(v)) continue;
           float gb[8], gpv[8];
-          LDR_GV(v, gvv)
+          float gvv[8];
+          IO<T>::unpack(gq[v], gvv);
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
             gb[k] = IO<T>::round(beta * gvv[k]);
@@ -1170,7 +1153,8 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
         for (int v = 0; v < VPT; ++v) {
           float e[8];
           IO<T>::unpack(rw[v], e);
-          LDR_GV(v, gvv)
+          float gvv[8];
+          IO<T>::unpack(gq[v], gvv);
 #pragma unroll
           for (int k = 0; k < 8; ++k) acc += gvv[k] * e[k];
         }
@@ -1183,7 +1167,6 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
           for (int v = 0; v < VPT; ++v) rw[c][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0 + c]) + roff + R.off(v));
       };
       int i0 = 0;
-#if LDR_B1_PIPE
       const int nfull = n - n % C;
       typename IO<T>::Raw cur[C][VPT];
       if (nfull > 0) load_chunk(0, cur);
@@ -1203,20 +1186,6 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
 #pragma unroll
           for (int v = 0; v < VPT; ++v) cur[c][v] = nxt[c][v];
       }
-#else
-      for (; i0 + C <= n; i0 += C) {
-        typename IO<T>::Raw raw[C][VPT];
-        load_chunk(i0, raw);
-        float pd[C];
-#pragma unroll
-        for (int c = 0; c < C; ++c) pd[c] = dotc(raw[c]);
-        row_sum<C>(pd, tpr, red);
-        if (valid) {
-#pragma unroll
-          for (int c = 0; c < C; ++c) take(i0 + c, pd[c], raw[c]);
-        }
-      }
-#endif
       for (; i0 < n; ++i0) {
         typename IO<T>::Raw raw[1][VPT];
 #pragma unroll
