@@ -95,7 +95,8 @@ def family_bytes(cfg, mode):
     gradient of each update a read took as its proposal adds the proposal's share (the add autograd would otherwise
     run) from that read's output gradient, which it reads anyway, and the iteration ends' shares of h0's gradient
     are summed once (blend_sum: one output gradient per iteration end in, one row out).
-    Also the reference dataflow's total (the formula of the survey), which moves more in its backward."""
+    Also the reference dataflow's total (its compulsory rows per token, e d (5N + 4 S2 + 4(N-1))), which moves more in
+    its backward."""
     from loopback_amd.cell import fuse_glue
     from loopback_amd.chain import algorithmic_bytes_per_token
     e = 2 if cfg.dtype == torch_bf16() else 4

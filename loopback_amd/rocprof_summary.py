@@ -2,14 +2,15 @@
 launch (FETCH_SIZE / WRITE_SIZE counter passes, scaled by what the same counters read for a device-to-device copy of
 known size). Writes the markdown tables kept with the profiles and the per-launch traffic figure bench.py reports.
 
-    python -m loopback_amd.rocprof_summary --trace gpurun_out/kt/kt_kernel_trace.csv \\
-        --stats gpurun_out/kt/kt_kernel_stats.csv --fetch gpurun_out/pf/pf_counter_collection.csv \\
-        --write gpurun_out/pw/pw_counter_collection.csv \\
-        --calib-fetch gpurun_out/cf/cf_counter_collection.csv --calib-write gpurun_out/cw/cw_counter_collection.csv \\
+    python -m loopback_amd.rocprof_summary --trace prof/kt/kt_kernel_trace.csv \\
+        --stats prof/kt/kt_kernel_stats.csv --fetch prof/pf/pf_counter_collection.csv \\
+        --write prof/pw/pw_counter_collection.csv \\
+        --calib-fetch prof/cf/cf_counter_collection.csv --calib-write prof/cw/cw_counter_collection.csv \\
         --config c4 --mode scores --out profiles
 
-The passes are split at the one k_split_queries launch each chain pass starts with; the last complete pass of the
-trace and the last pass of each counter run are the ones summarized. `--stats-only NAME` summarizes the --stats
+The passes are split at the one k_split_queries launch each chain pass starts with (modes without stored scores: at
+the first forward kernel of the library after a backward one); the last complete pass of the trace and the last
+pass of each counter run are the ones summarized. `--stats-only NAME` summarizes the --stats
 output of any run (the LM step) into profiles/NAME.md.
 """
 from __future__ import annotations

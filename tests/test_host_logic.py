@@ -74,8 +74,8 @@ def test_mode_flags(monkeypatch):
     assert stack_mode() == "list"
 
 
-def test_traffic_formula_matches_the_survey():
-    # headline: d=2048, N=32, bf16 -> 9,797,632 bulk bytes per token; config 3: 849,944 total incl. scalars
+def test_traffic_formula_of_the_reference_dataflow():
+    # headline: d=2048, N=32, bf16: e d (5N + 4 S2 + 4(N-1)) = 4096 * 2392 = 9,797,632 bulk bytes per token
     parts = C.algorithmic_bytes_per_token(32, 2048, 2)
     assert parts["total"] == 9_797_632
     assert C.algorithmic_bytes_per_token(8, 768, 2, backward=False)["total"] == (3 * 8 + 35 + 14) * 768 * 2
