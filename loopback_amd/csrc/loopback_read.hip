@@ -444,14 +444,23 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
   }
 }
 
+// LDS written by some lanes of a wave and read by others of the same wave: complete the writes, keep the order
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // write step on the matrix cores (bf16 updates): the scores are a (tokens x d) . (d x queries) product. Each fp32
 // query row is held as three bf16 parts q = hi + mid + lo (the split is exact to ~2^-24 relative); the update is
 // exactly bf16 after its rounding, so three bf16 MFMAs with fp32 accumulation give fp32-accurate scores.
 // A workgroup takes WM_TT tokens (WM_MB 16-row blocks); its 4 waves split d into 64-column chunks. In a chunk, lane
 // quad g holds columns [8g, 8g + 8) and [32 + 8g, 40 + 8g) of its row (one 8-element k-group per MFMA), so each
-// load and store instruction covers 64 contiguous bytes of every row it touches; the wave partials meet in LDS in a
-// fixed order. A wave requests the next chunk's rows before it works on the current one.
+// load instruction covers 64 contiguous bytes of every row it touches; the wave's V tile of the chunk goes through
+// LDS and is stored by 8 lanes per row, whole 128-byte lines per instruction (stored as 64-byte halves, memory saw
+// 1.3x the bytes of V). The wave partials of the scores meet in LDS in a fixed order. A wave requests the next
+// chunk's rows before it works on the current one.
 // v_mfma_f32_16x16x32_bf16 operands: lane l holds row (l % 16) of A and column (l % 16) of B over the k-group of its
 // quad (l / 16); the result holds rows 4 (l / 16) + i, i < 4, of column l % 16.
 // ---------------------------------------------------------------------------------------------------------------
@@ -478,6 +487,7 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
   constexpr int NBA = NB > 0 ? NB : 1;   // array extents
   __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
   __shared__ float s_ss[4][WM_MB][16];
+  __shared__ uint4 s_v[4][WM_TT][WM_KC / 8 + 1];   // each wave's V tile of a chunk (a 16-byte pad per row)
   const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
   const int64_t t0 = (int64_t)blockIdx.x * WM_TT;
   f32x4_t acc[WM_MB][NBA];
@@ -558,10 +568,21 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
         IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);   // the stored (rounded) update
 #pragma unroll
         for (int k = 0; k < 8; ++k) ss[mb] += rv[k] * rv[k];
-        // non-temporal: the read that follows streams V[s] with its other sources, and dirty cached lines would be
-        // written back in the middle of its stream
-        if (ok) __builtin_nontemporal_store(u32x4{u.x, u.y, u.z, u.w}, reinterpret_cast<u32x4*>(v + roff[mb] + cc[hf]));
+        s_v[w][16 * mb + row][quad + 4 * hf] = u;
       }
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < WM_TT * 8 / 64; ++k) {   // 8 lanes per token row
+      const int e = l + 64 * k, t = e >> 3, u8 = e & 7;
+      const int64_t tok = t0 + t;
+      const int col8 = c * WM_KC + 8 * u8;
+      const uint4 u = s_v[w][t][u8];
+      // non-temporal: the read that follows streams V[s] with its other sources, and dirty cached lines would be
+      // written back in the middle of its stream
+      if (tok < n_tok && col8 < d)
+        __builtin_nontemporal_store(u32x4{u.x, u.y, u.z, u.w}, reinterpret_cast<u32x4*>(v + tok * (int64_t)d + col8));
+    }
+    wave_lds_sync();   // the tile is read before the next chunk overwrites it
 #pragma unroll
     for (int p = 0; p < 3 * (NB > 0); ++p)
 #pragma unroll
@@ -844,13 +865,6 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
 // the raw scores are stored for the backward.
 // ---------------------------------------------------------------------------------------------------------------
 constexpr float RF_LAZY = 8.f;   // e^8 < 3000: the running sums stay far from overflow between rescales
-
-// LDS written by some lanes of a wave and read by others of the same wave: complete the writes, keep the order
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 template <typename T, int VPT, bool BLEND, int PD>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LDR_ON_WAVES)))
