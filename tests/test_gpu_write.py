@@ -2,7 +2,8 @@
 what torch's subtraction gives), R[s] the RMS scale of the rounded update, and the scores of the update against
 the queries of the reads still to come, DOTS[j, s, tok] = q_j . V[s, tok] for j >= s - 1 -- against an fp64 matmul
 of the rounded update (bf16: matrix cores from the queries' three bf16 parts; fp32: vector units). Ragged token
-counts and a width with a partial 64-column chunk included."""
+counts, widths below one 64-column chunk and a width with a partial chunk included; every slice is checked
+again after the last write."""
 import pytest
 import torch
 
@@ -12,7 +13,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("T,d", [(37, 64), (100, 768), (257, 1096), (64, 2048)])
+@pytest.mark.parametrize("T,d", [(37, 64), (100, 768), (257, 1096), (64, 2048), (19, 40), (5, 8)])
 @pytest.mark.parametrize("N", [2, 9, 33])
 def test_write_scores(dtype, T, d, N):
     from loopback_amd import fused_dattn as FD
@@ -28,6 +29,8 @@ def test_write_scores(dtype, T, d, N):
             assert torch.equal(v, hs[s] - xs[s]), s
             assert stack.r_done[s]
     torch.cuda.synchronize()
+    for s in range(N):   # no later write touched an earlier slice
+        assert torch.equal(stack.V[s].reshape(1, T, d), hs[s] - xs[s]), s
     V = stack.V.double().cpu().reshape(N, T, d)
     rr = rstd_ref(V, 1e-6).squeeze(-1)
     assert err_rms(stack.R.reshape(N, T).cpu(), rr) <= 2e-6
