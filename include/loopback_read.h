@@ -55,11 +55,13 @@ int ldr_row_layout(int64_t d, int* vpt, int* tpr);
 int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d);
 
 /* r[tok] = rsqrt(sum_k x[tok,k]^2 / d + eps).
- * Replaces _rstd_fwd_kernel and its launches (fused_dattn.py:206-215, 240, 705). */
+ * Replaces _rstd_fwd_kernel and its launches (fused_dattn.py:206-215, 240, 705). Any d >= 1 and any alignment, as
+ * the reference's masked kernel: rows the vector layout does not take (d not a multiple of 8 or above
+ * LDR_MAX_WIDTH, x not 16-byte aligned) run on scalar loads. */
 int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream);
 
 /* gx[tok,:] = gr[tok] * (-r[tok]^3) / d * x[tok,:], rounded to dtype.
- * Replaces _rstd_bwd_kernel (fused_dattn.py:218-229, 252). */
+ * Replaces _rstd_bwd_kernel (fused_dattn.py:218-229, 252). Any d >= 1 and any alignment, as ldr_rstd_fwd. */
 int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
                  void* stream);
 

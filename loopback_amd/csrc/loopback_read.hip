@@ -358,6 +358,42 @@ __global__ __launch_bounds__(WG) void k_rstd_bwd(const T* __restrict__ x, const 
   }
 }
 
+// Rows of any width and alignment (those the vector layout does not take: d not a multiple of 8, above the widest
+// row, or not 16-byte aligned): one wave per row, its lanes striding the row with scalar loads (64 consecutive
+// elements per step, coalesced), the sum reduced in registers.
+__device__ __forceinline__ float ld1(const bf16_t* p) { return __uint_as_float((uint32_t)*p << 16); }
+__device__ __forceinline__ float ld1(const float* p) { return *p; }
+__device__ __forceinline__ void st1(bf16_t* p, float v) { *p = __builtin_bit_cast(bf16_t, (__bf16)v); }
+__device__ __forceinline__ void st1(float* p, float v) { *p = v; }
+
+template <typename T>
+__global__ __launch_bounds__(WG) void k_rstd_fwd_any(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
+                                                     int64_t d, float eps) {
+  const int lane = (int)threadIdx.x & 63, w = (int)threadIdx.x >> 6;
+  for (int64_t tok = (int64_t)blockIdx.x * (WG / 64) + w; tok < n_tok; tok += (int64_t)gridDim.x * (WG / 64)) {
+    const T* row = x + tok * d;
+    float ss = 0.f;
+    for (int64_t k = lane; k < d; k += 64) {
+      const float e = ld1(row + k);
+      ss += e * e;
+    }
+    ss = lanes_reduce(ss, 64, AddOp());   // every lane of the wave is here: the row loop is wave-uniform
+    if (lane == 0) r[tok] = rsqrtf(ss / (float)d + eps);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(WG) void k_rstd_bwd_any(const T* __restrict__ x, const float* __restrict__ r,
+                                                     const float* __restrict__ gr, T* __restrict__ gx, int64_t n_tok,
+                                                     int64_t d) {
+  const int lane = (int)threadIdx.x & 63, w = (int)threadIdx.x >> 6;
+  for (int64_t tok = (int64_t)blockIdx.x * (WG / 64) + w; tok < n_tok; tok += (int64_t)gridDim.x * (WG / 64)) {
+    const float rv = r[tok];
+    const float c = gr[tok] * (-rv * rv * rv) / (float)d;
+    for (int64_t k = lane; k < d; k += 64) st1(gx + tok * d + k, c * ld1(x + tok * d + k));
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // write step: V[s] = round(h - x), R[s] from the rounded update, scores against the later read queries.
 // A tile of 32 tokens streams d in chunks of 128 columns: the chunk of the update goes to LDS (fp32) next to the
@@ -1605,13 +1641,17 @@ int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d) {
 
 int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (n_tok < 0 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok)) return LDR_E_ARG;
-  if (!al16(x)) return LDR_E_ALIGN;
-  int vpt, tpr, e = row_layout(d, &vpt, &tpr);
-  if (e) return e;
+  if (n_tok < 0 || d < 1 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok)) return LDR_E_ARG;
   if (n_tok == 0) return LDR_OK;
-  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  int vpt, tpr;
+  if (!al16(x) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other width or alignment: scalar loads
+    const unsigned grid = grid_of(cdiv(n_tok, WG / 64), 8192);
+    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_rstd_fwd_any<T>), dim3(grid), dim3(WG), 0, st,
+                                               static_cast<const T*>(x), r, n_tok, d, eps))
+    return launched();
+  }
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_rstd_fwd<T, VPT>), dim3(grid), dim3(WG), 0, st,
                                                                   static_cast<const T*>(x), r, n_tok, (int)d, tpr, eps)))
   return launched();
@@ -1620,14 +1660,18 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
 int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
                  void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
-  if (n_tok < 0 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(gr, n_tok) || !tok_ptr(gx, n_tok))
+  if (n_tok < 0 || d < 1 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(gr, n_tok) || !tok_ptr(gx, n_tok))
     return LDR_E_ARG;
-  if (!al16(x) || !al16(gx)) return LDR_E_ALIGN;
-  int vpt, tpr, e = row_layout(d, &vpt, &tpr);
-  if (e) return e;
   if (n_tok == 0) return LDR_OK;
-  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  int vpt, tpr;
+  if (!al16(x) || !al16(gx) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other width or alignment
+    const unsigned grid = grid_of(cdiv(n_tok, WG / 64), 8192);
+    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_rstd_bwd_any<T>), dim3(grid), dim3(WG), 0, st,
+                                               static_cast<const T*>(x), r, gr, static_cast<T*>(gx), n_tok, d))
+    return launched();
+  }
+  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_rstd_bwd<T, VPT>), dim3(grid), dim3(WG), 0, st,
                                                                   static_cast<const T*>(x), r, gr, static_cast<T*>(gx),
                                                                   n_tok, (int)d, tpr)))

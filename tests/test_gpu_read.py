@@ -163,21 +163,29 @@ def test_zero_query_identity_bitwise(dtype, n, boundary):
     assert torch.equal(tc, next_prior.view(1, 1, -1).expand(b, t, -1))
 
 
-def test_rstd_matches_reference_scale():
+@pytest.mark.parametrize("shape,offset", [((3, 33, 1536), 0), ((2, 17, 100), 0), ((1, 9, 7), 0), ((2, 5, 8200), 0),
+                                          ((2, 11, 768), 1)])
+def test_rstd_matches_reference_scale(shape, offset):
+    """rstd and its backward against fp64 autograd of the torch expression. As the reference's masked kernels, any
+    width and alignment: the vector rows (d a multiple of 8, aligned) and the scalar rows (d = 100, 7, 8200 above the
+    widest vector row, and rows one element off 16-byte alignment)."""
     from loopback_amd import fused_dattn as FD
     from oracle.reference_read import rstd_ref
+    b, t, d = shape
     for dtype in (torch.float32, torch.bfloat16):
-        x = (torch.randn(3, 33, 1536, generator=torch.Generator().manual_seed(4)) * 1.7).to(dtype)
-        xg = x.to(DEV).requires_grad_()
+        flat = (torch.randn(b * t * d + offset, generator=torch.Generator().manual_seed(4)) * 1.7).to(dtype)
+        fg = flat.to(DEV).requires_grad_()
+        xg = fg[offset:].view(b, t, d)   # contiguous; offset 1 leaves it off 16-byte alignment
+        print(f"case rstd {shape} offset={offset} {dtype}", flush=True)
         r = FD.rstd(xg, 1e-6)
-        gr = torch.randn(3, 33, 1, generator=torch.Generator().manual_seed(5))
+        gr = torch.randn(b, t, 1, generator=torch.Generator().manual_seed(5))
         (r * gr.to(DEV)).sum().backward()
-        xc = x.double().requires_grad_()
+        xc = flat[offset:].view(b, t, d).double().requires_grad_()
         rr = rstd_ref(xc, 1e-6)
         (rr * gr.double()).sum().backward()
         assert err_rms(r.detach(), rr.detach()) <= 1e-6
         tol = 1e-5 if dtype == torch.float32 else 1e-2
-        assert err_max(xg.grad, xc.grad) <= tol
+        assert err_max(fg.grad[offset:].view(b, t, d), xc.grad) <= tol
 
 
 def test_accumulating_list_layout_matches_plain():

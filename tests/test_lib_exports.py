@@ -70,8 +70,14 @@ def test_argument_checks_before_launch(lib):
     L = lib.LIB
     null = ctypes.c_void_p(0)
     assert L.ldr_rstd_fwd(null, null, 16, 64, 1e-6, 1, null) == -1
-    assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 60, 1e-6, 1, null) == -2
-    assert L.ldr_rstd_fwd(ctypes.c_void_p(4100), ctypes.c_void_p(4096), 16, 64, 1e-6, 1, null) == -3
+    assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 0, 1e-6, 1, null) == -1
+    assert L.ldr_rstd_bwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096),
+                          16, -8, 1, null) == -1
+    # (the scale takes any width and alignment; the read's vector kernels do not)
+    one_v = lib.u64_array([4096])
+    assert L.ldr_dots_online(one_v, 1, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 60, 1, null) == -2
+    assert L.ldr_dots_online(lib.u64_array([4100]), 1, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, 1,
+                             null) == -3
     assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 64, 1e-6, 7, null) == -4
     too_many = lib.u64_array([4096] * 65)
     assert L.ldr_dots_online(too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, 1, null) == -1
