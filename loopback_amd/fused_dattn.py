@@ -522,8 +522,10 @@ class FusedDattnReadStk(torch.autograd.Function):
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         if base.dtype != stack.V.dtype or not base.is_contiguous() or base.shape[:-1] != stack.V.shape[1:3]:
             raise RuntimeError("delta_attnres stacked read: base must be contiguous, the stack's dtype and shape")
-        if not 1 <= n <= stack.n_steps or base.shape[-1] != d or not _aligned(base):
+        if not 1 <= n <= stack.n_steps:
             raise RuntimeError(f"delta_attnres stacked read: {n} sources for a stack of {stack.n_steps}")
+        if base.shape[-1] != d or not _aligned(base):
+            raise RuntimeError(f"delta_attnres stacked read: base must have width {d} and 16-byte aligned rows")
         dt = _dtype_code(stack.V.dtype)
         st = _stream(dev)
         qc = q.detach().float().contiguous()
