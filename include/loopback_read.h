@@ -9,7 +9,8 @@
  *   - n_tok = b * t tokens, d the width (a multiple of 8, at most LDR_MAX_WIDTH); n_tok = 0 is a valid batch, for
  *     which the token-sized buffers may be NULL (as empty tensors give them): nothing is read or written but the
  *     per-read outputs (next_prior);
- *   - dtype is LDR_F32 or LDR_BF16 and applies to the update-shaped tensors (updates, base, out, g, dv, h, x);
+ *   - dtype is LDR_F32 or LDR_BF16 (the scale entry points also take LDR_F16) and applies to the update-shaped
+ *     tensors (updates, base, out, g, dv, h, x);
  *     every scale, score, coefficient and gradient scalar is fp32;
  *   - per-source arrays (src_v, src_r, ...) are HOST arrays of n device addresses, copied into the kernel
  *     arguments (no device pointer table, no host-to-device copy); n <= LDR_MAX_SOURCES;
@@ -30,6 +31,7 @@ extern "C" {
 
 #define LDR_F32 0
 #define LDR_BF16 1
+#define LDR_F16 2   /* the scale entry points only (ldr_rstd_fwd / ldr_rstd_bwd), as the reference's rstd */
 
 #define LDR_MAX_SOURCES 64
 #define LDR_MAX_WIDTH 8192
@@ -39,7 +41,7 @@ extern "C" {
 #define LDR_E_ARG (-1)    /* null pointer, negative size, bad flag */
 #define LDR_E_SHAPE (-2)  /* d not a multiple of 8 or too wide; n or nq out of range */
 #define LDR_E_ALIGN (-3)  /* a vector pointer is not 16-byte aligned */
-#define LDR_E_DTYPE (-4)  /* dtype is neither LDR_F32 nor LDR_BF16 */
+#define LDR_E_DTYPE (-4)  /* dtype is neither LDR_F32 nor LDR_BF16 (nor LDR_F16 where taken) */
 
 /* Version of this ABI; bumped on any signature change. */
 int ldr_abi_version(void);
@@ -57,11 +59,11 @@ int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d);
 /* r[tok] = rsqrt(sum_k x[tok,k]^2 / d + eps).
  * Replaces _rstd_fwd_kernel and its launches (fused_dattn.py:206-215, 240, 705). Any d >= 1 and any alignment, as
  * the reference's masked kernel: rows the vector layout does not take (d not a multiple of 8 or above
- * LDR_MAX_WIDTH, x not 16-byte aligned) run on scalar loads. */
+ * LDR_MAX_WIDTH, x not 16-byte aligned) run on scalar loads. dtype may also be LDR_F16 (scalar loads). */
 int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream);
 
 /* gx[tok,:] = gr[tok] * (-r[tok]^3) / d * x[tok,:], rounded to dtype.
- * Replaces _rstd_bwd_kernel (fused_dattn.py:218-229, 252). Any d >= 1 and any alignment, as ldr_rstd_fwd. */
+ * Replaces _rstd_bwd_kernel (fused_dattn.py:218-229, 252). Any d >= 1, alignment and dtype, as ldr_rstd_fwd. */
 int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
                  void* stream);
 

@@ -363,8 +363,10 @@ __global__ __launch_bounds__(WG) void k_rstd_bwd(const T* __restrict__ x, const 
 // elements per step, coalesced), the sum reduced in registers.
 __device__ __forceinline__ float ld1(const bf16_t* p) { return __uint_as_float((uint32_t)*p << 16); }
 __device__ __forceinline__ float ld1(const float* p) { return *p; }
+__device__ __forceinline__ float ld1(const _Float16* p) { return (float)*p; }
 __device__ __forceinline__ void st1(bf16_t* p, float v) { *p = __builtin_bit_cast(bf16_t, (__bf16)v); }
 __device__ __forceinline__ void st1(float* p, float v) { *p = v; }
+__device__ __forceinline__ void st1(_Float16* p, float v) { *p = (_Float16)v; }
 
 template <typename T>
 __global__ __launch_bounds__(WG) void k_rstd_fwd_any(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
@@ -1601,6 +1603,10 @@ int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n, int64_t
 #define LDR_DTYPE_SWITCH(DT, ...)                                \
   if ((DT) == LDR_BF16) { typedef bf16_t T; __VA_ARGS__; }       \
   else { typedef float T; __VA_ARGS__; }
+#define LDR_DTYPE_SWITCH3(DT, ...)                               \
+  if ((DT) == LDR_BF16) { typedef bf16_t T; __VA_ARGS__; }       \
+  else if ((DT) == LDR_F16) { typedef _Float16 T; __VA_ARGS__; } \
+  else { typedef float T; __VA_ARGS__; }
 
 template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
 // one-pass online read: sources in flight per row (enough bytes in flight to cover the HBM latency)
@@ -1623,7 +1629,7 @@ const char* ldr_strerror(int code) {
     case LDR_E_ARG: return "loopback_read: invalid argument (null pointer, bad count or flag)";
     case LDR_E_SHAPE: return "loopback_read: unsupported shape (d must be a multiple of 8 and <= 8192; 1 <= n <= 64)";
     case LDR_E_ALIGN: return "loopback_read: a vector pointer is not 16-byte aligned";
-    case LDR_E_DTYPE: return "loopback_read: dtype must be LDR_F32 or LDR_BF16";
+    case LDR_E_DTYPE: return "loopback_read: dtype must be LDR_F32 or LDR_BF16 (or LDR_F16 for the scale)";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "loopback_read: unknown error";
   }
 }
@@ -1640,15 +1646,15 @@ int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d) {
 }
 
 int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream) {
-  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (!dtype_ok(dtype) && dtype != LDR_F16) return LDR_E_DTYPE;
   if (n_tok < 0 || d < 1 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok)) return LDR_E_ARG;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   int vpt, tpr;
-  if (!al16(x) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other width or alignment: scalar loads
+  if (dtype == LDR_F16 || !al16(x) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other row: scalar loads
     const unsigned grid = grid_of(cdiv(n_tok, WG / 64), 8192);
-    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_rstd_fwd_any<T>), dim3(grid), dim3(WG), 0, st,
-                                               static_cast<const T*>(x), r, n_tok, d, eps))
+    LDR_DTYPE_SWITCH3(dtype, hipLaunchKernelGGL((k_rstd_fwd_any<T>), dim3(grid), dim3(WG), 0, st,
+                                                static_cast<const T*>(x), r, n_tok, d, eps))
     return launched();
   }
   const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
@@ -1659,16 +1665,16 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
 
 int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
                  void* stream) {
-  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (!dtype_ok(dtype) && dtype != LDR_F16) return LDR_E_DTYPE;
   if (n_tok < 0 || d < 1 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(gr, n_tok) || !tok_ptr(gx, n_tok))
     return LDR_E_ARG;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   int vpt, tpr;
-  if (!al16(x) || !al16(gx) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other width or alignment
+  if (dtype == LDR_F16 || !al16(x) || !al16(gx) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other row
     const unsigned grid = grid_of(cdiv(n_tok, WG / 64), 8192);
-    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_rstd_bwd_any<T>), dim3(grid), dim3(WG), 0, st,
-                                               static_cast<const T*>(x), r, gr, static_cast<T*>(gx), n_tok, d))
+    LDR_DTYPE_SWITCH3(dtype, hipLaunchKernelGGL((k_rstd_bwd_any<T>), dim3(grid), dim3(WG), 0, st,
+                                                static_cast<const T*>(x), r, gr, static_cast<T*>(gx), n_tok, d))
     return launched();
   }
   const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);

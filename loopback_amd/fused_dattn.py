@@ -67,6 +67,15 @@ def _dtype_code(dtype: torch.dtype) -> int:
     raise RuntimeError(f"delta_attnres HIP read: updates must be bfloat16 or float32, got {dtype}")
 
 
+def _scale_dtype_code(dtype: torch.dtype) -> int:
+    """The scale kernels also take fp16 rows, as the reference's rstd does; the read's kernels do not."""
+    if dtype == torch.float16:
+        return L.F16
+    if dtype in (torch.bfloat16, torch.float32):
+        return _dtype_code(dtype)
+    raise RuntimeError(f"delta_attnres HIP rstd: input must be bfloat16, float16 or float32, got {dtype}")
+
+
 def _require_gpu(t: torch.Tensor, what: str) -> None:
     if not t.is_cuda:
         raise RuntimeError(f"delta_attnres HIP read: {what} must be a GPU (HIP) tensor, got device {t.device}")
@@ -113,7 +122,7 @@ class _Rstd(torch.autograd.Function):
         d = xc.shape[-1]
         n_tok = xc.numel() // d
         r = torch.empty(xc.shape[:-1] + (1,), device=xc.device, dtype=torch.float32)
-        _run("rstd_fwd", _p(xc), _p(r), n_tok, d, float(eps), _dtype_code(xc.dtype), _stream(xc.device))
+        _run("rstd_fwd", _p(xc), _p(r), n_tok, d, float(eps), _scale_dtype_code(xc.dtype), _stream(xc.device))
         ctx.save_for_backward(xc, r)
         return r
 
@@ -124,8 +133,7 @@ class _Rstd(torch.autograd.Function):
         n_tok = xc.numel() // d
         gx = torch.empty_like(xc)
         grc = gr.float().contiguous()
-        _run("rstd_bwd", _p(xc), _p(r), _p(grc), _p(gx), n_tok, d, _dtype_code(xc.dtype),
-                                  _stream(xc.device))
+        _run("rstd_bwd", _p(xc), _p(r), _p(grc), _p(gx), n_tok, d, _scale_dtype_code(xc.dtype), _stream(xc.device))
         return gx, None
 
 

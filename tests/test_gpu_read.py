@@ -167,12 +167,12 @@ def test_zero_query_identity_bitwise(dtype, n, boundary):
                                           ((2, 11, 768), 1)])
 def test_rstd_matches_reference_scale(shape, offset):
     """rstd and its backward against fp64 autograd of the torch expression. As the reference's masked kernels, any
-    width and alignment: the vector rows (d a multiple of 8, aligned) and the scalar rows (d = 100, 7, 8200 above the
-    widest vector row, and rows one element off 16-byte alignment)."""
+    width, alignment and float dtype: the vector rows (bf16 and fp32, d a multiple of 8, aligned) and the scalar rows
+    (d = 100, 7, 8200 above the widest vector row, rows one element off 16-byte alignment, and fp16)."""
     from loopback_amd import fused_dattn as FD
     from oracle.reference_read import rstd_ref
     b, t, d = shape
-    for dtype in (torch.float32, torch.bfloat16):
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
         flat = (torch.randn(b * t * d + offset, generator=torch.Generator().manual_seed(4)) * 1.7).to(dtype)
         fg = flat.to(DEV).requires_grad_()
         xg = fg[offset:].view(b, t, d)   # contiguous; offset 1 leaves it off 16-byte alignment
