@@ -21,6 +21,8 @@ How each part is pinned (tests/test_oracle_*.py): closed forms C1/C2/C4/C5/C6 of
 boundary entry at lam; beta = 0 -> Plain Loop bitwise), the key against torch's own rms_norm, a pure-Python brute
 force of the paper's equation on tiny inputs, and `analytic_backward` against autograd and central differences.
 The reference ships no golden vectors for this path; tests/golden/ holds vectors this oracle wrote in fp64.
+The code is device-agnostic torch: the checks run it on the CPU; one whole-model test runs the cell on the GPU beside
+the HIP read, so that every other op of the model is the same kernel in both and the read alone can differ.
 """
 from __future__ import annotations
 
@@ -77,8 +79,8 @@ class OracleCell:
         base = proposal + self.beta * (h0 - proposal) if at_boundary else proposal
         cdt = _score_dtype(proposal.dtype)
         b, t, _ = proposal.shape
-        one_tok = torch.ones(b, t, 1, dtype=torch.float32 if cdt == torch.float32 else cdt)
-        one_prior = torch.ones(1, dtype=one_tok.dtype)
+        one_tok = torch.ones(b, t, 1, dtype=torch.float32 if cdt == torch.float32 else cdt, device=proposal.device)
+        one_prior = torch.ones(1, dtype=one_tok.dtype, device=proposal.device)
         base_coeffs = one_tok if coeffs is None else torch.cat((coeffs, one_tok), dim=-1)
         next_prior = one_prior if prior_coeffs is None else torch.cat((prior_coeffs, one_prior), dim=-1)
         if at_boundary:

@@ -5,8 +5,8 @@ Loopback at beta = 0 with zero queries (the reference audit's C6: every coeffici
 plain residual sum), and a loss near log(vocab) at init.
 GPU: the model with the HIP read against the same weights on the CPU with the oracle read in fp64 -- loss and every
 parameter gradient (fp32: norm-relative 1e-4; bf16: loss within 1e-2 relative) -- the model through every read
-path (stored / online scores, list layout, torch glue) agreeing, and a few training steps that lower the loss on a
-fixed batch. CPU also: the meta-device init path leaves the queries at zero.
+path (stored / online scores, list layout, torch glue) agreeing, the model at init bitwise the same with the
+reference read run on the GPU, and a few training steps that lower the loss on a fixed batch. CPU also: the meta-device init path leaves the queries at zero.
 """
 import copy
 import math
@@ -23,7 +23,7 @@ TINY = dict(hidden_size=64, num_heads=4, vocab_size=97, prelude=1, loop_blocks=2
 
 
 class OracleRead(nn.Module):
-    """The reference read cell as the LM's read (list layout, any dtype / device of its inputs on the CPU)."""
+    """The reference read cell as the LM's read (list layout, any dtype, on its inputs' device)."""
 
     def __init__(self, read):
         super().__init__()
@@ -106,6 +106,35 @@ def test_hip_lm_matches_oracle_lm(dtype):
         assert set(g) == set(gr)
         for k in gr:
             assert torch.isfinite(g[k]).all(), k
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lm_at_init_is_the_reference_read_bitwise(dtype):
+    """The reference's whole-model check (tests/test_fused_dattn.py:128-154, 210-215): at init (zero queries) the
+    model with the HIP read and the same model with the reference read -- the oracle cell, on the same GPU, so every
+    other op is the same kernel -- give the same loss bitwise: at zero query the read is exactly its base in both.
+    The gradients (summed in other orders by the two backwards) agree to 1e-5 (fp32) / 1e-2 (bf16) norm-relative."""
+    torch.manual_seed(4)
+    cfg = LMConfig(**TINY)
+    model = LoopbackLM(cfg)
+    assert not model.read.query.any()                         # the reference's zero init
+    hip = copy.deepcopy(model).to(device="cuda", dtype=dtype)
+    ref = copy.deepcopy(model).to(device="cuda", dtype=dtype)
+    ref.read = OracleRead(ref.read)
+    ids = ids_for(cfg, b=2, t=40).cuda()
+    print(f"case lm at init {dtype}", flush=True)
+    la, lb = hip(ids), ref(ids)
+    assert torch.equal(la, lb), (la.item(), lb.item())
+    la.backward()
+    lb.backward()
+    torch.cuda.synchronize()
+    ga, gb = _grads(hip), _grads(ref)
+    assert set(ga) == set(gb)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    for k in gb:
+        err = ((ga[k] - gb[k]).norm() / gb[k].norm().clamp_min(1e-30)).item()
+        assert err <= tol, (k, err)
 
 
 @pytest.mark.gpu
