@@ -194,6 +194,8 @@ def main():
     # the launch stream once every few steps; the steps themselves create no cycles that need collecting.
     gc.collect()
     gc.freeze()
+    resident = torch.cuda.memory_allocated()   # the inputs and the cell, before any pass
+    torch.cuda.reset_peak_memory_stats()
     timer = KernelTimer()
     t0 = time.perf_counter()
     for step in range(args.steps):
@@ -203,6 +205,7 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     FD._TIMER = None
+    peak = torch.cuda.max_memory_allocated()
     ms_per_step = 1e3 * elapsed / args.steps
     ksum = timer.summary()
     fam, ref_bytes = family_bytes(cfg, args.mode)
@@ -250,7 +253,11 @@ def main():
                   "formula_wall_gbs": ref_bytes / (ms_per_step * 1e-3) / 1e9,
                   "kernels": {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 4),
                                   "gbs": (fam[k] / (v["total_ms"] * 1e-3) / 1e9) if k in fam else None}
-                              for k, v in sorted(ksum.items())}},
+                              for k, v in sorted(ksum.items())},
+                  # device memory, as the reference's --bench reports it: the inputs resident before the passes,
+                  # and the peak during them (the pass's stacks, saved tensors and gradients on top of the inputs)
+                  "memory_gib": {"resident": resident / 2**30, "peak": peak / 2**30,
+                                 "pass_peak": (peak - resident) / 2**30}},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
