@@ -2,7 +2,8 @@
 //
 // The read kernels stream n sources row by row (one 16-byte vector per lane, rows of 4 KiB) and write at most a few
 // rows per row set. These probes do the same with no arithmetic: read the n sources (XOR-folded so the loads are
-// not dead), optionally write one row per row set; and a plain device copy. bench-side code (stream_probe.py) times
+// not dead), optionally write one row per row set (right after its reads, or batched 16 row sets at a time); and a
+// plain device copy. bench-side code (stream_probe.py) times
 // them to give the practical ceiling each kernel's read/write mix allows, next to the 8 TB/s peak.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -36,6 +37,35 @@ __global__ __launch_bounds__(256) void k_probe_read(Tab t, int n, int64_t rows, 
   if (s == 0x9e3779b9u) sink[0] = s;   // never true for the probe's data; keeps the loads live
 }
 
+// the same mix with the written rows batched: the out rows of 16 consecutive row sets are kept in LDS and written
+// together after the set's reads, one contiguous 64 KiB region (the stored-score read's staged output)
+constexpr int BURST = 16;
+__global__ __launch_bounds__(256) void k_probe_read_burst(Tab t, int n, int64_t rows, u32x4* __restrict__ out,
+                                                          unsigned* __restrict__ sink) {
+  __shared__ u32x4 s_out[BURST][ROWV];
+  const int lane = (int)threadIdx.x;
+  unsigned s = 0;
+  for (int64_t blk = blockIdx.x; blk < rows / BURST; blk += gridDim.x) {
+    for (int r = 0; r < BURST; ++r) {
+      const int64_t row = blk * BURST + r;
+      u32x4 acc = {0u, 0u, 0u, 0u};
+      int i = 0;
+      for (; i + 8 <= n; i += 8) {
+        u32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(t.p[i + u] + row * ROWV + lane);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u];
+      }
+      for (; i < n; ++i) acc ^= __builtin_nontemporal_load(t.p[i] + row * ROWV + lane);
+      s_out[r][lane] = acc;
+      s ^= acc.x ^ acc.y ^ acc.z ^ acc.w;
+    }
+    for (int r = 0; r < BURST; ++r) out[(blk * BURST + r) * ROWV + lane] = s_out[r][lane];   // this lane's own
+  }
+  if (s == 0x9e3779b9u) sink[0] = s;
+}
+
 __global__ __launch_bounds__(256) void k_probe_copy(const u32x4* __restrict__ a, u32x4* __restrict__ b, int64_t n) {
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
     b[i] = __builtin_nontemporal_load(a + i);
@@ -54,6 +84,19 @@ int ldp_read(const uint64_t* src, int n, int64_t rows, void* out, void* sink, in
   for (int i = 0; i < n; ++i)
     if (!t.p[i] || (reinterpret_cast<uintptr_t>(t.p[i]) & 15u)) return -1;
   hipLaunchKernelGGL(k_probe_read, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), t, n, rows,
+                     static_cast<u32x4*>(out), static_cast<unsigned*>(sink));
+  return (int)hipGetLastError();
+}
+
+// As ldp_read with out required, the written rows batched 16 row sets at a time (rows a multiple of 16).
+int ldp_read_burst(const uint64_t* src, int n, int64_t rows, void* out, void* sink, int grid, void* stream) {
+  if (!src || n < 1 || n > MAXP || rows < BURST || (rows % BURST) || !out || !sink || grid < 1) return -1;
+  Tab t;
+  for (int i = 0; i < MAXP; ++i) t.p[i] = i < n ? reinterpret_cast<const u32x4*>(src[i]) : nullptr;
+  for (int i = 0; i < n; ++i)
+    if (!t.p[i] || (reinterpret_cast<uintptr_t>(t.p[i]) & 15u)) return -1;
+  if (reinterpret_cast<uintptr_t>(out) & 15u) return -1;
+  hipLaunchKernelGGL(k_probe_read_burst, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), t, n, rows,
                      static_cast<u32x4*>(out), static_cast<unsigned*>(sink));
   return (int)hipGetLastError();
 }

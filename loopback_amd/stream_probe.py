@@ -1,7 +1,8 @@
 """The practical streaming ceilings of the box for the read kernels' access patterns (libloopback_probe.so):
 
   * read-only, 32 sources of 64 MiB streamed row by row (the read kernels' pattern, nothing written);
-  * the same with one 4 KiB row written per row set (1 write per 32 reads, the read forward's mix);
+  * the same with one 4 KiB row written per row set (1 write per 32 reads, the read forward's mix), each row right
+    after its reads, or 16 consecutive rows kept in LDS and written together (the read forward's staged output);
   * a device copy (1 read, 1 write per element);
 each at several grid sizes, best of 5. Reported as GB/s of the bytes each probe moves, beside the 8 TB/s peak.
 
@@ -28,6 +29,8 @@ def _lib():
     lib.ldp_read.restype = ctypes.c_int
     lib.ldp_read.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.c_int, ctypes.c_int64, ctypes.c_void_p,
                              ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.ldp_read_burst.restype = ctypes.c_int
+    lib.ldp_read_burst.argtypes = lib.ldp_read.argtypes
     lib.ldp_copy.restype = ctypes.c_int
     lib.ldp_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
     return lib
@@ -66,15 +69,18 @@ def main():
             raise RuntimeError(f"stream_probe: {what} failed ({code})")
 
     res = {}
-    for grid in (1024, 2048, 4096):
+    for grid in (512, 1024, 2048, 4096):
         ro = _best(lambda: check(lib.ldp_read(ptrs, n, rows, None, ctypes.c_void_p(sink.data_ptr()), grid, st),
                                  "read"))
         rw = _best(lambda: check(lib.ldp_read(ptrs, n, rows, ctypes.c_void_p(out.data_ptr()),
                                               ctypes.c_void_p(sink.data_ptr()), grid, st), "read+write"))
+        rb = _best(lambda: check(lib.ldp_read_burst(ptrs, n, rows, ctypes.c_void_p(out.data_ptr()),
+                                                    ctypes.c_void_p(sink.data_ptr()), grid, st), "read+burst write"))
         cp = _best(lambda: check(lib.ldp_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(src[n // 2].data_ptr()),
                                               src_bytes // 2, grid, st), "copy"))
         res[grid] = {"read_32_sources": src_bytes / ro / 1e9,
                      "read_32_sources_write_1": (src_bytes + rows * row_bytes) / rw / 1e9,
+                     "read_32_sources_write_1_burst16": (src_bytes + rows * row_bytes) / rb / 1e9,
                      "copy": src_bytes / cp / 1e9}
     best = {k: max(r[k] for r in res.values()) for k in next(iter(res.values()))}
     print(json.dumps({"metric": "streaming ceilings (GB/s of bytes moved)", "peak_gbs": PEAK_GBS, "best": best,
