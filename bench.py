@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c4", choices=["c2", "c3", "c4"])
+    ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4"])
     ap.add_argument("--mode", default="scores", choices=["scores", "stack", "list"])
     ap.add_argument("--graph", action="store_true",
                     help="forward-only configs: time replays of the pass captured in a HIP graph (no host work)")
@@ -138,7 +138,14 @@ def cpu_baseline(cfg, tokens):
         if time.perf_counter() - t_start > 30:
             break
     med = statistics.median(times)
-    return {"value": tokens / med, "unit": "read-tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), None)
+    except OSError:
+        pass
+    return {"value": tokens / med, "unit": "read-tokens/s", "cores": torch.get_num_threads(), "cpu_model": model,
+            "kind": "port",
             "sample": f"oracle chain (restated reference read, torch CPU) {cfg.name} with T={tokens} tokens, "
                       f"{'fwd+bwd' if cfg.backward else 'fwd'}, median of {len(times)} runs, {med:.3f} s/run"}
 
