@@ -83,43 +83,3 @@ def test_linear_block_chain_matches_oracle(K, R, dtype, mode):
         for a, b, c in zip(g, gr, g64):
             assert err_norm(a, c) <= 2 * err_norm(b, c) + 2e-3
 
-
-def _held_by_kept_loss(mode, K=2, R=4, n_tok=8192, d=256, dtype=torch.bfloat16):
-    """Bytes still allocated after one chain's backward when only its loss is kept (inputs, parameters and their
-    gradients excluded), and the size of the pass's stacks (V, R and their gradients)."""
-    from loopback_amd.cell import LoopDeltaAttnRes
-    g = torch.Generator().manual_seed(0)
-    cell = LoopDeltaAttnRes(d, R, K, beta=BETA, eps=EPS).to(DEV)
-    with torch.no_grad():
-        cell.query.copy_(torch.randn(K * R - 1, d, generator=g) * 0.5)
-    Ws = [(torch.randn(d, d, generator=g) * 0.03).to(DEV).requires_grad_() for _ in range(K * R)]
-    h0 = (torch.randn(1, n_tok, d, generator=g) * 0.5).to(DEV, dtype).requires_grad_()
-    torch.cuda.synchronize()
-    before = torch.cuda.memory_allocated()
-    stack = cell.new_stack(h0.shape, dtype, h0.device, mode=mode)
-    h, deltas, keys, coeffs, prior = h0, [], [], None, None
-    for s in range(K * R):
-        l, blk = divmod(s, K)
-        hs = (h.float() @ Ws[s]).to(dtype) + h
-        deltas.append(stack.write(s, hs, h))
-        h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
-    loss = (h.float() ** 2).mean()
-    loss.backward()
-    stack_bytes = 2 * (stack.V.numel() * stack.V.element_size() + stack.R.numel() * stack.R.element_size())
-    del stack, h, hs, deltas, keys, coeffs, prior
-    for p in (*Ws, h0, cell.query):
-        p.grad = None
-    torch.cuda.synchronize()
-    return torch.cuda.memory_allocated() - before, stack_bytes, loss
-
-
-@pytest.mark.parametrize("mode", ["stack", "scores"])
-def test_kept_loss_holds_no_stack(mode):
-    """A loss kept after its backward (a training loop that holds each micro-batch's loss until the optimizer step)
-    keeps none of the pass's stacked storage alive: the reference's memory check (tests/test_dattn_stack.py:161-199),
-    under 5 % of the stacks' bytes."""
-    print(f"case kept loss {mode}", flush=True)
-    _held_by_kept_loss(mode)   # warm-up
-    held, stack_bytes, kept = _held_by_kept_loss(mode)
-    assert held < 0.05 * stack_bytes, (held, stack_bytes)
-    del kept
