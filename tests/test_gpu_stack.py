@@ -8,7 +8,8 @@ against the oracle chain; mirrors tests/test_dattn_stack.py:68-199 of the refere
      the same read kernels (the stacked write forms the RMS scale itself, summed in another order, so they agree to
      fp32 round-off; bitwise when both take the scales from the same tensors);
   2. eval (no grad) chains, also with more iterations than trained (remapped queries);
-  3. memory: a loss kept after its backward holds no stack.
+  3. memory: a loss kept after its backward holds no stack;
+  4. misuse: the reference module's RuntimeError cases and this build's limits.
 """
 import pytest
 import torch
@@ -298,3 +299,51 @@ def test_empty_token_batch_priors(mode):
             torch.cuda.synchronize()
             assert coeffs.shape == (1, 0, s + 1)
             assert torch.allclose(prior.cpu().double(), oprior, rtol=1e-6, atol=0), (s, prior, oprior)
+
+
+def test_misuse_raises():
+    """The reference module's RuntimeError cases (fused_dattn.py:371, 714, 733-734) and this build's limits, each
+    raised before any launch: a stacked read whose base is not the stack's dtype or is not contiguous; a scale's
+    backward before any read's; accumulating list reads run backward out of order (a source without a buffer); an
+    rstd input of an unsupported dtype; a list read of a width the kernels do not take."""
+    from loopback_amd import fused_dattn as FD
+    d, t, n = 64, 8, 2
+    stack = FD.DattnStack(3, (1, t, d), torch.bfloat16, DEV)
+    xs = [torch.randn(1, t, d, device=DEV, dtype=torch.bfloat16) for _ in range(3)]
+    with torch.no_grad():
+        ups = [stack.write(s, xs[s], torch.zeros_like(xs[s])) for s in range(n)]
+        scales = [stack.rstd(s, ups[s], 1e-6) for s in range(n)]
+    q = torch.zeros(d, device=DEV)
+    cbar = torch.ones(1, t, n, device=DEV)
+    c0 = torch.ones(n, device=DEV)
+    with pytest.raises(RuntimeError, match="base"):
+        FD.FusedDattnReadStk.apply(stack, 1, q, xs[2].float(), cbar, c0, *ups, *scales)
+    wide = torch.randn(1, t, 2 * d, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="base"):
+        FD.FusedDattnReadStk.apply(stack, 1, q, wide[..., :d], cbar, c0, *ups, *scales)
+
+    lone = FD.DattnStack(2, (1, t, d), torch.float32, DEV)
+    delta = torch.randn(1, t, d, device=DEV, requires_grad=True)
+    r = lone.rstd(0, delta, 1e-6)
+    with pytest.raises(RuntimeError, match="before any read"):
+        r.sum().backward()
+
+    vals = [torch.randn(1, t, d, device=DEV, requires_grad=True) for _ in range(3)]
+    rs = [FD.rstd(v, 1e-6) for v in vals]
+    acc = FD.DattnGradAccum()
+    base = torch.randn(1, t, d, device=DEV)
+    out1, _ = FD.FusedDattnReadAcc.apply(acc, 1, q, base, torch.ones(1, t, 2, device=DEV), torch.ones(2, device=DEV),
+                                         *vals[:2], *rs[:2])
+    out2, _ = FD.FusedDattnReadAcc.apply(acc, 2, q, base, torch.ones(1, t, 3, device=DEV), torch.ones(3, device=DEV),
+                                         *vals, *rs)
+    out1.sum().backward(retain_graph=True)      # read 1 first: only two buffers
+    with pytest.raises(RuntimeError, match="out of order"):
+        out2.sum().backward()
+
+    with pytest.raises(RuntimeError, match="float64"):
+        FD.rstd(torch.randn(1, t, d, device=DEV, dtype=torch.float64), 1e-6)
+    odd = [torch.randn(1, t, 12, device=DEV) for _ in range(2)]
+    with pytest.raises(RuntimeError, match="unsupported"):
+        FD.FusedDattnRead.apply(torch.zeros(12, device=DEV), torch.randn(1, t, 12, device=DEV),
+                                torch.ones(1, t, 2, device=DEV), torch.ones(2, device=DEV), *odd,
+                                *[FD.rstd(x, 1e-6) for x in odd])
