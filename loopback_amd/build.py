@@ -1,14 +1,19 @@
 """Build libloopback_read.so (the read's kernels and C ABI) and libloopback_probe.so (the streaming-ceiling probes of
 stream_probe.py) in-tree with hipcc for gfx950 (MI355X).
 
-    python -m loopback_amd.build            # compile, print the commands
+    python -m loopback_amd.build                          # compile, print the commands
+    python -m loopback_amd.build -D LDR_RF_GRID=768 ...   # with launch settings other than the measured defaults
 
-The libraries land next to this file, so they travel with the source tree to the GPU box; nothing is installed.
-Compiling needs hipcc only, not a GPU.
+The launch settings (the LDR_* constants at the top of csrc/loopback_read.hip: sources per batch, workgroups,
+tile sizes, staging space) are compile-time constants of the kernels; -D NAME=VALUE (or LOOPBACK_READ_DEFINES,
+space-separated NAME=VALUE words) sets them for a build -- the counterpart of the reference module's tunable launch
+globals (fused_dattn.py:43-52). The libraries land next to this file, so they travel with the source tree to the GPU
+box; nothing is installed. Compiling needs hipcc only, not a GPU.
 """
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -34,9 +39,20 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: str, lib: str, verbose: bool) -> None:
+_DEFINE = re.compile(r"LDR_[A-Z0-9_]+(=[A-Za-z0-9_.+-]+)?")
+
+
+def _defines(defines) -> list[str]:
+    words = list(defines or []) + os.environ.get("LOOPBACK_READ_DEFINES", "").split()
+    for w in words:
+        if not _DEFINE.fullmatch(w):
+            raise ValueError(f"loopback_read build: a define must be LDR_NAME[=VALUE], got {w!r}")
+    return [f"-D{w}" for w in words]
+
+
+def _compile(src: str, lib: str, verbose: bool, defines=None) -> None:
     tmp = lib + ".tmp"
-    cmd = [hipcc(), *FLAGS, f"-I{INCLUDE}", "-o", tmp, src]
+    cmd = [hipcc(), *FLAGS, *_defines(defines), f"-I{INCLUDE}", "-o", tmp, src]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -45,13 +61,18 @@ def _compile(src: str, lib: str, verbose: bool) -> None:
     os.replace(tmp, lib)
 
 
-def build(verbose: bool = True) -> str:
-    """Compile both libraries (always; a stale build never survives a call); returns the read library's path."""
-    _compile(SRC, LIB, verbose)
+def build(verbose: bool = True, defines=None) -> str:
+    """Compile both libraries (always; a stale build never survives a call); returns the read library's path.
+    defines: NAME=VALUE launch settings for the read library (see the module docstring)."""
+    _compile(SRC, LIB, verbose, defines)
     _compile(PROBE_SRC, PROBE_LIB, verbose)
     return LIB
 
 
 if __name__ == "__main__":
-    build()
+    import argparse
+    ap = argparse.ArgumentParser(description="build the loopback_read and probe libraries for gfx950")
+    ap.add_argument("-D", dest="defines", action="append", default=[], metavar="LDR_NAME=VALUE",
+                    help="a launch setting of the read kernels (repeatable)")
+    build(defines=ap.parse_args().defines)
     sys.exit(0)

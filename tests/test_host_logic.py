@@ -115,3 +115,16 @@ def test_remap_query_rows():
     assert torch.equal(remap_query(q, K, R0, 1, "last"), q[:K - 1])
     with pytest.raises(ValueError):
         remap_query(q, K, R0, 4, "first")
+
+
+def test_build_defines(monkeypatch):
+    """The launch settings a build takes (the counterpart of the reference module's tunable launch globals):
+    LDR_NAME=VALUE words from -D and from LOOPBACK_READ_DEFINES, nothing else."""
+    from loopback_amd.build import _defines
+    monkeypatch.delenv("LOOPBACK_READ_DEFINES", raising=False)
+    assert _defines(["LDR_RF_GRID=768"]) == ["-DLDR_RF_GRID=768"]
+    monkeypatch.setenv("LOOPBACK_READ_DEFINES", "LDR_B1_TT=16 LDR_NT=0")
+    assert _defines([]) == ["-DLDR_B1_TT=16", "-DLDR_NT=0"]
+    for bad in (["RF_GRID=1"], ["LDR_X=1; rm"], ["-O0"]):
+        with pytest.raises(ValueError):
+            _defines(bad)
