@@ -43,7 +43,7 @@ extern "C" {
 #define LDR_E_ALIGN (-3)  /* a vector pointer is not 16-byte aligned */
 #define LDR_E_DTYPE (-4)  /* dtype is neither LDR_F32 nor LDR_BF16 (nor LDR_F16 where taken) */
 
-/* Version of this ABI; bumped on any signature change. */
+/* Version of this ABI; bumped on any signature change or change of what an entry point accepts. */
 int ldr_abi_version(void);
 
 /* Human-readable text for a return code of any entry point (static storage). */

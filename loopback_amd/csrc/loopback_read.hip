@@ -1645,7 +1645,7 @@ template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 8; }
+int ldr_abi_version(void) { return 9; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
