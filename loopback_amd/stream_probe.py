@@ -3,6 +3,8 @@
   * read-only, 32 sources of 64 MiB streamed row by row (the read kernels' pattern, nothing written);
   * the same with one 4 KiB row written per row set (1 write per 32 reads, the read forward's mix), each row right
     after its reads, or 16 consecutive rows kept in LDS and written together (the read forward's staged output);
+  * the write step's traffic, two rows in and one out per token (16384 x 2048 bf16), in the write kernel's chunked
+    layout (128 bytes of a row per lane group) and in whole rows per wave;
   * a device copy (1 read, 1 write per element);
 each at several grid sizes, best of 5. Reported as GB/s of the bytes each probe moves, beside the 8 TB/s peak.
 
@@ -31,6 +33,9 @@ def _lib():
                              ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     lib.ldp_read_burst.restype = ctypes.c_int
     lib.ldp_read_burst.argtypes = lib.ldp_read.argtypes
+    lib.ldp_write.restype = ctypes.c_int
+    lib.ldp_write.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                              ctypes.c_void_p]
     lib.ldp_copy.restype = ctypes.c_int
     lib.ldp_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
     return lib
@@ -83,6 +88,15 @@ def main():
                      "read_32_sources_write_1_burst16": (src_bytes + rows * row_bytes) / rb / 1e9,
                      "copy": src_bytes / cp / 1e9}
     best = {k: max(r[k] for r in res.values()) for k in next(iter(res.values()))}
+    # the write step's traffic (h, x in; v out; 16384 rows of 2048 bf16), its own grid of 64-token workgroups
+    wrows = 16384
+    hw = src[0].view(torch.bfloat16)[: wrows * 2048]
+    xw = src[1].view(torch.bfloat16)[: wrows * 2048]
+    vw = out.view(torch.bfloat16)[: wrows * 2048]   # out holds exactly 16384 x 2048 bf16
+    for which, key in ((0, "write_h_x_chunked"), (1, "write_h_x_rows")):
+        t = _best(lambda: check(lib.ldp_write(ctypes.c_void_p(hw.data_ptr()), ctypes.c_void_p(xw.data_ptr()),
+                                              ctypes.c_void_p(vw.data_ptr()), wrows, which, st), key))
+        best[key] = 3 * wrows * 2048 * 2 / t / 1e9
     print(json.dumps({"metric": "streaming ceilings (GB/s of bytes moved)", "peak_gbs": PEAK_GBS, "best": best,
                       "by_grid": {str(g): r for g, r in res.items()}}), flush=True)
     print("| probe | best GB/s | of peak |")
