@@ -9,7 +9,8 @@ against the oracle chain; mirrors tests/test_dattn_stack.py:68-199 of the refere
      fp32 round-off; bitwise when both take the scales from the same tensors);
   2. eval (no grad) chains, also with more iterations than trained (remapped queries);
   3. memory: a loss kept after its backward holds no stack;
-  4. misuse: the reference module's RuntimeError cases and this build's limits.
+  4. misuse: the reference module's RuntimeError cases and this build's limits;
+  5. streams: a chain on a side stream, fwd+bwd, bitwise the default-stream chain.
 """
 import pytest
 import torch
@@ -347,3 +348,29 @@ def test_misuse_raises():
         FD.FusedDattnRead.apply(torch.zeros(12, device=DEV), torch.randn(1, t, 12, device=DEV),
                                 torch.ones(1, t, 2, device=DEV), torch.ones(2, device=DEV), *odd,
                                 *[FD.rstd(x, 1e-6) for x in odd])
+
+
+@pytest.mark.parametrize("mode", ["list", "stack", "scores"])
+def test_chain_on_a_side_stream_is_bitwise_the_default_one(mode):
+    """Every launch goes on the caller's current stream (the autograd thread's too, for the backward): a chain whose
+    inputs are produced on a side stream right before it, run there fwd+bwd, gives the same bits as on the default
+    stream (the kernels are deterministic; a launch on another stream could race those inputs)."""
+    from loopback_amd.chain import ChainConfig, make_inputs, run_chain
+    cfg = ChainConfig(f"side-{mode}", 256, 2, 3, 1, 2048, torch.bfloat16, True, q_std=0.5)
+    h0, D, Q, G = make_inputs(cfg, "cpu")
+    ref_h, ref_loss, ref_g = run_chain(cfg, h0.to(DEV), [x.to(DEV) for x in D], Q.to(DEV), G.to(DEV), mode)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        big = torch.randn(4096, 4096, device=DEV)
+        for _ in range(4):
+            big = big @ big.T * 1e-3             # keep the side stream busy ahead of the chain
+        hd = (h0.to(DEV).float() + 0 * big[0, 0]).to(h0.dtype)   # the inputs depend on that work
+        Dd = [x.to(DEV) for x in D]
+        h, loss, g = run_chain(cfg, hd, Dd, Q.to(DEV), G.to(DEV), mode)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(h, ref_h) and torch.equal(loss, ref_loss)
+    assert torch.equal(g["h0"], ref_g["h0"]) and torch.equal(g["query"], ref_g["query"])
+    assert all(torch.equal(a, b) for a, b in zip(g["D"], ref_g["D"]))
