@@ -52,6 +52,9 @@
 #ifndef LDR_B1_WAVE_ROWS
 #define LDR_B1_WAVE_ROWS 1   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
+#ifndef LDR_WM_ROWS
+#define LDR_WM_ROWS 1        // write: rows streamed whole (d a multiple of 256), else in the matrix cores' layout
+#endif
 #ifndef LDR_NT
 #define LDR_NT 1             // non-temporal loads for the streamed sources
 #endif
@@ -639,6 +642,140 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
           for (int mb = 0; mb < WM_MB; ++mb)
             acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qh), acc[mb][b],
                                                                  0, 0, 0);
+        }
+  }
+#pragma unroll
+  for (int mb = 0; mb < WM_MB; ++mb) {
+    ss[mb] += __shfl_xor(ss[mb], 16, 64);
+    ss[mb] += __shfl_xor(ss[mb], 32, 64);
+    if (quad == 0) s_ss[w][mb][row] = ss[mb];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) s_part[w][mb][b][l] = acc[mb][b];
+  }
+  __syncthreads();
+  if (tid < 16 * WM_MB) {
+    const int mb = tid >> 4, rr = tid & 15;
+    const float tot = ((s_ss[0][mb][rr] + s_ss[1][mb][rr]) + s_ss[2][mb][rr]) + s_ss[3][mb][rr];
+    const int64_t tok = t0 + tid;
+    if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
+  }
+  if constexpr (NB > 0) {   // the scores (NB = 0 writes none)
+    for (int e = tid; e < WM_MB * NB * 64; e += WG) {
+      const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
+      const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
+      const int jj = 16 * b + (ll & 15);
+      if (jj >= nq) continue;
+      const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
+      float* dst = dots + (int64_t)jj * dots_jstride + tok;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (tok + i < n_tok) dst[i] = sum[i];
+    }
+  }
+}
+
+// The write with rows streamed whole (d a multiple of 256): per 256-column step, wave w moves 16 rows of h and x in
+// 512-byte row segments (32 lanes per row), stores V row-major and puts it in an LDS tile; then each wave runs the
+// matrix-core product of its 64-column quarter (chunk 4 step + w, as k_write_mfma's chunks) on the tile. The chunk
+// order per wave, the operands and the order of every sum are k_write_mfma's: V, R and the scores are its bits.
+template <int NB>
+__global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h, const bf16_t* __restrict__ x,
+                                                   bf16_t* __restrict__ v, float* __restrict__ r,
+                                                   const bf16_t* __restrict__ qb, int64_t qb_part_stride,
+                                                   float* __restrict__ dots, int64_t n_tok, int d, int nq,
+                                                   int64_t dots_jstride, float eps) {
+  constexpr int NBA = NB > 0 ? NB : 1;
+  constexpr int KS = 4 * WM_KC;   // columns per step
+  __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
+  __shared__ float s_ss[4][WM_MB][16];
+  __shared__ uint4 s_a[WM_TT][KS / 8 + 1];   // the step's V tile (a 16-byte pad per row)
+  const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * WM_TT;
+  f32x4_t acc[WM_MB][NBA];
+#pragma unroll
+  for (int mb = 0; mb < WM_MB; ++mb)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[WM_MB];
+#pragma unroll
+  for (int mb = 0; mb < WM_MB; ++mb) ss[mb] = 0.f;
+  int qrow[NBA];
+#pragma unroll
+  for (int b = 0; b < NBA; ++b) qrow[b] = min(16 * b + row, nq > 0 ? nq - 1 : 0);
+  // this lane's rows in the streaming layout: 16 w + 2 i + (l / 32), i < 8, vector column l % 32 of the step
+  const int lr = l & 31, lh = l >> 5;
+  int64_t rof[8];
+  bool rok[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t tok = t0 + 16 * w + 2 * i + lh;
+    rok[i] = tok < n_tok;
+    rof[i] = (rok[i] ? tok : n_tok - 1) * (int64_t)d;
+  }
+  auto load_rows = [&](int st, uint4 (&hr)[8], uint4 (&xr)[8]) {
+    const int col = st * KS + lr * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      hr[i] = *reinterpret_cast<const uint4*>(h + rof[i] + col);
+      xr[i] = *reinterpret_cast<const uint4*>(x + rof[i] + col);
+    }
+  };
+  const int nsteps = d / KS;
+  uint4 hr[8], xr[8];
+  load_rows(0, hr, xr);
+  for (int st = 0; st < nsteps; ++st) {
+    const int c = 4 * st + w;   // this wave's chunk of the step
+    int cc[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) cc[hf] = c * WM_KC + quad * WM_QS + WM_HS * hf;
+    uint4 qv[3][NBA][2];   // the chunk's query parts (cache-resident)
+#pragma unroll
+    for (int p = 0; p < 3 * (NB > 0); ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          qv[p][b][hf] = *reinterpret_cast<const uint4*>(qb + p * qb_part_stride + (int64_t)qrow[b] * d + cc[hf]);
+    uint4 hc[8], xc[8];   // this step's rows; the next step's are requested now
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { hc[i] = hr[i]; xc[i] = xr[i]; }
+    if (st + 1 < nsteps) load_rows(st + 1, hr, xr);   // uniform branch
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float hv[8], xv[8], vv[8];
+      IO<bf16_t>::unpack(IO<bf16_t>::Raw{hc[i]}, hv);
+      IO<bf16_t>::unpack(IO<bf16_t>::Raw{xc[i]}, xv);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) vv[k] = rok[i] ? hv[k] - xv[k] : 0.f;
+      const u32x4 u{pack2(vv[0], vv[1]), pack2(vv[2], vv[3]), pack2(vv[4], vv[5]), pack2(vv[6], vv[7])};
+      // non-temporal: the read that follows streams V[s] with its other sources
+      if (rok[i]) __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(v + rof[i] + st * KS + lr * 8));
+      s_a[16 * w + 2 * i + lh][lr] = make_uint4(u.x, u.y, u.z, u.w);
+    }
+    __syncthreads();
+    uint4 va[WM_MB][2];
+#pragma unroll
+    for (int mb = 0; mb < WM_MB; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const uint4 u = s_a[16 * mb + row][w * (WM_KC / 8) + quad + 4 * hf];
+        va[mb][hf] = u;
+        float rv[8];
+        IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss[mb] += rv[k] * rv[k];
+      }
+    __syncthreads();   // the tile is read before the next step overwrites it
+#pragma unroll
+    for (int p = 0; p < 3 * (NB > 0); ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+          for (int mb = 0; mb < WM_MB; ++mb)
+            acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qv[p][b][hf]),
+                                                                 acc[mb][b], 0, 0, 0);
         }
   }
 #pragma unroll
@@ -1728,8 +1865,10 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
   if (dtype == LDR_BF16) {   // matrix-core scores
     const unsigned grid = (unsigned)cdiv(n_tok, WM_TT);
     const bf16_t* qbp = nq > 0 ? static_cast<const bf16_t*>(qb) : nullptr;
+    const bool rows = LDR_WM_ROWS && d % (4 * WM_KC) == 0;   // rows streamed whole when d is whole steps
 #define LDR_WM_LAUNCH(NBV)                                                                                        \
-  hipLaunchKernelGGL(k_write_mfma<NBV>, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(h),               \
+  hipLaunchKernelGGL((rows ? k_write_rows<NBV> : k_write_mfma<NBV>), dim3(grid), dim3(WG), 0, st,                \
+                     static_cast<const bf16_t*>(h),                                                               \
                      static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), r_out, qbp, qb_part_stride, dots, \
                      n_tok, (int)d, (int)nq, dots_jstride, eps)
     if (nq == 0) LDR_WM_LAUNCH(0);

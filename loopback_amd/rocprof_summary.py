@@ -22,7 +22,7 @@ import os
 import sys
 
 FAMILIES = [("k_read_fwd", "read_fwd"), ("k_read_online", "read_fwd_online"), ("k_bwd1", "read_bwd1"), ("k_dv_assemble", "dv_assemble"),
-            ("k_write_mfma", "write_dots"), ("k_write_dots", "write_dots"), ("k_dots", "dots_online"),
+            ("k_write_mfma", "write_dots"), ("k_write_rows", "write_dots"), ("k_write_dots", "write_dots"), ("k_dots", "dots_online"),
             ("k_reduce_rows", "reduce_rows"), ("k_split_queries", "split_queries"), ("k_rstd", "rstd"),
             ("k_bwd2_list", "read_bwd2_list"), ("k_blend_sum", "blend_sum")]
 COPY_BYTES = 1 << 30   # bench.py --copy-calibration copies 1 GiB
@@ -40,7 +40,7 @@ def _rows(path):
         return list(csv.DictReader(f))
 
 
-FWD_KERNELS = ("k_split_queries", "k_write_mfma", "k_write_dots", "k_rstd_fwd", "k_read_fwd", "k_read_online", "k_dots")
+FWD_KERNELS = ("k_split_queries", "k_write_mfma", "k_write_rows", "k_write_dots", "k_rstd_fwd", "k_read_fwd", "k_read_online", "k_dots")
 BWD_KERNELS = ("k_bwd1", "k_dv_assemble", "k_reduce_rows", "k_blend_sum", "k_bwd2_list", "k_rstd_bwd")
 
 
