@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("T,d", [(37, 64), (100, 768), (257, 1096), (64, 2048), (19, 40), (5, 8)])
-@pytest.mark.parametrize("N", [2, 9, 33])
+@pytest.mark.parametrize("N", [2, 9, 33, 64])   # 64: up to 63 queries, the 4-block score kernels
 def test_write_scores(dtype, T, d, N):
     from loopback_amd import fused_dattn as FD
     from oracle.reference_read import rstd_ref
