@@ -1,33 +1,42 @@
 """Benchmark of the Loopback depth-attention read on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--mode scores] [--no-cpu-baseline]
+                    [--no-extra-configs]
 
 A step is one pass of the read path over one batch: the K x R chain of the benchmark configuration (default
 config 4: d=2048, K=4, R=8 -> N=32 updates, 31 reads, T = 8 x 2048 tokens, bf16 updates, fp32 scores), forward and
 backward -- N writes (with the read-query scores), N-1 reads, their backwards, the updates' gradients -- with the
-synthetic blocks x -> x + D_s and the caller's torch glue included. Inputs are resident in HBM before timing.
+synthetic blocks x -> x + D_s and the caller's glue included. Inputs are resident in HBM before timing.
 
 Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / wall time), plus
-  roofline      the dominant kernel (most time per pass): its compulsory bytes per launch / its mean launch
-                duration, from HIP events on the launch stream during the last timed step, against 8 TB/s;
-  chain         every library kernel of the pass: compulsory bytes / summed kernel time, and the reference
-                dataflow's bytes (its backward read-modify-writes a gradient stack) over the same time and over
-                the wall time;
-  cpu_baseline  the CPU oracle (the restated reference read, fp32/bf16 torch on the host cores) on a bounded sample
-                of the same chain (T reduced), fwd+bwd, tokens/s.
+  roofline      the dominant kernel (most time per pass): the reference dataflow's algorithmic bytes per launch for
+                that kernel (the survey's per-kernel rows: a read moves n sources, its base and its output) / its mean
+                launch duration, from HIP events on the launch stream during the last timed step, against 8 TB/s;
+                the HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE for this source (the committed
+                profile, labelled with the kernel source it was measured on);
+  chain         every library kernel of the pass: this build's compulsory bytes / summed kernel time, and the
+                reference dataflow's bytes (its backward read-modify-writes a gradient stack) over the same time and
+                over the wall time;
+  configs       configs 2 and 3 timed the same way (wall time per pass; --no-extra-configs skips them);
+  cpu_baseline  the CPU oracle (the restated reference read, torch on the host cores) on a bounded sample of the
+                same chain (T reduced), fwd+bwd, read-tokens/s and effective GB/s; beside it config 1 (the
+                reference's CPU case: d=768, N=8, 512 tokens, fp32, forward) as the survey plans it.
 """
 from __future__ import annotations
 
 import argparse
 import contextlib
 import gc
+import hashlib
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
 
 
 def parse():
@@ -40,6 +49,7 @@ def parse():
     ap.add_argument("--graph", action="store_true",
                     help="forward-only configs: time replays of the pass captured in a HIP graph (no host work)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-configs", action="store_true", help="skip the c2 / c3 timings of the default run")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the CPU baseline sample")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device to device once (torch copy kernel): the known-size reference that "
@@ -86,25 +96,35 @@ class KernelTimer:
         return {k: {"launches": v[0], "total_ms": v[1], "mean_us": 1e3 * v[1] / v[0]} for k, v in out.items()}
 
 
-def family_bytes(cfg, mode):
-    """Compulsory HBM bytes per pass (T tokens) of each kernel family of this build -- what each kernel must move:
-    write 3 rows per token (h, x in; V out), read (n+2) (n sources, base in; out; with online scores the same, in one pass), backward pass 1
-    (n+1) (n sources, g), update gradient (m+3) (the m output gradients of the reads holding the update, the update,
-    the result and its negation for the write's x) -- in rows of e * d bytes; per-(token, source) fp32 scalars left
-    out (< 1 %). With the caller's glue in the stacked read, a read at an iteration end also reads h0, the update
-    gradient of each update a read took as its proposal adds the proposal's share (the add autograd would otherwise
-    run) from that read's output gradient, which it reads anyway, and the iteration ends' shares of h0's gradient
-    are summed once (blend_sum: one output gradient per iteration end in, one row out).
-    Also the reference dataflow's total (its compulsory rows per token, e d (5N + 4 S2 + 4(N-1))), which moves more in
-    its backward."""
+def torch_bf16():
+    import torch
+    return torch.bfloat16
+
+
+def _shape(cfg, mode):
     from loopback_amd.cell import fuse_glue
-    from loopback_amd.chain import algorithmic_bytes_per_token
     e = 2 if cfg.dtype == torch_bf16() else 4
     N, T = cfg.N, cfg.n_tok
     S2 = N * (N + 1) // 2 - 1
-    row = e * cfg.d * T
     fused = mode != "list" and fuse_glue()
     ends = sum(1 for s in range(1, N) if s % cfg.K == cfg.K - 1) if fused else 0
+    return e, N, T, S2, ends, e * cfg.d * T
+
+
+def family_bytes(cfg, mode):
+    """Compulsory HBM bytes per pass (T tokens) of each kernel family of this build -- what each kernel must move:
+    write 3 rows per token (h, x in; V out), read (n+2) (n sources, base in; out; with online scores the same, in
+    one pass), backward pass 1 (n+1) (n sources, g), update gradient (m+3) (the m output gradients of the reads
+    holding the update, the update, the result and its negation for the write's x) -- in rows of e * d bytes;
+    per-(token, source) fp32 scalars left out (< 1 %). With the caller's glue in the stacked read, a read at an
+    iteration end also reads h0, the update gradient of each update a read took as its proposal adds the proposal's
+    share (the add autograd would otherwise run) from that read's output gradient, which it reads anyway, and the
+    iteration ends' shares of h0's gradient are summed once (blend_sum: one output gradient per iteration end in,
+    one row out).
+    Also the reference dataflow's total (its compulsory rows per token, e d (5N + 4 S2 + 4(N-1))), which moves more in
+    its backward."""
+    from loopback_amd.chain import algorithmic_bytes_per_token
+    e, N, T, S2, ends, row = _shape(cfg, mode)
     read = "read_fwd" if mode == "scores" else "read_fwd_online"   # online scores: formed in the same pass
     fam = {"write_dots": 3 * N * row, read: (S2 + 2 * (N - 1) + ends) * row}
     if cfg.backward:
@@ -116,38 +136,144 @@ def family_bytes(cfg, mode):
     return fam, ref_total
 
 
-def torch_bf16():
-    import torch
-    return torch.bfloat16
+def survey_bytes(cfg, mode):
+    """The reference dataflow's algorithmic bytes per pass of the work each kernel family does (the survey's rows
+    per token, without this build's extras): the write 3N, the reads sum_s (n + 2) (n sources, base, out), backward
+    pass 1 sum_s (n + 1); the update gradient does the reference's backward pass 2 and scale-gradient
+    accumulation, (N - 1) + N + 2 (S2 - N) + 3N. The fused blend's h0 rows (reads at an iteration end) are
+    counted apart (`extra_rows_per_pass`). blend_sum has no counterpart in the reference's kernels."""
+    e, N, T, S2, ends, row = _shape(cfg, mode)
+    read = "read_fwd" if mode == "scores" else "read_fwd_online"
+    out = {"write_dots": 3 * N * row, read: (S2 + 2 * (N - 1)) * row}
+    if cfg.backward:
+        out["read_bwd1"] = (S2 + N - 1) * row
+        out["dv_assemble"] = ((N - 1) + N + 2 * (S2 - N) + 3 * N) * row
+    return out, {read: ends}
 
 
-def cpu_baseline(cfg, tokens):
-    """The oracle chain on the host cores, fwd(+bwd), on `tokens` tokens of the same configuration."""
+def source_sha256() -> str:
+    with open(os.path.join(ROOT, "loopback_amd", "csrc", "loopback_read.hip"), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
+def committed_traffic(config, mode, dom):
+    """HBM bytes per launch of `dom` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this
+    configuration (profiles/traffic_chain_<config>.txt, copy-calibrated), labelled with the kernel source it was
+    measured on and whether that is this build's source."""
+    path = os.path.join(ROOT, "profiles", f"traffic_chain_{config}.txt")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        tr = json.load(f)
+    if tr.get("mode") != mode or dom not in tr.get("hbm_bytes_per_launch", {}):
+        return None, None
+    measured_on = tr.get("source_sha256")
+    label = {"file": os.path.relpath(path, ROOT), "measured_on_source_sha256": measured_on,
+             "measured_at_commit": tr.get("commit"), "this_source_sha256": source_sha256(),
+             "current": measured_on == source_sha256()}
+    return tr["hbm_bytes_per_launch"][dom], label
+
+
+def time_chain(cfg, mode, steps, warmup, timer=None):
+    """Warm-up, then `steps` timed chain passes bracketed by synchronizations; returns (elapsed s, resident bytes,
+    peak bytes). With `timer`, the last timed pass brackets every library kernel with events."""
     import torch
+    from loopback_amd import fused_dattn as FD
+    from loopback_amd.chain import make_cell, make_inputs, run_chain
+    dev = torch.device("cuda", 0)
+    h0, D, Q, G = make_inputs(cfg, dev)
+    cell = make_cell(cfg, Q)   # the model's read cell, made once (a training loop keeps its model)
+    for _ in range(warmup):
+        run_chain(cfg, h0, D, Q, G, mode, cell=cell)
+    torch.cuda.synchronize()
+    # The interpreter's long-lived objects (torch, the loaded modules) go to the permanent generation, as a serving
+    # or training loop does after start-up: a full cyclic collection walks them all (~40 ms here) and would stall
+    # the launch stream once every few steps; the steps themselves create no cycles that need collecting.
+    gc.collect()
+    gc.freeze()
+    resident = torch.cuda.memory_allocated()   # the inputs and the cell, before any pass
+    torch.cuda.reset_peak_memory_stats()
+    t0 = time.perf_counter()
+    for step in range(steps):
+        if timer is not None and step == steps - 1:
+            FD._TIMER = timer      # the last timed step: every library kernel bracketed by events on its stream
+        run_chain(cfg, h0, D, Q, G, mode, cell=cell)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    FD._TIMER = None
+    gc.unfreeze()
+    peak = torch.cuda.max_memory_allocated()
+    del h0, D, Q, G, cell
+    torch.cuda.empty_cache()
+    return elapsed, resident, peak
+
+
+def cpu_model() -> str | None:
+    """The host CPU's model name, as lscpu reports it (else /proc/cpuinfo), with its family / model / stepping."""
+    name = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        name = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), None)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    ids = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ":" not in ln:
+                    if ids:
+                        break
+                    continue
+                k, v = (x.strip() for x in ln.split(":", 1))
+                if k in ("model name", "cpu family", "model", "stepping") and k not in ids:
+                    ids[k] = v
+    except OSError:
+        pass
+    name = name or ids.get("model name")
+    if name and all(k in ids for k in ("cpu family", "model", "stepping")):
+        name += f" (family {ids['cpu family']}, model {ids['model']}, stepping {ids['stepping']})"
+    return name
+
+
+def _cpu_time(cfg, tokens, min_s, max_s):
+    """Median seconds per oracle chain pass on `tokens` tokens (>= 5 runs after a warm-up, about min_s of work)."""
     from oracle.reference_read import run_chain
     from loopback_amd.chain import make_inputs
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     h0, D, Q, G = make_inputs(cfg, "cpu", n_tok=tokens)
     run_chain(cfg.K, cfg.R, h0, D, Q, G, beta=cfg.beta, eps=cfg.eps, grad=cfg.backward)   # warm-up
     times, t_start = [], time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < 10 and len(times) < 50):
+    while len(times) < 5 or (time.perf_counter() - t_start < min_s and len(times) < 50):
         t0 = time.perf_counter()
         run_chain(cfg.K, cfg.R, h0, D, Q, G, beta=cfg.beta, eps=cfg.eps, grad=cfg.backward)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > 30:
+        if time.perf_counter() - t_start > max_s:
             break
-    med = statistics.median(times)
-    model = None
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), None)
-    except OSError:
-        pass
-    return {"value": tokens / med, "unit": "read-tokens/s", "cores": torch.get_num_threads(), "cpu_model": model,
-            "kind": "port",
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(cfg, tokens):
+    """The oracle chain on the host cores on `tokens` tokens of the headline configuration (fwd+bwd), and config 1
+    (the reference's CPU case) whole; tokens/s and the effective GB/s of the reference dataflow's bytes."""
+    import torch
+    from loopback_amd.chain import CONFIGS, algorithmic_bytes_per_token
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    med, runs = _cpu_time(cfg, tokens, 10, 30)
+    e = 2 if cfg.dtype == torch.bfloat16 else 4
+    bpt = algorithmic_bytes_per_token(cfg.N, cfg.d, e, backward=cfg.backward)["total"]
+    c1 = CONFIGS["c1"]
+    med1, runs1 = _cpu_time(c1, c1.n_tok, 5, 15)
+    bpt1 = algorithmic_bytes_per_token(c1.N, c1.d, 4, backward=False, dots=False)["total"]
+    return {"value": tokens / med, "unit": "read-tokens/s", "cores": torch.get_num_threads(),
+            "affinity_cores": cores, "cpu_model": cpu_model(), "kind": "port",
+            "gbs": bpt * tokens / med / 1e9,
             "sample": f"oracle chain (restated reference read, torch CPU) {cfg.name} with T={tokens} tokens, "
-                      f"{'fwd+bwd' if cfg.backward else 'fwd'}, median of {len(times)} runs, {med:.3f} s/run"}
+                      f"{'fwd+bwd' if cfg.backward else 'fwd'}, median of {runs} runs, {med:.3f} s/run; gbs = the "
+                      f"reference dataflow's {bpt} B/token x tokens/s",
+            "config1": {"value": c1.n_tok / med1, "unit": "tokens/s", "gbs": bpt1 * c1.n_tok / med1 / 1e9,
+                        "sample": f"oracle chain {c1.name}: d=768, K=2, R=4, T={c1.n_tok}, fp32, fwd; median of "
+                                  f"{runs1} runs, {med1 * 1e3:.1f} ms/run; gbs = {bpt1} B/token (the DOTS-off form, "
+                                  f"e = 4) x tokens/s"}}
 
 
 def main():
@@ -163,17 +289,15 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
-    from loopback_amd import fused_dattn as FD
-    from loopback_amd.chain import CONFIGS, capture_forward, make_cell, make_inputs, run_chain
+    from loopback_amd.chain import CONFIGS, capture_forward, make_inputs
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
-    h0, D, Q, G = make_inputs(cfg, dev)
-    torch.cuda.synchronize()
     if args.graph:   # the forward pass as one HIP graph: no Python or launch work per pass
         if cfg.backward:
             print("bench.py: --graph times forward-only configurations (c2)", file=sys.stderr)
             sys.exit(2)
+        h0, D, Q, G = make_inputs(cfg, dev)
         graph, _ = capture_forward(cfg, h0, D, Q, args.mode)
         for _ in range(max(1, args.warmup)):
             graph.replay()
@@ -192,46 +316,20 @@ def main():
                           "config": {"workload": cfg.name, "mode": args.mode, "graph": True}}), flush=True)
         return
 
-    cell = make_cell(cfg, Q)   # the model's read cell, made once (a training loop keeps its model)
-    for _ in range(args.warmup):
-        run_chain(cfg, h0, D, Q, G, args.mode, cell=cell)
-    torch.cuda.synchronize()
-    # The interpreter's long-lived objects (torch, the loaded modules) go to the permanent generation, as a serving
-    # or training loop does after start-up: a full cyclic collection walks them all (~40 ms here) and would stall
-    # the launch stream once every few steps; the steps themselves create no cycles that need collecting.
-    gc.collect()
-    gc.freeze()
-    resident = torch.cuda.memory_allocated()   # the inputs and the cell, before any pass
-    torch.cuda.reset_peak_memory_stats()
     timer = KernelTimer()
-    t0 = time.perf_counter()
-    for step in range(args.steps):
-        if step == args.steps - 1:
-            FD._TIMER = timer      # the last timed step: every library kernel bracketed by events on its stream
-        run_chain(cfg, h0, D, Q, G, args.mode, cell=cell)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    FD._TIMER = None
-    peak = torch.cuda.max_memory_allocated()
+    elapsed, resident, peak = time_chain(cfg, args.mode, args.steps, args.warmup, timer)
     ms_per_step = 1e3 * elapsed / args.steps
     ksum = timer.summary()
     fam, ref_bytes = family_bytes(cfg, args.mode)
+    sv, extra_rows = survey_bytes(cfg, args.mode)
     own_bytes = sum(fam.values())
     dom = max((k for k in fam if k in ksum), key=lambda k: ksum[k]["total_ms"])
     launches = ksum[dom]["launches"]
-    bytes_per_launch = fam[dom] / launches
     mean_s = ksum[dom]["mean_us"] * 1e-6
-    achieved = bytes_per_launch / mean_s / 1e9
+    alg = sv.get(dom, fam[dom]) / launches           # the survey's bytes per launch of the dominant kernel
+    achieved = alg / mean_s / 1e9
     kernel_ms = sum(v["total_ms"] for v in ksum.values())
-    # HBM bytes per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of
-    # this configuration (profiles/traffic_chain_<config>.txt, copy-calibrated), when there is one for this mode
-    traffic = None
-    tr_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"traffic_chain_{args.config}.txt")
-    if os.path.exists(tr_path):
-        with open(tr_path) as f:
-            tr = json.load(f)
-        if tr.get("mode") == args.mode:
-            traffic = tr["hbm_bytes_per_launch"].get(dom)
+    traffic, traffic_label = committed_traffic(args.config, args.mode, dom)
 
     line = {
         "metric": ("depth-read tokens/sec (fwd+bwd), d=2048, N=32 stack" if args.config == "c4" else
@@ -250,22 +348,38 @@ def main():
         "config": {"workload": cfg.name, "d": cfg.d, "K": cfg.K, "R": cfg.R, "N": cfg.N, "tokens": cfg.n_tok,
                    "mode": args.mode, "backward": cfg.backward, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "algorithmic_bytes_per_launch": bytes_per_launch, "mean_launch_us": ksum[dom]["mean_us"],
-                     "launches_per_step": launches},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_label,
+                     "algorithmic_bytes_per_launch": alg, "mean_launch_us": ksum[dom]["mean_us"],
+                     "launches_per_step": launches,
+                     "extra_rows_per_pass": extra_rows.get(dom, 0),
+                     "build_bytes_per_launch": fam[dom] / launches,
+                     "build_frac": fam[dom] / launches / mean_s / 1e9 / HBM_PEAK_GBS},
         "chain": {"own_bytes_per_token": own_bytes / cfg.n_tok, "kernel_ms": kernel_ms,
                   "achieved_gbs": own_bytes / (kernel_ms * 1e-3) / 1e9,
                   "reference_formula_bytes_per_token": ref_bytes / cfg.n_tok,
                   "formula_gbs": ref_bytes / (kernel_ms * 1e-3) / 1e9,
                   "formula_wall_gbs": ref_bytes / (ms_per_step * 1e-3) / 1e9,
                   "kernels": {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 4),
-                                  "gbs": (fam[k] / (v["total_ms"] * 1e-3) / 1e9) if k in fam else None}
+                                  "gbs": (fam[k] / (v["total_ms"] * 1e-3) / 1e9) if k in fam else None,
+                                  "survey_gbs": (sv[k] / (v["total_ms"] * 1e-3) / 1e9) if k in sv else None}
                               for k, v in sorted(ksum.items())},
                   # device memory, as the reference's --bench reports it: the inputs resident before the passes,
                   # and the peak during them (the pass's stacks, saved tensors and gradients on top of the inputs)
                   "memory_gib": {"resident": resident / 2**30, "peak": peak / 2**30,
                                  "pass_peak": (peak - resident) / 2**30}},
     }
+    if args.config == "c4" and not args.no_extra_configs:
+        extra = {}
+        for key in ("c2", "c3"):
+            c = CONFIGS[key]
+            el, _, _ = time_chain(c, args.mode, 20, 5)
+            _, rb = family_bytes(c, args.mode)
+            ms = 1e3 * el / 20
+            extra[key] = {"workload": c.name, "ms_per_step": ms, "value": c.n_tok * 20 / el,
+                          "unit": "read-tokens/s", "backward": c.backward,
+                          "formula_wall_gbs": rb / (ms * 1e-3) / 1e9,
+                          "formula_wall_frac": rb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        line["configs"] = extra
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)
     print(json.dumps(line), flush=True)

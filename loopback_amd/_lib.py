@@ -82,7 +82,8 @@ def check(code: int, what: str) -> None:
 
 
 def u64_array(values) -> ctypes.Array:
-    vals = [int(v) for v in values]
+    """A host array of device addresses (ints) for a per-source argument."""
+    vals = values if isinstance(values, list) else list(values)
     return (ctypes.c_uint64 * max(1, len(vals)))(*vals)
 
 

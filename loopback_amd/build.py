@@ -1,5 +1,4 @@
-"""Build libloopback_read.so (the read's kernels and C ABI) and libloopback_probe.so (the streaming-ceiling probes of
-stream_probe.py) in-tree with hipcc for gfx950 (MI355X).
+"""Build libloopback_read.so (the read's kernels and C ABI) in-tree with hipcc for gfx950 (MI355X).
 
     python -m loopback_amd.build                          # compile, print the commands
     python -m loopback_amd.build -D LDR_RF_GRID=768 ...   # with launch settings other than the measured defaults
@@ -23,8 +22,9 @@ ROOT = os.path.dirname(HERE)
 SRC = os.path.join(HERE, "csrc", "loopback_read.hip")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libloopback_read.so")
-PROBE_SRC = os.path.join(HERE, "csrc", "stream_probe.hip")
-PROBE_LIB = os.path.join(HERE, "libloopback_probe.so")
+# A test fixture: the same source built with the write's matrix-core layout for every width (LDR_WM_ROWS=0), so the
+# GPU tests can check that the whole-row write kernel gives the matrix-core kernel's bits. Nothing else loads it.
+TEST_LIB_MFMA_WRITE = os.path.join(HERE, "libloopback_read_mfma_write.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code (plain fp32 VALU instead).
@@ -50,28 +50,36 @@ def _defines(defines) -> list[str]:
     return [f"-D{w}" for w in words]
 
 
-def _compile(src: str, lib: str, verbose: bool, defines=None) -> None:
+def _start(src: str, lib: str, verbose: bool, defines) -> tuple:
     tmp = lib + ".tmp"
     cmd = [hipcc(), *FLAGS, *_defines(defines), f"-I{INCLUDE}", "-o", tmp, src]
     if verbose:
         print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True), tmp, lib
+
+
+def _finish(job) -> None:
+    proc, tmp, lib = job
+    out, err = proc.communicate()
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}) for {os.path.basename(lib)}:\n{out}\n{err}")
     os.replace(tmp, lib)
 
 
 def build(verbose: bool = True, defines=None) -> str:
-    """Compile both libraries (always; a stale build never survives a call); returns the read library's path.
-    defines: NAME=VALUE launch settings for the read library (see the module docstring)."""
-    _compile(SRC, LIB, verbose, defines)
-    _compile(PROBE_SRC, PROBE_LIB, verbose)
+    """Compile the library (always; a stale build never survives a call) and, beside it, the test fixture
+    TEST_LIB_MFMA_WRITE (the two compiles run in parallel); returns the library's path.
+    defines: NAME=VALUE launch settings (see the module docstring)."""
+    jobs = [_start(SRC, LIB, verbose, defines),
+            _start(SRC, TEST_LIB_MFMA_WRITE, verbose, list(defines or []) + ["LDR_WM_ROWS=0"])]
+    for job in jobs:
+        _finish(job)
     return LIB
 
 
 if __name__ == "__main__":
     import argparse
-    ap = argparse.ArgumentParser(description="build the loopback_read and probe libraries for gfx950")
+    ap = argparse.ArgumentParser(description="build the loopback_read library for gfx950")
     ap.add_argument("-D", dest="defines", action="append", default=[], metavar="LDR_NAME=VALUE",
                     help="a launch setting of the read kernels (repeatable)")
     build(defines=ap.parse_args().defines)

@@ -94,6 +94,19 @@ constexpr int MAXS = LDR_MAX_SOURCES;
 constexpr int TT_MAX = 32;              // tokens per tile in the tiled kernels
 constexpr int SP = MAXS + 1;            // padded LDS row of per-source scalars
 
+// The launch settings a build may change, and the ranges the kernels are written for (a value outside them would
+// overflow a tile in LDS, leave rows unwritten or loop without advancing: the build refuses it).
+static_assert(LDR_RF_UNROLL >= 1 && LDR_RF_STAGE_U >= 1, "read forward: at least one source per batch");
+static_assert(LDR_RF_STAGE >= 0, "read forward: staging bytes must be >= 0");
+static_assert(LDR_RF_MAX_VPT >= 1 && LDR_RF_MAX_VPT <= 4 && LDR_AS_MAX_VPT >= 1 && LDR_AS_MAX_VPT <= 4 &&
+              LDR_B1_MAX_VPT >= 1 && LDR_B1_MAX_VPT <= 4, "vectors per lane: 1..4 (the kernels' instantiations)");
+static_assert(LDR_RF_VPT >= 0 && LDR_RF_VPT <= 4 && LDR_AS_VPT >= 0 && LDR_AS_VPT <= 4 && LDR_B1_VPT >= 0 &&
+              LDR_B1_VPT <= 4, "fixed vectors per lane: 0 (chosen from d) or 1..4");
+static_assert(LDR_AS_RB >= 1 && LDR_AS_JB >= 1, "update gradient: at least one row per lane and one read per batch");
+static_assert(LDR_B1_C >= 0 && LDR_B1_C <= 8, "backward pass 1: 0 (by vectors per lane) or 1..8 sources per chunk");
+static_assert(LDR_ON_PD >= 1 && LDR_ON_WAVES >= 1, "online read: at least one source in flight, one wave per SIMD");
+static_assert(LDR_AS_GRID >= 1 && LDR_RF_GRID >= 1 && LDR_ON_GRID >= 1 && LDR_B1_GRID >= 1, "grids: >= 1 workgroup");
+
 typedef uint16_t bf16_t;                // bf16 storage (raw bits)
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -322,26 +335,70 @@ __device__ __forceinline__ void load_prior(const Coef& c, int n, float* s_c0, fl
 // ---------------------------------------------------------------------------------------------------------------
 // rstd forward / backward (list layout, and the stacked layout's scale when the write did not store it)
 // ---------------------------------------------------------------------------------------------------------------
-template <typename T, int VPT>
-__global__ __launch_bounds__(WG) void k_rstd_fwd(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
-                                                 int d, int tpr, float eps) {
-  __shared__ float red[4];
-  const Rows R(d, tpr);
-  const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
-  for (int64_t gi = blockIdx.x; gi < groups; gi += gridDim.x) {
-    const int64_t tok = gi * R.rpw + R.rs;
-    const T* row = x + (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
-    float ss[1] = {0.f};
+// the fp32 write's tile: 32 tokens, d in chunks of 128 columns (k_write_dots)
+constexpr int WR_TT = 32, WR_KC = 128, WR_KP = WR_KC + 4, WR_MQ = 8;
+
+// The scale of a stored update is formed in one summation order wherever it is formed -- by the write kernels
+// (which store it beside the update) or by these kernels (the list layout's rstd, the stacked layout when the write
+// did not store it) -- so both layouts read with bitwise equal scales, and so bitwise equal outputs.
+//
+// bf16 rows: the order of k_write_mfma / k_write_rows. Columns go in 64-column chunks, chunk c to slot w = c mod 4;
+// inside a chunk, quad q takes columns [8q, 8q + 8) and [32 + 8q, 40 + 8q). Partial (w, q) is the fused
+// multiply-add sum over its chunks in order, its two column groups in order, and their elements in order. Then
+// W_w = (p_w0 + p_w1) + (p_w2 + p_w3), and sum = ((W_0 + W_1) + W_2) + W_3.
+// Here a row takes 16 lanes (lane 4 w + q holds partial (w, q)), 4 rows per wave.
+__global__ __launch_bounds__(WG) void k_rstd_bf16(const bf16_t* __restrict__ x, float* __restrict__ r, int64_t n_tok,
+                                                  int d, float eps) {
+  const int tid = (int)threadIdx.x, lane = tid & 63, j = lane & 15, w = j >> 2, quad = j & 3;
+  const int nchunks = (d + 63) >> 6;
+  for (int64_t t0 = (int64_t)blockIdx.x * (WG / 16); t0 < n_tok; t0 += (int64_t)gridDim.x * (WG / 16)) {
+    const int64_t tok = t0 + (tid >> 4);
+    const bf16_t* row = x + (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
+    float ss = 0.f;
+#pragma unroll 4
+    for (int c = w; c < nchunks; c += 4) {
 #pragma unroll
-    for (int v = 0; v < VPT; ++v) {
-      float e[8];
-      IO<T>::load(row + R.off(v), e);
-      const float keep = R.act(v) ? 1.f : 0.f;
+      for (int hf = 0; hf < 2; ++hf) {
+        const int col = c * 64 + quad * 8 + 32 * hf;
+        if (col < d) {   // d is a multiple of 8: a column group is whole or past the row
+          float e[8];
+          IO<bf16_t>::load(row + col, e);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) ss[0] += keep * e[k] * e[k];
+          for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(e[k], e[k], ss);
+        }
+      }
     }
-    row_sum<1>(ss, tpr, red);
-    if (tok < n_tok && R.lr == 0) r[tok] = rsqrtf(ss[0] / (float)d + eps);
+    ss += __shfl_xor(ss, 1, 64);   // (p_w0 + p_w1), (p_w2 + p_w3)
+    ss += __shfl_xor(ss, 2, 64);   // W_w
+    const int g0 = lane & ~15;
+    const float w0 = __shfl(ss, g0, 64), w1 = __shfl(ss, g0 + 4, 64), w2 = __shfl(ss, g0 + 8, 64),
+                w3 = __shfl(ss, g0 + 12, 64);
+    const float tot = ((w0 + w1) + w2) + w3;
+    if (tok < n_tok && j == 0) r[tok] = rsqrtf(tot / (float)d + eps);
+  }
+}
+
+// fp32 rows: the order of k_write_dots. Lane m of a row's 16 takes columns [c0 + 8m, c0 + 8m + 8) for c0 = 0, 128,
+// 256, ... (fused multiply-adds, chunks then elements in order); the 16 partials meet in the butterfly xor 8, 4, 2, 1.
+__global__ __launch_bounds__(WG) void k_rstd_f32(const float* __restrict__ x, float* __restrict__ r, int64_t n_tok,
+                                                 int d, float eps) {
+  const int tid = (int)threadIdx.x, m = tid & 15;
+  for (int64_t t0 = (int64_t)blockIdx.x * (WG / 16); t0 < n_tok; t0 += (int64_t)gridDim.x * (WG / 16)) {
+    const int64_t tok = t0 + (tid >> 4);
+    const float* row = x + (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
+    float ss = 0.f;
+#pragma unroll 4
+    for (int c0 = 0; c0 < d; c0 += WR_KC) {
+      const int col = c0 + 8 * m;
+      if (col < d) {
+        float e[8];
+        IO<float>::load(row + col, e);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(e[k], e[k], ss);
+      }
+    }
+    for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (tok < n_tok && m == 0) r[tok] = rsqrtf(ss / (float)d + eps);
   }
 }
 
@@ -411,7 +468,6 @@ __global__ __launch_bounds__(WG) void k_rstd_bwd_any(const T* __restrict__ x, co
 // A tile of 32 tokens streams d in chunks of 128 columns: the chunk of the update goes to LDS (fp32) next to the
 // chunk of up to 64 query rows, and 256 lanes form the 32 x nq dot products (lane = token + 32 * query group).
 // ---------------------------------------------------------------------------------------------------------------
-constexpr int WR_TT = 32, WR_KC = 128, WR_KP = WR_KC + 4, WR_MQ = 8;
 
 template <typename T>
 __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, const T* __restrict__ x,
@@ -443,7 +499,7 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
         for (int k = 0; k < 8; ++k) vv[k] = IO<T>::round(hv[k] - xv[k]);
         IO<T>::store(v + tok * (int64_t)d + col, vv);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) ss[e] += vv[k] * vv[k];
+        for (int k = 0; k < 8; ++k) ss[e] = __builtin_fmaf(vv[k], vv[k], ss[e]);   // the scale's order: k_rstd_f32
       } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) vv[k] = 0.f;
@@ -520,6 +576,9 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 #endif
 constexpr int WM_MB = LDR_WM_MB;   // 16-token blocks per workgroup
 constexpr int WM_TT = 16 * WM_MB;   // tokens per workgroup
+static_assert(WM_MB == 1 || WM_MB == 2 || WM_MB == 4, "write: 1, 2 or 4 16-token blocks per workgroup");
+// k_write_rows maps its 4 waves x 16 rows onto the workgroup's tokens: it takes 64-token workgroups only
+constexpr bool WM_ROWS = LDR_WM_ROWS && WM_MB == 4;
 constexpr int WM_KC = 64;   // columns per chunk
 constexpr int WM_QS = 8;    // column step between the quads of a wave
 constexpr int WM_HS = 32;   // column step between a lane's two k-groups
@@ -615,7 +674,7 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
         float rv[8];
         IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);   // the stored (rounded) update
 #pragma unroll
-        for (int k = 0; k < 8; ++k) ss[mb] += rv[k] * rv[k];
+        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(rv[k], rv[k], ss[mb]);   // k_rstd_bf16's order
         s_v[w][16 * mb + row][quad + 4 * hf] = u;
       }
     wave_lds_sync();
@@ -684,6 +743,7 @@ __global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h,
                                                    const bf16_t* __restrict__ qb, int64_t qb_part_stride,
                                                    float* __restrict__ dots, int64_t n_tok, int d, int nq,
                                                    int64_t dots_jstride, float eps) {
+  static_assert(WM_MB == 4, "k_write_rows: its 4 waves x 16 rows are the workgroup's 64 tokens");
   constexpr int NBA = NB > 0 ? NB : 1;
   constexpr int KS = 4 * WM_KC;   // columns per step
   __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
@@ -763,7 +823,7 @@ __global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h,
         float rv[8];
         IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) ss[mb] += rv[k] * rv[k];
+        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(rv[k], rv[k], ss[mb]);   // k_rstd_bf16's order
       }
     __syncthreads();   // the tile is read before the next step overwrites it
 #pragma unroll
@@ -806,6 +866,16 @@ __global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h,
         if (tok + i < n_tok) dst[i] = sum[i];
     }
   }
+}
+
+// the write kernel for bf16 updates: rows streamed whole when d is whole 256-column steps (and the build keeps
+// 64-token workgroups), else the matrix cores' layout; both give the same bits
+template <int NB>
+auto write_kernel(bool rows) {
+  if constexpr (WM_ROWS) {
+    if (rows) return &k_write_rows<NB>;
+  }
+  return &k_write_mfma<NB>;
 }
 
 // the three bf16 parts of fp32 query rows: qb[p][j][k], p = 0 (hi), 1 (mid), 2 (lo); q = hi + mid + lo
@@ -1737,6 +1807,9 @@ inline int tile_tokens(int tpr) { const int rpw = WG / tpr; return rpw > 16 ? rp
 #ifndef LDR_B1_TT
 #define LDR_B1_TT 32          // backward pass 1: tokens per tile (at least one row per row slot)
 #endif
+// a power of two <= TT_MAX: the tile is then a multiple of the rows per workgroup and fits the LDS planes
+static_assert(LDR_B1_TT >= 1 && LDR_B1_TT <= TT_MAX && (LDR_B1_TT & (LDR_B1_TT - 1)) == 0,
+              "backward pass 1: tokens per tile must be a power of two <= 32");
 inline int b1_tile(int tpr) { const int t = tile_tokens(tpr); return t > LDR_B1_TT ? t : LDR_B1_TT; }
 
 int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n, int64_t n_tok) {
@@ -1818,9 +1891,12 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
                                                 static_cast<const T*>(x), r, n_tok, d, eps))
     return launched();
   }
-  const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 8192);
-  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_rstd_fwd<T, VPT>), dim3(grid), dim3(WG), 0, st,
-                                                                  static_cast<const T*>(x), r, n_tok, (int)d, tpr, eps)))
+  // the write kernels' summation order (the same bits as the scale a stacked write stores)
+  const unsigned grid = grid_of(cdiv(n_tok, WG / 16), 8192);
+  if (dtype == LDR_BF16)
+    hipLaunchKernelGGL(k_rstd_bf16, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(x), r, n_tok, (int)d, eps);
+  else
+    hipLaunchKernelGGL(k_rstd_f32, dim3(grid), dim3(WG), 0, st, static_cast<const float*>(x), r, n_tok, (int)d, eps);
   return launched();
 }
 
@@ -1865,9 +1941,9 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
   if (dtype == LDR_BF16) {   // matrix-core scores
     const unsigned grid = (unsigned)cdiv(n_tok, WM_TT);
     const bf16_t* qbp = nq > 0 ? static_cast<const bf16_t*>(qb) : nullptr;
-    const bool rows = LDR_WM_ROWS && d % (4 * WM_KC) == 0;   // rows streamed whole when d is whole steps
+    const bool rows = d % (4 * WM_KC) == 0;   // rows streamed whole when d is whole steps
 #define LDR_WM_LAUNCH(NBV)                                                                                        \
-  hipLaunchKernelGGL((rows ? k_write_rows<NBV> : k_write_mfma<NBV>), dim3(grid), dim3(WG), 0, st,                \
+  hipLaunchKernelGGL((write_kernel<NBV>(rows)), dim3(grid), dim3(WG), 0, st,                                     \
                      static_cast<const bf16_t*>(h),                                                               \
                      static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), r_out, qbp, qb_part_stride, dots, \
                      n_tok, (int)d, (int)nq, dots_jstride, eps)

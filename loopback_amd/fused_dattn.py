@@ -52,11 +52,16 @@ MAX_SOURCES = L.MAX_SOURCES
 # plumbing
 # ---------------------------------------------------------------------------------------------------------------
 def _p(t: torch.Tensor | None):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    """A tensor's device address for a pointer argument (an int; None is NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+_raw_stream = torch._C._cuda_getCurrentRawStream   # the device's current hipStream_t, as an int
 
 
 def _stream(dev: torch.device):
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    """The current stream of `dev` (the launch stream of every entry point)."""
+    return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
 
 
 def _dtype_code(dtype: torch.dtype) -> int:
@@ -85,6 +90,13 @@ def _aligned(t: torch.Tensor) -> bool:
     return t.data_ptr() % 16 == 0
 
 
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    """t as a contiguous fp32 tensor for a kernel argument (t itself when it already is one)."""
+    if t.dtype is torch.float32 and t.is_contiguous():
+        return t.detach()
+    return t.detach().float().contiguous()
+
+
 def _inv_sqrt(d: int) -> float:
     return 1.0 / (d ** 0.5)
 
@@ -94,14 +106,19 @@ def _inv_sqrt(d: int) -> float:
 _TIMER = None
 
 
+# the entry points, bound once (name without the ldr_ prefix -> ctypes function with its signature)
+_FN = {name[4:]: getattr(_LIB, name) for name in L.SIGNATURES}
+
+
 def _run(name: str, *args) -> None:
-    fn = getattr(_LIB, "ldr_" + name)
+    fn = _FN[name]
     if _TIMER is None:
         code = fn(*args)
     else:
         with _TIMER(name):
             code = fn(*args)
-    L.check(code, name)
+    if code:
+        L.check(code, name)
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -185,9 +202,9 @@ def _forward_impl(ctx, q, base, cbar, c0, srcs):
     dev = v0.device
     dt = _dtype_code(v0.dtype)
     st = _stream(dev)
-    qc = q.detach().float().contiguous()
-    c0c = c0.detach().float().contiguous()
-    cbar_c = cbar.detach().float().contiguous()
+    qc = _f32(q)
+    c0c = _f32(c0)
+    cbar_c = _f32(cbar)
     base_c = base.detach().contiguous()
     out = torch.empty_like(base_c)
     tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
@@ -339,7 +356,7 @@ class DattnStack:
 
     Backward state: dR [n_steps, b, t, 1] (the scales' gradients, accumulated by the reads' backwards, zeroed on the
     first), WZ [pairs, b*t, 2] (per (read, source) pair and token: w = tc - cbar and dz r / sqrt(d)), and per read
-    whose backward ran, its output gradient and query (`bwd`). The updates' gradients are assembled from those by the
+    whose backward ran, its output gradient and query with their addresses (`bwd`). The updates' gradients are assembled from those by the
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
     transposed operand for its tensor-core product; the HIP write reads Q directly)."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
@@ -379,7 +396,7 @@ class DattnStack:
         self.r_done = [False] * self.n_steps      # R[s] (and the scores of update s) written by the write of s
         self.Q = self.QT = self.QB = self.DOTS = None
         if query is not None:
-            self.Q = query.detach().float().contiguous()
+            self.Q = _f32(query)
             nq = self.Q.shape[0]
             if nq > L.MAX_QUERIES or self.Q.shape[-1] != d:
                 raise RuntimeError(f"delta_attnres stacked read: query must be (<= {L.MAX_QUERIES}, {d}), "
@@ -504,9 +521,11 @@ class _RstdStk(torch.autograd.Function):
         if added is not None and (added[0].shape != x.shape or added[0].dtype != xc.dtype
                                   or not added[0].is_contiguous()):
             added = (added[0].to(xc.dtype).contiguous().view(x.shape), added[1])
-        g_ptrs = L.u64_array(stack.bwd[k][0].data_ptr() for k in reads)
-        wz_ptrs = L.u64_array(stack.WZ[_pair(k, s)].data_ptr() for k in reads)
-        q_ptrs = L.u64_array(stack.bwd[k][1].data_ptr() for k in reads)
+        bwd = stack.bwd
+        wz0, wz_row = stack.WZ.data_ptr(), stack.WZ.stride(0) * stack.WZ.element_size()
+        g_ptrs = L.u64_array([bwd[k][2] for k in reads])
+        wz_ptrs = L.u64_array([wz0 + _pair(k, s) * wz_row for k in reads])
+        q_ptrs = L.u64_array([bwd[k][3] for k in reads])
         _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc),
              _p(None if added is None else added[0]), 0.0 if added is None else float(added[1]), _p(dv),
              _p(dv_neg), stack.n_tok, stack.d, _dtype_code(xc.dtype), _stream(xc.device))
@@ -536,9 +555,9 @@ class FusedDattnReadStk(torch.autograd.Function):
             raise RuntimeError(f"delta_attnres stacked read: base must have width {d} and 16-byte aligned rows")
         dt = _dtype_code(stack.V.dtype)
         st = _stream(dev)
-        qc = q.detach().float().contiguous()
-        c0c = c0.detach().float().contiguous()
-        cbar_c = cbar.detach().float().contiguous()
+        qc = _f32(q)
+        c0c = _f32(c0)
+        cbar_c = _f32(cbar)
         if cbar_c.numel() != n_tok * n or c0c.numel() != n:
             raise RuntimeError("delta_attnres stacked read: cbar must be (b, t, n) and c0 (n,)")
         out = torch.empty_like(base)
@@ -570,7 +589,8 @@ class FusedDattnReadStk(torch.autograd.Function):
         wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
         dq, dcbar = _bwd1(vp, rp, n, g, gt, prob, dots, tc, cbar_c, c0c, drp, True, wz, n_tok, n_tok, d,
                           _dtype_code(stack.V.dtype), dev)
-        stack.bwd[step] = (g, qc)        # for the updates' gradients, formed once per update
+        # for the updates' gradients, formed once per update (the tensors, and their addresses for the kernel tables)
+        stack.bwd[step] = (g, qc, g.data_ptr(), qc.data_ptr())
         final = [i == step or (step == 1 and i == 0) for i in range(n)]   # the last read of scale i, in backward order
         grads = (None, None, dq.to(ctx.q_dtype), g, dcbar.view(*ctx.base_shape[:-1], n), None,
                  *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
@@ -616,9 +636,9 @@ class FusedCombineStk(torch.autograd.Function):
         dt = _dtype_code(stack.V.dtype)
         st = _stream(dev)
         lam = 1.0 - float(beta) if at_boundary else 1.0
-        qc = query[step - 1].detach().float().contiguous()
-        coeffs_c = coeffs.detach().float().contiguous()
-        prior_c = prior.detach().float().contiguous()
+        qc = _f32(query[step - 1])
+        coeffs_c = _f32(coeffs)
+        prior_c = _f32(prior)
         if coeffs_c.numel() != n_tok * (n - 1) or prior_c.numel() != n - 1:
             raise RuntimeError("delta_attnres fused combine: coeffs must be (b, t, n-1) and prior (n-1,)")
         out = torch.empty_like(proposal)
@@ -680,7 +700,7 @@ class FusedCombineStk(torch.autograd.Function):
                            _dtype_code(stack.V.dtype), dev, cols=n - 1, lam=ctx.lam, g_prop=g_prop, g_h0=g_h0,
                            beta=ctx.beta, part=stack.dq_parts[:, step - 1, :])
         stack.dq_rows.add(step - 1)
-        stack.bwd[step] = (g, qc)
+        stack.bwd[step] = (g, qc, g.data_ptr(), qc.data_ptr())
         final = [i == step or (step == 1 and i == 0) for i in range(n)]
         dquery = None
         if step == 1:   # read 1's backward is the pass's last: every read's partials, summed in one launch

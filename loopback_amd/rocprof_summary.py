@@ -8,7 +8,8 @@ known size). Writes the markdown tables kept with the profiles and the per-launc
         --calib-fetch prof/cf/cf_counter_collection.csv --calib-write prof/cw/cw_counter_collection.csv \\
         --config c4 --mode scores --out profiles
 
-The passes are split at the one k_split_queries launch each chain pass starts with (modes without stored scores: at
+Run it in the job that profiled (the traffic summary records the sha256 of the kernel source it finds, which bench.py
+compares with its own). The passes are split at the one k_split_queries launch each chain pass starts with (modes without stored scores: at
 the first forward kernel of the library after a backward one); the last complete pass of the trace and the last
 pass of each counter run are the ones summarized. `--stats-only NAME` summarizes the --stats
 output of any run (the LM step) into profiles/NAME.md.
@@ -139,6 +140,7 @@ def main(argv=None):
     ap.add_argument("--mode", default="scores")
     ap.add_argument("--out", default="profiles")
     ap.add_argument("--commands", default="", help="the commands that produced the inputs (quoted into the summaries)")
+    ap.add_argument("--commit", default=None, help="the commit the profiled tree was taken from (recorded as given)")
     a = ap.parse_args(argv)
     if a.stats_only:
         lines = [f"# {a.title or a.stats_only}", ""]
@@ -209,6 +211,8 @@ def main(argv=None):
     with open(os.path.join(a.out, f"traffic_chain_{tag}.txt"), "w") as f:
         json.dump({"config": a.config, "mode": a.mode,
                    "source": f"profiles/traffic_chain_{tag}.md (commands and calibration there)",
+                   # the kernel source the counters were read on (this tool runs in the same job as the profile)
+                   "source_sha256": bench.source_sha256(), "commit": a.commit,
                    "fetch_scale": fs, "write_scale": ws, "hbm_bytes_per_launch": per_launch}, f, indent=1)
         f.write("\n")
 

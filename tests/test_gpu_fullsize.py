@@ -1,5 +1,7 @@
-"""The benchmark configurations at their full size (T = 16384 tokens) on the GPU, checked through properties that
-do not need the oracle to run at that size:
+"""The benchmark configurations on the GPU. Config 1 (the reference's CPU case, 512 tokens) against the whole oracle
+chain. Configs 2-4 at their full size (T = 16384 tokens), checked through properties that do not need the oracle to
+run at that size, the stacked read both with the caller's glue as torch ops (the reference trainer's call sequence)
+and inside the kernels:
   * the read is per token, so the HIP chain over all tokens restricted to a token subset must equal the oracle chain
     (the restated reference read in bf16, on the same inputs) over that subset -- final state, dL/dh0 and every
     dL/dD_s within 1e-2 norm-relative, and no further from the fp64 oracle than the reference read is;
@@ -12,7 +14,7 @@ do not need the oracle to run at that size:
 import pytest
 import torch
 
-from gpu_helpers import DEV, err_norm
+from gpu_helpers import DEV, err_norm, err_rms
 from oracle.reference_read import run_chain as oracle_chain
 
 pytestmark = pytest.mark.gpu
@@ -30,11 +32,49 @@ def flat(x):
     return x.reshape(-1, x.shape[-1])
 
 
-@pytest.mark.parametrize("key", ["c2", "c3", "c4"])
-def test_fullsize_chain_on_token_subset(key):
+@pytest.mark.parametrize("mode,glue", [("list", "1"), ("stack", "1"), ("scores", "1"), ("stack", "0"),
+                                       ("scores", "0")])
+def test_config1_forward_matches_oracle(monkeypatch, mode, glue):
+    """BASELINE config 1, the reference's CPU case: d=768, K=2, R=4 (8 updates, 7 reads), 2 x 256 tokens, fp32,
+    forward only; updates and h0 N(0,1), queries N(0, 0.02^2), lambda = 1/4. Through every read path, every state of
+    the chain and every read's installed coefficients against the oracle chain: max-abs <= 1e-5 x RMS against the
+    exact (fp64) chain and against the fp32 chain."""
+    from loopback_amd.chain import CONFIGS, make_cell, make_inputs
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
+    cfg = CONFIGS["c1"]
+    assert (cfg.d, cfg.K, cfg.R, cfg.b, cfg.t, cfg.dtype, cfg.backward) == (768, 2, 4, 2, 256, torch.float32, False)
+    print(f"case config1 {mode} glue={glue}", flush=True)
+    h0, D, Q, G = make_inputs(cfg, "cpu")
+    cell = make_cell(cfg, Q.to(DEV))
+    states, coeffs_log = [], []
+    with torch.no_grad():
+        hd = h0.to(DEV)
+        stack = cell.new_stack(hd.shape, hd.dtype, hd.device, mode=mode)
+        h, deltas, keys, coeffs, prior = hd, [], [], None, None
+        for s in range(cfg.N):
+            l, blk = divmod(s, cfg.K)
+            x = h
+            hs = x + D[s].to(DEV)
+            deltas.append(stack.write(s, hs, x) if stack is not None else hs - x)
+            h, coeffs, prior = cell.combine(hs, hd, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
+            states.append(h.cpu())
+            coeffs_log.append(coeffs.cpu())
+    torch.cuda.synchronize()
+    for dt in (torch.float64, torch.float32):
+        cast = (lambda x: x.to(dt))
+        ref_states, ref_coeffs, _, _, _ = oracle_chain(cfg.K, cfg.R, cast(h0), [cast(x) for x in D], cast(Q),
+                                                       cast(G), beta=cfg.beta, eps=cfg.eps, grad=False)
+        e = [err_rms(a, b) for a, b in zip(states, ref_states)] + \
+            [err_rms(a, b) for a, b in zip(coeffs_log[1:], ref_coeffs[1:])]
+        assert max(e) <= 1e-5, (dt, e)
+
+
+@pytest.mark.parametrize("key,glue", [("c2", "1"), ("c2", "0"), ("c3", "1"), ("c3", "0"), ("c4", "1"), ("c4", "0")])
+def test_fullsize_chain_on_token_subset(monkeypatch, key, glue):
     from loopback_amd.chain import CONFIGS, make_inputs, run_chain
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
     cfg = CONFIGS[key]
-    print(f"case fullsize {cfg.name}", flush=True)
+    print(f"case fullsize {cfg.name} glue={glue}", flush=True)
     h0, D, Q, G = make_inputs(cfg, DEV)
     modes = ["scores", "stack"] if key == "c2" else ["scores"]
     outs = {}

@@ -188,39 +188,6 @@ def test_rstd_matches_reference_scale(shape, offset):
         assert err_max(fg.grad[offset:].view(b, t, d), xc.grad) <= tol
 
 
-def test_accumulating_list_layout_matches_plain():
-    """FusedDattnReadAcc (in-kernel accumulation, fused_dattn.py:353-376) gives the plain list layout's gradients:
-    a three-read chain over shared sources, bf16."""
-    from loopback_amd import fused_dattn as FD
-    d, b, t = 256, 1, 64
-    gen = torch.Generator().manual_seed(21)
-    vals = [torch.randn(b, t, d, generator=gen).to(torch.bfloat16) for _ in range(4)]
-    qs = torch.randn(3, d, generator=gen) * 0.5
-    results = []
-    for accumulate in (False, True):
-        vs = [v.to(DEV).requires_grad_() for v in vals]
-        acc = FD.DattnGradAccum()
-        rs = [FD.rstd(v, 1e-6) for v in vs]
-        loss = 0.0
-        cbar = torch.ones(b, t, 1, device=DEV)
-        prior = torch.ones(1, device=DEV)
-        for s in range(1, 4):
-            base = vs[s] * 0.5
-            cb = torch.cat((cbar, torch.ones(b, t, 1, device=DEV)), -1)
-            pr = torch.cat((prior, torch.ones(1, device=DEV)), -1)
-            srcs = (*vs[:s + 1], *rs[:s + 1])
-            if accumulate:
-                out, tc = FD.FusedDattnReadAcc.apply(acc, s, qs[s - 1].to(DEV), base, cb, pr, *srcs)
-            else:
-                out, tc = FD.FusedDattnRead.apply(qs[s - 1].to(DEV), base, cb, pr, *srcs)
-            loss = loss + out.float().pow(2).mean()
-            cbar, prior = tc, pr
-        loss.backward()
-        results.append([v.grad.float().cpu() for v in vs])
-    for a, b_ in zip(*results):
-        assert err_max(a, b_) <= 1e-2
-
-
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("T,d,n", [(300, 2048, 31), (77, 768, 9), (41, 64, 64), (50, 1024, 3), (33, 3072, 5)])
 @pytest.mark.parametrize("boundary", [False, True])

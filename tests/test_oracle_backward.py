@@ -1,5 +1,6 @@
 """The oracle's read and gradients against what mathematics fixes, on CPU in fp64:
-  * the key rms_no_affine == torch.nn.functional.rms_norm without a weight (library routine);
+  * the key rms_no_affine, and the scale rstd_ref times its input, == torch.nn.functional.rms_norm without a weight
+    (library routine);
   * autograd of read_core == the closed-form backward (analytic_backward, numpy, no autograd) for out, tc and the
     gradients of q, base, cbar and every source (through both its value and its RMS scale), with and without an
     upstream tc gradient;
@@ -34,6 +35,23 @@ def test_key_is_rms_norm():
     x = torch.randn(3, 7, 96, dtype=torch.float64)
     ref = torch.nn.functional.rms_norm(x, (96,), weight=None, eps=1e-6)
     assert (rms_no_affine(x, 1e-6) - ref).abs().max().item() < 1e-14
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
+def test_scale_is_rms_norm(dtype):
+    """The scale alone (the oracle's rstd_ref and the module's own, fused_dattn.py:197-199): r x is torch's rms_norm
+    of x, r being (..., 1). The module's is fp32 for every input (the reference's `delta.float()`); the oracle keeps
+    fp64 for fp64 input (its exact evaluation) and scales bf16 input in fp32, as the reference does."""
+    from loopback_amd import fused_dattn as FD
+    from oracle.reference_read import rstd_ref
+    x = (torch.randn(3, 7, 96, dtype=torch.float64) * 3.0).to(dtype)
+    for fn, wide in ((rstd_ref, dtype == torch.float64), (FD.rstd_ref, False)):
+        xf = x.double() if wide else x.float()
+        ref = torch.nn.functional.rms_norm(xf, (96,), weight=None, eps=1e-6)
+        r = fn(x, 1e-6)
+        assert r.shape == (3, 7, 1) and r.dtype == xf.dtype
+        tol = 1e-14 if wide else 2e-6
+        assert ((r * xf) - ref).abs().max().item() <= tol * ref.abs().max().item()
 
 
 @pytest.mark.parametrize("n", [1, 2, 5, 9])
