@@ -142,6 +142,23 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
                   float* dq_part, int64_t dq_part_stride, void* g_prop, void* g_h0, float beta, int64_t n_tok,
                   int64_t d, int dtype, void* stream);
 
+/* Backward pass 1 and its query gradient in one call that allocates nothing and takes no workspace: every output
+ * of ldr_read_bwd1 (same arguments) except the partials, and dq[c] = sum_tok sum_i dz_i r_i v_i[c] inv_sqrt_d
+ * (fp32, d; zeros for an empty batch) -- the bits of ldr_read_bwd1 followed by ldr_reduce_rows over its partials.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid allocation). The partials go to a device array the library holds on
+ * each GPU it runs on (LDR_B1_GRID x LDR_MAX_WIDTH fp32: 512 x 8192 x 4 B = 16 MiB with the default launch settings,
+ * kept until the process ends; its address is looked up once per device on the first call there). Calls that
+ * overlap on one GPU (on two streams, or from two threads) share that array and race: serialize them. Returns
+ * LDR_E_SHAPE for a width or batch whose partials would not fit the array (none with d <= LDR_MAX_WIDTH at the
+ * default launch settings). */
+int ldr_read_bwd1_noalloc(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const void* g, const float* gt,
+                          const float* p, const float* dots, int64_t dots_stride, const float* tc, const float* cbar,
+                          int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d,
+                          float* dcbar, int64_t dcbar_cols, const uint64_t* dr, int dr_accum, float* wz,
+                          int64_t wz_stride, float* dq, void* g_prop, void* g_h0, float beta, int64_t n_tok, int64_t d,
+                          int dtype, void* stream);
+
 /* out[c] = sum_p part[p * d + c] in a fixed order (deterministic).
  * Replaces the torch dq_part.sum(0) (fused_dattn.py:317, 785). */
 int ldr_reduce_rows(const float* part, int64_t rows, int64_t d, float* out, void* stream);

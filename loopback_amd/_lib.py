@@ -12,7 +12,7 @@ import torch  # noqa: F401  -- first: the library must bind to the HIP runtime t
 
 from . import build as _build
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 F32, BF16, F16 = 0, 1, 2   # F16: the scale entry points only
 MAX_SOURCES = 64
 MAX_WIDTH = 8192
@@ -45,6 +45,10 @@ SIGNATURES = {
     "ldr_read_bwd1": (_i32, [_u64p, _u64p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
                              _c_void_p, _i64, _c_void_p, _i64, _f32, _f32, _c_void_p, _i64, _u64p, _i32, _c_void_p,
                              _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _f32, _i64, _i64, _i32, _c_void_p]),
+    "ldr_read_bwd1_noalloc": (_i32, [_u64p, _u64p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                     _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _f32, _f32, _c_void_p, _i64, _u64p,
+                                     _i32, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _f32, _i64, _i64, _i32,
+                                     _c_void_p]),
     "ldr_reduce_rows": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
     "ldr_read_bwd2_list": (_i32, [_u64p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32,
                                   _c_void_p]),

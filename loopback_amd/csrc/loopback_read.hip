@@ -17,6 +17,7 @@
 #include <stddef.h>
 #include <math.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "loopback_read.h"
@@ -1850,12 +1851,64 @@ template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_
 
 }  // namespace
 
+// ---------------------------------------------------------------------------------------------------------------
+// the workspace of ldr_read_bwd1_noalloc: backward pass 1's query-gradient partials (one row of d fp32 per
+// workgroup) in a device array the library holds on every GPU it runs on, sized for the widest row and the most
+// workgroups pass 1 launches (512 x 8192 fp32 = 16 MiB with the default launch settings)
+// ---------------------------------------------------------------------------------------------------------------
+#define LDR_NOALLOC_PART_FLOATS ((int64_t)LDR_B1_GRID * LDR_MAX_WIDTH)
+static __device__ __align__(256) float scratch[LDR_NOALLOC_PART_FLOATS];
+
+namespace {
+
+constexpr int SCRATCH_DEVICES = 64;
+// scratch's address on each device, looked up once per device (each GPU holds its own copy of the array); a race
+// between two first calls on one device stores the same address twice
+std::atomic<float*> g_scratch[SCRATCH_DEVICES];
+
+// the address of `scratch` on the device `st` runs on (the current device for the null stream)
+int scratch_on(hipStream_t st, float** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return (int)e;
+  int dev = cur;
+  if (st) {
+    hipDevice_t sd = 0;
+    if ((e = hipStreamGetDevice(st, &sd)) != hipSuccess) return (int)e;
+    dev = (int)sd;
+  }
+  if (dev < 0 || dev >= SCRATCH_DEVICES) return LDR_E_ARG;
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+    void* a = nullptr;
+    e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess) return (int)e;
+    if (!a) return (int)hipErrorInvalidSymbol;
+    p = static_cast<float*>(a);
+    g_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return LDR_OK;
+}
+
+// a vector of fp32 zeros, by a kernel (no memset node in a captured graph)
+__global__ __launch_bounds__(WG) void k_zero(float* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x; i < n; i += (int64_t)gridDim.x * WG) p[i] = 0.f;
+}
+
+}  // namespace
+
 // ===============================================================================================================
 // C ABI
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 9; }
+int ldr_abi_version(void) { return 10; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -2112,6 +2165,33 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
                                                                   static_cast<T*>(g_h0), beta, n_tok, (int)d, tpr,
                                                                   tt)))
   return launched();
+}
+
+int ldr_read_bwd1_noalloc(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const void* g, const float* gt,
+                          const float* p, const float* dots, int64_t dots_stride, const float* tc, const float* cbar,
+                          int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d,
+                          float* dcbar, int64_t dcbar_cols, const uint64_t* dr, int dr_accum, float* wz,
+                          int64_t wz_stride, float* dq, void* g_prop, void* g_h0, float beta, int64_t n_tok, int64_t d,
+                          int dtype, void* stream) {
+  if (!dq) return LDR_E_ARG;
+  int vpt, tpr;
+  int e = row_layout(d, &vpt, &tpr, B1_MAX_VPT, LDR_B1_WAVE_ROWS, LDR_B1_VPT, true);
+  if (e) return e;
+  const int64_t parts = ldr_read_bwd1_parts(n_tok, d);
+  if (parts * d > LDR_NOALLOC_PART_FLOATS) return LDR_E_SHAPE;   // the partials would not fit the workspace
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* ws = nullptr;
+  if ((e = scratch_on(st, &ws))) return e;
+  // every argument check of ldr_read_bwd1 runs before its launch; it launches nothing for an empty batch
+  if ((e = ldr_read_bwd1(src_v, src_r, n, g, gt, p, dots, dots_stride, tc, cbar, cbar_cols, c0, c0_cols, lam,
+                         inv_sqrt_d, dcbar, dcbar_cols, dr, dr_accum, wz, wz_stride, ws, d, g_prop, g_h0, beta, n_tok,
+                         d, dtype, stream)))
+    return e;
+  if (n_tok == 0) {   // a sum over no tokens
+    hipLaunchKernelGGL(k_zero, dim3(grid_of(cdiv(d, WG), 64)), dim3(WG), 0, st, dq, d);
+    return launched();
+  }
+  return ldr_reduce_rows(ws, parts, d, dq, stream);
 }
 
 int ldr_reduce_rows(const float* part, int64_t rows, int64_t d, float* out, void* stream) {
