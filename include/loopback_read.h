@@ -67,20 +67,27 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
 int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
                  void* stream);
 
-/* The write step of update s: v_out = round(h - x); r_out[tok] = rsqrt(mean(v_out^2) + eps) of the rounded
- * update; for jj < nq: dots[jj * dots_jstride + tok] = q[jj, :] . v_out[tok, :], where q points at the first query
- * row needed and dots at that query's score slice for source s (nq = 0: no scores). bf16 updates take the scores
- * on the matrix cores from qb, the three bf16 parts of those query rows (ldr_split_queries; part p of row jj at
- * qb + p * qb_part_stride + jj * d); fp32 updates take them on the vector units from q. Replaces _write_stk_kernel
- * (fused_dattn.py:561-585, launched at 684-687; its tensor-core product is tl.dot with tf32x3, 583). */
+/* The write step of update s: v_out = round(h - x); r_out[tok] = rsqrt(mean(v_out^2) + eps) of the rounded update
+ * (summed in ldr_rstd_fwd's order, so the same bits); and the scores of the update against the read queries
+ * j_lo .. nq - 1 of the pass: dots[(j - j_lo) * dots_jstride + tok] = q[j, :] . v_out[tok, :] (dots points at query
+ * j_lo's score slice for source s; j_lo == nq: no scores). bf16 updates take the scores on the matrix cores from
+ * qb, the operand table ldr_split_queries made of the nq fp32 queries; fp32 updates take them on the vector units
+ * from q, the fp32 queries [nq, d]. Replaces _write_stk_kernel (fused_dattn.py:561-585, launched at 684-687; its
+ * tensor-core product is tl.dot with tf32x3, 583). */
 int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, const void* qb,
-                   int64_t qb_part_stride, float* dots, int64_t n_tok, int64_t d, int64_t nq, int64_t dots_jstride,
-                   float eps, int dtype, void* stream);
+                   int64_t nq, int64_t j_lo, float* dots, int64_t n_tok, int64_t d, int64_t dots_jstride, float eps,
+                   int dtype, void* stream);
 
-/* The three bf16 parts of n fp32 query values, q = hi + mid + lo (exact to ~2^-24 relative): qb[0:n] = hi,
- * qb[n:2n] = mid, qb[2n:3n] = lo. The matrix-core operand of ldr_write_dots; replaces the reference's zero-padded
- * transposed query operand QT (fused_dattn.py:657-660). */
-int ldr_split_queries(const float* q, int64_t n, void* qb, void* stream);
+/* Size of the operand table of nq fp32 queries of width d, in bf16 elements (0 for nq or d out of range). */
+int64_t ldr_query_parts_elems(int64_t nq, int64_t d);
+
+/* The matrix-core operand table of nq fp32 queries q [nq, d] (16-byte aligned, ldr_query_parts_elems(nq, d) bf16):
+ * each value split into three bf16 parts q = hi + mid + lo (exact to ~2^-24 relative), laid out in the order the
+ * write's matrix-core product loads them -- per 64-column chunk, 16-query block, part and k-group half, the 64 lanes'
+ * 16-byte operands consecutive (lane l: query 16 b + l mod 16, columns 64 c + 8 (l / 16) + 32 hf .. + 8; zeros past
+ * the last query and past d). Replaces the reference's zero-padded transposed query operand QT
+ * (fused_dattn.py:657-660). */
+int ldr_split_queries(const float* q, int64_t nq, int64_t d, void* qb, void* stream);
 
 /* Online scores: out[i * out_stride + tok] = q . v_i[tok, :] for the n sources (fp32). Together with
  * ldr_read_fwd it is the read without stored scores (replaces the score half of _dattn_fwd_stk_kernel,

@@ -12,7 +12,7 @@ import torch  # noqa: F401  -- first: the library must bind to the HIP runtime t
 
 from . import build as _build
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 F32, BF16, F16 = 0, 1, 2   # F16: the scale entry points only
 MAX_SOURCES = 64
 MAX_WIDTH = 8192
@@ -32,9 +32,10 @@ SIGNATURES = {
     "ldr_read_bwd1_parts": (_i64, [_i64, _i64]),
     "ldr_rstd_fwd": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _f32, _i32, _c_void_p]),
     "ldr_rstd_bwd": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
-    "ldr_write_dots": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
-                              _i64, _i64, _i64, _i64, _f32, _i32, _c_void_p]),
-    "ldr_split_queries": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p]),
+    "ldr_write_dots": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
+                              _c_void_p, _i64, _i64, _i64, _f32, _i32, _c_void_p]),
+    "ldr_query_parts_elems": (_i64, [_i64, _i64]),
+    "ldr_split_queries": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
     "ldr_dots_online": (_i32, [_u64p, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p]),
     "ldr_read_fwd": (_i32, [_u64p, _u64p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _f32, _c_void_p, _i64,
                             _c_void_p, _i64, _f32, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32,

@@ -53,6 +53,9 @@
 #ifndef LDR_B1_WAVE_ROWS
 #define LDR_B1_WAVE_ROWS 1   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
+#ifndef LDR_WRITE_VALU
+#define LDR_WRITE_VALU 0     // write: bf16 scores on the vector units (k_write_dots) instead of the matrix cores; a
+#endif                       // comparison build (its scale then follows the fp32 write's summation order)
 #ifndef LDR_WM_ROWS
 #define LDR_WM_ROWS 1        // write: rows streamed whole (d a multiple of 256), else in the matrix cores' layout
 #endif
@@ -97,7 +100,8 @@ constexpr int SP = MAXS + 1;            // padded LDS row of per-source scalars
 
 // The launch settings a build may change, and the ranges the kernels are written for (a value outside them would
 // overflow a tile in LDS, leave rows unwritten or loop without advancing: the build refuses it).
-static_assert(LDR_RF_UNROLL >= 1 && LDR_RF_STAGE_U >= 1, "read forward: at least one source per batch");
+static_assert(LDR_RF_UNROLL >= 1 && LDR_RF_STAGE_U >= 1 && LDR_RF_UNROLL <= 8 && LDR_RF_STAGE_U <= 8,
+              "read forward: 1..8 sources per batch");
 static_assert(LDR_RF_STAGE >= 0, "read forward: staging bytes must be >= 0");
 static_assert(LDR_RF_MAX_VPT >= 1 && LDR_RF_MAX_VPT <= 4 && LDR_AS_MAX_VPT >= 1 && LDR_AS_MAX_VPT <= 4 &&
               LDR_B1_MAX_VPT >= 1 && LDR_B1_MAX_VPT <= 4, "vectors per lane: 1..4 (the kernels' instantiations)");
@@ -578,6 +582,18 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int WM_MB = LDR_WM_MB;   // 16-token blocks per workgroup
 constexpr int WM_TT = 16 * WM_MB;   // tokens per workgroup
 static_assert(WM_MB == 1 || WM_MB == 2 || WM_MB == 4, "write: 1, 2 or 4 16-token blocks per workgroup");
+#ifndef LDR_WM_DEPTH
+#define LDR_WM_DEPTH 1        // whole-row write: 256-column steps of rows in flight
+#endif
+constexpr int WM_DEPTH = LDR_WM_DEPTH;
+#ifndef LDR_WM_QPF
+#define LDR_WM_QPF 0          // whole-row write: request the next step's query parts a step ahead
+#endif
+#ifndef LDR_WM_DBUF
+#define LDR_WM_DBUF 0         // whole-row write: two LDS tiles alternated, one barrier per step
+#endif
+constexpr bool WM_QPF = LDR_WM_QPF, WM_DBUF = LDR_WM_DBUF;
+static_assert(WM_DEPTH >= 1 && WM_DEPTH <= 3, "write: 1..3 steps of rows in flight");
 // k_write_rows maps its 4 waves x 16 rows onto the workgroup's tokens: it takes 64-token workgroups only
 constexpr bool WM_ROWS = LDR_WM_ROWS && WM_MB == 4;
 constexpr int WM_KC = 64;   // columns per chunk
@@ -586,11 +602,24 @@ constexpr int WM_HS = 32;   // column step between a lane's two k-groups
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
-template <int NB>   // NB 16-query blocks (nq <= 16 NB); NB = 0: no scores
+// The bf16 parts of the read queries in the matrix cores' operand order (written once per stack by
+// k_split_queries): for chunk c of 64 columns, 16-query block b, part p (hi, mid, lo) and k-group half hf, the 64
+// lanes' 16-byte operands are consecutive -- qt[(((c nbq + b) 3 + p) 2 + hf) 64 + l], lane l holding query
+// 16 b + l mod 16 at columns 64 c + 8 (l / 16) + 32 hf .. + 8 (zeros past the last query and past d) -- so one wave
+// load is 1 KiB of whole cache lines. A write scores the queries j_lo .. nq - 1: blocks b0 = j_lo / 16 .. nbq - 1,
+// the rows below j_lo computed and not stored.
+struct QTile {
+  const uint4* qt;
+  int nbq;    // 16-query blocks in the table
+  int b0;     // first block scored
+  int j_lo;   // first query stored (dots points at its slice)
+  int nq;     // queries in the table
+};
+
+template <int NB>   // NB 16-query blocks scored (from block qt.b0); NB = 0: no scores
 __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h, const bf16_t* __restrict__ x,
-                                                   bf16_t* __restrict__ v, float* __restrict__ r,
-                                                   const bf16_t* __restrict__ qb, int64_t qb_part_stride,
-                                                   float* __restrict__ dots, int64_t n_tok, int d, int nq,
+                                                   bf16_t* __restrict__ v, float* __restrict__ r, QTile qt,
+                                                   float* __restrict__ dots, int64_t n_tok, int d,
                                                    int64_t dots_jstride, float eps) {
   constexpr int NBA = NB > 0 ? NB : 1;   // array extents
   __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
@@ -614,10 +643,6 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
     tok_ok[mb] = tok < n_tok;
     roff[mb] = (tok_ok[mb] ? tok : n_tok - 1) * (int64_t)d;
   }
-  // this lane's query row in each block, clamped (rows past nq are computed and never stored)
-  int qrow[NBA];
-#pragma unroll
-  for (int b = 0; b < NBA; ++b) qrow[b] = min(16 * b + row, nq > 0 ? nq - 1 : 0);
   const int nchunks = (d + WM_KC - 1) / WM_KC;
   // a chunk's h and x rows: every 16-token block, the lane's two 8-column k-groups (clamped in bounds)
   auto load_hx = [&](int c, uint4 (&hr)[WM_MB][2], uint4 (&xr)[WM_MB][2]) {
@@ -650,7 +675,7 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
-          qv[p][b][hf] = *reinterpret_cast<const uint4*>(qb + p * qb_part_stride + (int64_t)qrow[b] * d + cc[hf]);
+          qv[p][b][hf] = qt.qt[((((int64_t)c * qt.nbq + qt.b0 + b) * 3 + p) * 2 + hf) * 64 + l];
 
     uint4 hc[WM_MB][2], xc[WM_MB][2];   // this chunk's rows; the next chunk's are requested now
 #pragma unroll
@@ -697,144 +722,8 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-          const uint4 qh = col_ok[hf] ? qv[p][b][hf] : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-          for (int mb = 0; mb < WM_MB; ++mb)
-            acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qh), acc[mb][b],
-                                                                 0, 0, 0);
-        }
-  }
-#pragma unroll
-  for (int mb = 0; mb < WM_MB; ++mb) {
-    ss[mb] += __shfl_xor(ss[mb], 16, 64);
-    ss[mb] += __shfl_xor(ss[mb], 32, 64);
-    if (quad == 0) s_ss[w][mb][row] = ss[mb];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) s_part[w][mb][b][l] = acc[mb][b];
-  }
-  __syncthreads();
-  if (tid < 16 * WM_MB) {
-    const int mb = tid >> 4, rr = tid & 15;
-    const float tot = ((s_ss[0][mb][rr] + s_ss[1][mb][rr]) + s_ss[2][mb][rr]) + s_ss[3][mb][rr];
-    const int64_t tok = t0 + tid;
-    if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
-  }
-  if constexpr (NB > 0) {   // the scores (NB = 0 writes none)
-    for (int e = tid; e < WM_MB * NB * 64; e += WG) {
-      const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
-      const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
-      const int jj = 16 * b + (ll & 15);
-      if (jj >= nq) continue;
-      const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
-      float* dst = dots + (int64_t)jj * dots_jstride + tok;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (tok + i < n_tok) dst[i] = sum[i];
-    }
-  }
-}
-
-// The write with rows streamed whole (d a multiple of 256): per 256-column step, wave w moves 16 rows of h and x in
-// 512-byte row segments (32 lanes per row), stores V row-major and puts it in an LDS tile; then each wave runs the
-// matrix-core product of its 64-column quarter (chunk 4 step + w, as k_write_mfma's chunks) on the tile. The chunk
-// order per wave, the operands and the order of every sum are k_write_mfma's: V, R and the scores are its bits.
-template <int NB>
-__global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h, const bf16_t* __restrict__ x,
-                                                   bf16_t* __restrict__ v, float* __restrict__ r,
-                                                   const bf16_t* __restrict__ qb, int64_t qb_part_stride,
-                                                   float* __restrict__ dots, int64_t n_tok, int d, int nq,
-                                                   int64_t dots_jstride, float eps) {
-  static_assert(WM_MB == 4, "k_write_rows: its 4 waves x 16 rows are the workgroup's 64 tokens");
-  constexpr int NBA = NB > 0 ? NB : 1;
-  constexpr int KS = 4 * WM_KC;   // columns per step
-  __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
-  __shared__ float s_ss[4][WM_MB][16];
-  __shared__ uint4 s_a[WM_TT][KS / 8 + 1];   // the step's V tile (a 16-byte pad per row)
-  const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
-  const int64_t t0 = (int64_t)blockIdx.x * WM_TT;
-  f32x4_t acc[WM_MB][NBA];
-#pragma unroll
-  for (int mb = 0; mb < WM_MB; ++mb)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float ss[WM_MB];
-#pragma unroll
-  for (int mb = 0; mb < WM_MB; ++mb) ss[mb] = 0.f;
-  int qrow[NBA];
-#pragma unroll
-  for (int b = 0; b < NBA; ++b) qrow[b] = min(16 * b + row, nq > 0 ? nq - 1 : 0);
-  // this lane's rows in the streaming layout: 16 w + 2 i + (l / 32), i < 8, vector column l % 32 of the step
-  const int lr = l & 31, lh = l >> 5;
-  int64_t rof[8];
-  bool rok[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t tok = t0 + 16 * w + 2 * i + lh;
-    rok[i] = tok < n_tok;
-    rof[i] = (rok[i] ? tok : n_tok - 1) * (int64_t)d;
-  }
-  auto load_rows = [&](int st, uint4 (&hr)[8], uint4 (&xr)[8]) {
-    const int col = st * KS + lr * 8;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      hr[i] = *reinterpret_cast<const uint4*>(h + rof[i] + col);
-      xr[i] = *reinterpret_cast<const uint4*>(x + rof[i] + col);
-    }
-  };
-  const int nsteps = d / KS;
-  uint4 hr[8], xr[8];
-  load_rows(0, hr, xr);
-  for (int st = 0; st < nsteps; ++st) {
-    const int c = 4 * st + w;   // this wave's chunk of the step
-    int cc[2];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) cc[hf] = c * WM_KC + quad * WM_QS + WM_HS * hf;
-    uint4 qv[3][NBA][2];   // the chunk's query parts (cache-resident)
-#pragma unroll
-    for (int p = 0; p < 3 * (NB > 0); ++p)
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-          qv[p][b][hf] = *reinterpret_cast<const uint4*>(qb + p * qb_part_stride + (int64_t)qrow[b] * d + cc[hf]);
-    uint4 hc[8], xc[8];   // this step's rows; the next step's are requested now
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { hc[i] = hr[i]; xc[i] = xr[i]; }
-    if (st + 1 < nsteps) load_rows(st + 1, hr, xr);   // uniform branch
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float hv[8], xv[8], vv[8];
-      IO<bf16_t>::unpack(IO<bf16_t>::Raw{hc[i]}, hv);
-      IO<bf16_t>::unpack(IO<bf16_t>::Raw{xc[i]}, xv);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) vv[k] = rok[i] ? hv[k] - xv[k] : 0.f;
-      const u32x4 u{pack2(vv[0], vv[1]), pack2(vv[2], vv[3]), pack2(vv[4], vv[5]), pack2(vv[6], vv[7])};
-      // non-temporal: the read that follows streams V[s] with its other sources
-      if (rok[i]) __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(v + rof[i] + st * KS + lr * 8));
-      s_a[16 * w + 2 * i + lh][lr] = make_uint4(u.x, u.y, u.z, u.w);
-    }
-    __syncthreads();
-    uint4 va[WM_MB][2];
-#pragma unroll
-    for (int mb = 0; mb < WM_MB; ++mb)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const uint4 u = s_a[16 * mb + row][w * (WM_KC / 8) + quad + 4 * hf];
-        va[mb][hf] = u;
-        float rv[8];
-        IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(rv[k], rv[k], ss[mb]);   // k_rstd_bf16's order
-      }
-    __syncthreads();   // the tile is read before the next step overwrites it
-#pragma unroll
-    for (int p = 0; p < 3 * (NB > 0); ++p)
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-#pragma unroll
-          for (int mb = 0; mb < WM_MB; ++mb)
+          for (int mb = 0; mb < WM_MB; ++mb)   // (columns past d: zero operands on both sides)
             acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qv[p][b][hf]),
                                                                  acc[mb][b], 0, 0, 0);
         }
@@ -858,10 +747,167 @@ __global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h,
     for (int e = tid; e < WM_MB * NB * 64; e += WG) {
       const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
       const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
-      const int jj = 16 * b + (ll & 15);
-      if (jj >= nq) continue;
+      const int jj = 16 * (qt.b0 + b) + (ll & 15);   // the query; dots points at query j_lo's slice
+      if (jj < qt.j_lo || jj >= qt.nq) continue;
       const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
-      float* dst = dots + (int64_t)jj * dots_jstride + tok;
+      float* dst = dots + (int64_t)(jj - qt.j_lo) * dots_jstride + tok;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (tok + i < n_tok) dst[i] = sum[i];
+    }
+  }
+}
+
+// The write with rows streamed whole (d a multiple of 256): per 256-column step, wave w moves 16 rows of h and x in
+// 512-byte row segments (32 lanes per row), stores V row-major and puts it in an LDS tile; then each wave runs the
+// matrix-core product of its 64-column quarter (chunk 4 step + w, as k_write_mfma's chunks) on the tile. The chunk
+// order per wave, the operands and the order of every sum are k_write_mfma's: V, R and the scores are its bits.
+template <int NB>
+__global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h, const bf16_t* __restrict__ x,
+                                                   bf16_t* __restrict__ v, float* __restrict__ r, QTile qt,
+                                                   float* __restrict__ dots, int64_t n_tok, int d,
+                                                   int64_t dots_jstride, float eps) {
+  static_assert(WM_MB == 4, "k_write_rows: its 4 waves x 16 rows are the workgroup's 64 tokens");
+  constexpr int NBA = NB > 0 ? NB : 1;
+  constexpr int KS = 4 * WM_KC;   // columns per step
+  __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
+  __shared__ float s_ss[4][WM_MB][16];
+  // the step's V tile (a 16-byte pad per row); with WM_DBUF two tiles alternate between steps, so a step needs one
+  // barrier (its tile is written, then read; the next step writes the other tile)
+  __shared__ uint4 s_a[WM_DBUF ? 2 : 1][WM_TT][KS / 8 + 1];
+  const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * WM_TT;
+  f32x4_t acc[WM_MB][NBA];
+#pragma unroll
+  for (int mb = 0; mb < WM_MB; ++mb)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[WM_MB];
+#pragma unroll
+  for (int mb = 0; mb < WM_MB; ++mb) ss[mb] = 0.f;
+  // this lane's rows in the streaming layout: 16 w + 2 i + (l / 32), i < 8, vector column l % 32 of the step
+  const int lr = l & 31, lh = l >> 5;
+  int64_t rof[8];
+  bool rok[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t tok = t0 + 16 * w + 2 * i + lh;
+    rok[i] = tok < n_tok;
+    rof[i] = (rok[i] ? tok : n_tok - 1) * (int64_t)d;
+  }
+  auto load_rows = [&](int st, uint4 (&hr)[8], uint4 (&xr)[8]) {
+    const int col = st * KS + lr * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      hr[i] = *reinterpret_cast<const uint4*>(h + rof[i] + col);
+      xr[i] = *reinterpret_cast<const uint4*>(x + rof[i] + col);
+    }
+  };
+  const int nsteps = d / KS;
+  // one 256-column step; its rows arrive in (hb, xb), which then take the rows of step st + WM_DEPTH: WM_DEPTH steps
+  // of rows are in flight while a step is worked on
+  // the query parts of this wave's chunk of step st (cache-resident)
+  auto load_q = [&](int st, uint4 (&qv)[3][NBA][2]) {
+    const int c = 4 * st + w;
+#pragma unroll
+    for (int p = 0; p < 3 * (NB > 0); ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          qv[p][b][hf] = qt.qt[((((int64_t)c * qt.nbq + qt.b0 + b) * 3 + p) * 2 + hf) * 64 + l];
+  };
+  uint4 qcur[3][NBA][2], qnext[3][NBA][2];   // WM_QPF: the next step's parts are requested a step ahead
+  if (WM_QPF && NB > 0) load_q(0, qcur);
+  auto step = [&](int st, uint4 (&hb)[8], uint4 (&xb)[8]) {
+    uint4 (&qv)[3][NBA][2] = qcur;
+    if (NB > 0) {
+      if (!WM_QPF) load_q(st, qcur);
+      else if (st + 1 < nsteps) load_q(st + 1, qnext);
+    }
+    auto& tile = s_a[WM_DBUF ? (st & 1) : 0];
+    uint4 hc[8], xc[8];   // this step's rows; the buffer now takes the rows WM_DEPTH steps ahead
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { hc[i] = hb[i]; xc[i] = xb[i]; }
+    if (st + WM_DEPTH < nsteps) load_rows(st + WM_DEPTH, hb, xb);   // uniform branch
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float hv[8], xv[8], vv[8];
+      IO<bf16_t>::unpack(IO<bf16_t>::Raw{hc[i]}, hv);
+      IO<bf16_t>::unpack(IO<bf16_t>::Raw{xc[i]}, xv);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) vv[k] = rok[i] ? hv[k] - xv[k] : 0.f;
+      const u32x4 u{pack2(vv[0], vv[1]), pack2(vv[2], vv[3]), pack2(vv[4], vv[5]), pack2(vv[6], vv[7])};
+      // non-temporal: the read that follows streams V[s] with its other sources
+      if (rok[i]) __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(v + rof[i] + st * KS + lr * 8));
+      tile[16 * w + 2 * i + lh][lr] = make_uint4(u.x, u.y, u.z, u.w);
+    }
+    __syncthreads();
+    uint4 va[WM_MB][2];
+#pragma unroll
+    for (int mb = 0; mb < WM_MB; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const uint4 u = tile[16 * mb + row][w * (WM_KC / 8) + quad + 4 * hf];
+        va[mb][hf] = u;
+        float rv[8];
+        IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(rv[k], rv[k], ss[mb]);   // k_rstd_bf16's order
+      }
+    if (!WM_DBUF) __syncthreads();   // the tile is read before the next step overwrites it
+#pragma unroll
+    for (int p = 0; p < 3 * (NB > 0); ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+          for (int mb = 0; mb < WM_MB; ++mb)
+            acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qv[p][b][hf]),
+                                                                 acc[mb][b], 0, 0, 0);
+        }
+    if (WM_QPF && NB > 0) {
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int b = 0; b < NBA; ++b)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) qcur[p][b][hf] = qnext[p][b][hf];
+    }
+  };
+  uint4 hr[WM_DEPTH][8], xr[WM_DEPTH][8];
+#pragma unroll
+  for (int k = 0; k < WM_DEPTH; ++k)
+    if (k < nsteps) load_rows(k, hr[k], xr[k]);
+  for (int st = 0; st < nsteps; st += WM_DEPTH) {
+#pragma unroll
+    for (int k = 0; k < WM_DEPTH; ++k)
+      if (st + k < nsteps) step(st + k, hr[k], xr[k]);   // uniform branch; the buffer index is static
+  }
+#pragma unroll
+  for (int mb = 0; mb < WM_MB; ++mb) {
+    ss[mb] += __shfl_xor(ss[mb], 16, 64);
+    ss[mb] += __shfl_xor(ss[mb], 32, 64);
+    if (quad == 0) s_ss[w][mb][row] = ss[mb];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) s_part[w][mb][b][l] = acc[mb][b];
+  }
+  __syncthreads();
+  if (tid < 16 * WM_MB) {
+    const int mb = tid >> 4, rr = tid & 15;
+    const float tot = ((s_ss[0][mb][rr] + s_ss[1][mb][rr]) + s_ss[2][mb][rr]) + s_ss[3][mb][rr];
+    const int64_t tok = t0 + tid;
+    if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
+  }
+  if constexpr (NB > 0) {   // the scores (NB = 0 writes none)
+    for (int e = tid; e < WM_MB * NB * 64; e += WG) {
+      const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
+      const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
+      const int jj = 16 * (qt.b0 + b) + (ll & 15);   // the query; dots points at query j_lo's slice
+      if (jj < qt.j_lo || jj >= qt.nq) continue;
+      const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
+      float* dst = dots + (int64_t)(jj - qt.j_lo) * dots_jstride + tok;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (tok + i < n_tok) dst[i] = sum[i];
@@ -879,19 +925,43 @@ auto write_kernel(bool rows) {
   return &k_write_mfma<NB>;
 }
 
-// the three bf16 parts of fp32 query rows: qb[p][j][k], p = 0 (hi), 1 (mid), 2 (lo); q = hi + mid + lo
-__global__ __launch_bounds__(WG) void k_split_queries(const float* __restrict__ q, bf16_t* __restrict__ qb, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x; i < n; i += (int64_t)gridDim.x * WG) {
-    const float a = q[i];
-    const __bf16 hi = (__bf16)a;
-    const float r1 = a - (float)hi;
-    const __bf16 mid = (__bf16)r1;
-    const __bf16 lo = (__bf16)(r1 - (float)mid);
-    qb[i] = __builtin_bit_cast(bf16_t, hi);
-    qb[n + i] = __builtin_bit_cast(bf16_t, mid);
-    qb[2 * n + i] = __builtin_bit_cast(bf16_t, lo);
+// the three bf16 parts of fp32 query values, q = hi + mid + lo, into the operand table (QTile's layout)
+__global__ __launch_bounds__(WG) void k_split_queries(const float* __restrict__ q, uint4* __restrict__ qt, int nq,
+                                                      int d, int nbq, int64_t n_vec) {
+  for (int64_t e = (int64_t)blockIdx.x * WG + threadIdx.x; e < n_vec; e += (int64_t)gridDim.x * WG) {
+    const int l = (int)(e & 63);
+    int64_t rest = e >> 6;
+    const int hf = (int)(rest & 1);
+    rest >>= 1;
+    const int p = (int)(rest % 3);
+    rest /= 3;
+    const int b = (int)(rest % nbq);
+    const int64_t c = rest / nbq;
+    const int j = 16 * b + (l & 15);
+    const int64_t col0 = c * 64 + 8 * (l >> 4) + 32 * hf;
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+      uint32_t two = 0;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int64_t col = col0 + k + kk;
+        const float a = (j < nq && col < d) ? q[(int64_t)j * d + col] : 0.f;
+        const __bf16 hi = (__bf16)a;
+        const float r1 = a - (float)hi;
+        const __bf16 mid = (__bf16)r1;
+        const __bf16 lo = (__bf16)(r1 - (float)mid);
+        const __bf16 part = p == 0 ? hi : (p == 1 ? mid : lo);
+        two |= (uint32_t)__builtin_bit_cast(bf16_t, part) << (16 * kk);
+      }
+      w[k / 2] = two;
+    }
+    qt[e] = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
+
+inline int64_t query_blocks(int64_t nq) { return (nq + 15) / 16; }
+inline int64_t query_chunks(int64_t d) { return (d + 63) / 64; }
 
 // ---------------------------------------------------------------------------------------------------------------
 // online scores: out[i][tok] = q . v_i[tok]  (the read without a stored score table)
@@ -1043,6 +1113,8 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
       if (tok >= n_tok) break;
       const float* wrow = &s_w[rr * SP];
       const int64_t roff = tok * (int64_t)d;
+      constexpr int U = STAGE ? LDR_RF_STAGE_U : LDR_RF_UNROLL;
+      using Raw = typename IO<T>::Raw;
       float acc[VPT][8];
 #pragma unroll
       for (int v = 0; v < VPT; ++v) IO<T>::load(base + roff + R.off(v), acc[v]);
@@ -1058,9 +1130,8 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
         }
       }
       int i = 0;
-      constexpr int U = STAGE ? LDR_RF_STAGE_U : LDR_RF_UNROLL;
       for (; i + U <= n; i += U) {
-        typename IO<T>::Raw raw[U][VPT];
+        Raw raw[U][VPT];
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -1078,7 +1149,7 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
         }
       }
       if (U > 4 && i + 4 <= n) {
-        typename IO<T>::Raw raw[4][VPT];
+        Raw raw[4][VPT];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -1908,7 +1979,7 @@ __global__ __launch_bounds__(WG) void k_zero(float* __restrict__ p, int64_t n) {
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 10; }
+int ldr_abi_version(void) { return 11; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -1975,51 +2046,65 @@ int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64
 }
 
 int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, const void* qb,
-                   int64_t qb_part_stride, float* dots, int64_t n_tok, int64_t d, int64_t nq, int64_t dots_jstride,
-                   float eps, int dtype, void* stream) {
+                   int64_t nq, int64_t j_lo, float* dots, int64_t n_tok, int64_t d, int64_t dots_jstride, float eps,
+                   int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (n_tok < 0 || !tok_ptr(h, n_tok) || !tok_ptr(x, n_tok) || !tok_ptr(v_out, n_tok) || !tok_ptr(r_out, n_tok) ||
-      nq < 0)
+      nq < 0 || j_lo < 0 || j_lo > nq)
     return LDR_E_ARG;
   if (nq > LDR_MAX_QUERIES) return LDR_E_SHAPE;
-  if (nq > 0 && (!tok_ptr(dots, n_tok) || dots_jstride < n_tok)) return LDR_E_ARG;
-  if (nq > 0 && dtype == LDR_BF16 && (!qb || qb_part_stride < nq * d)) return LDR_E_ARG;
-  if (nq > 0 && dtype == LDR_F32 && !q) return LDR_E_ARG;
-  if (!al16(h) || !al16(x) || !al16(v_out) || (nq > 0 && q && !al16(q)) ||
-      (nq > 0 && dtype == LDR_BF16 && (!al16(qb) || (qb_part_stride & 7))))
+  const bool scores = j_lo < nq;
+  const bool valu = dtype == LDR_F32 || LDR_WRITE_VALU;   // scores on the vector units, from the fp32 queries
+  if (scores && (!tok_ptr(dots, n_tok) || dots_jstride < n_tok)) return LDR_E_ARG;
+  if (scores && ((valu && !q) || (!valu && !qb))) return LDR_E_ARG;
+  if (!al16(h) || !al16(x) || !al16(v_out) || (scores && valu && !al16(q)) || (scores && !valu && !al16(qb)))
     return LDR_E_ALIGN;
   if (d <= 0 || (d & 7) || d > LDR_MAX_WIDTH) return LDR_E_SHAPE;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == LDR_BF16) {   // matrix-core scores
+  if (!valu) {   // matrix-core scores from the operand table of the nq queries
     const unsigned grid = (unsigned)cdiv(n_tok, WM_TT);
-    const bf16_t* qbp = nq > 0 ? static_cast<const bf16_t*>(qb) : nullptr;
+    const int nbq = (int)query_blocks(nq), b0 = (int)(j_lo / 16);
+    const QTile qtl{static_cast<const uint4*>(qb), nbq, b0, (int)j_lo, (int)nq};
+    const int nb = scores ? nbq - b0 : 0;
     const bool rows = d % (4 * WM_KC) == 0;   // rows streamed whole when d is whole steps
 #define LDR_WM_LAUNCH(NBV)                                                                                        \
-  hipLaunchKernelGGL((write_kernel<NBV>(rows)), dim3(grid), dim3(WG), 0, st,                                     \
-                     static_cast<const bf16_t*>(h),                                                               \
-                     static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), r_out, qbp, qb_part_stride, dots, \
-                     n_tok, (int)d, (int)nq, dots_jstride, eps)
-    if (nq == 0) LDR_WM_LAUNCH(0);
-    else if (nq <= 16) LDR_WM_LAUNCH(1);
-    else if (nq <= 32) LDR_WM_LAUNCH(2);
-    else LDR_WM_LAUNCH(4);
+  hipLaunchKernelGGL((write_kernel<NBV>(rows)), dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(h),      \
+                     static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), r_out, qtl, dots, n_tok, (int)d, \
+                     dots_jstride, eps)
+    switch (nb) {
+      case 0: LDR_WM_LAUNCH(0); break;
+      case 1: LDR_WM_LAUNCH(1); break;
+      case 2: LDR_WM_LAUNCH(2); break;
+      case 3: LDR_WM_LAUNCH(3); break;
+      default: LDR_WM_LAUNCH(4); break;
+    }
 #undef LDR_WM_LAUNCH
-  } else {
+  } else {   // vector-unit scores from the fp32 queries (fp32 updates; bf16 too in a build with LDR_WRITE_VALU)
     const unsigned grid = (unsigned)cdiv(n_tok, WR_TT);
-    hipLaunchKernelGGL((k_write_dots<float>), dim3(grid), dim3(WG), 0, st, static_cast<const float*>(h),
-                       static_cast<const float*>(x), static_cast<float*>(v_out), r_out, q, dots, n_tok, (int)d, (int)nq,
-                       dots_jstride, eps);
+    const float* qj = scores ? q + j_lo * d : nullptr;
+    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_write_dots<T>), dim3(grid), dim3(WG), 0, st,
+                                               static_cast<const T*>(h), static_cast<const T*>(x),
+                                               static_cast<T*>(v_out), r_out, qj, dots, n_tok, (int)d,
+                                               (int)(nq - j_lo), dots_jstride, eps))
   }
   return launched();
 }
 
-int ldr_split_queries(const float* q, int64_t n, void* qb, void* stream) {
-  if (!q || !qb || n < 0) return LDR_E_ARG;
-  if (n == 0) return LDR_OK;
-  const unsigned grid = grid_of(cdiv(n, WG), 1024);
+int64_t ldr_query_parts_elems(int64_t nq, int64_t d) {
+  if (nq < 0 || nq > LDR_MAX_QUERIES || d <= 0 || d > LDR_MAX_WIDTH) return 0;
+  return query_chunks(d) * query_blocks(nq) * 3 * 2 * 64 * 8;
+}
+
+int ldr_split_queries(const float* q, int64_t nq, int64_t d, void* qb, void* stream) {
+  if (nq < 0 || d <= 0 || (nq > 0 && (!q || !qb))) return LDR_E_ARG;
+  if (nq > LDR_MAX_QUERIES || d > LDR_MAX_WIDTH) return LDR_E_SHAPE;
+  if (!al16(qb)) return LDR_E_ALIGN;
+  if (nq == 0) return LDR_OK;
+  const int64_t n_vec = ldr_query_parts_elems(nq, d) / 8;
+  const unsigned grid = grid_of(cdiv(n_vec, WG), 1024);
   hipLaunchKernelGGL(k_split_queries, dim3(grid), dim3(WG), 0, static_cast<hipStream_t>(stream), q,
-                     static_cast<bf16_t*>(qb), n);
+                     static_cast<uint4*>(qb), (int)nq, (int)d, (int)query_blocks(nq), n_vec);
   return launched();
 }
 

@@ -358,7 +358,8 @@ class DattnStack:
     first), WZ [pairs, b*t, 2] (per (read, source) pair and token: w = tc - cbar and dz r / sqrt(d)), and per read
     whose backward ran, its output gradient and query with their addresses (`bwd`). The updates' gradients are assembled from those by the
     scales' backwards; dV stays None (no gradient stack is read-modified-written). QT is None (the reference's
-    transposed operand for its tensor-core product; the HIP write reads Q directly)."""
+    transposed operand for its tensor-core product); QB holds the queries' bf16 parts in the order the write's
+    matrix-core product loads them."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
                  "assembled", "neg", "dq_parts", "dq_rows", "wh", "gadd", "h0_ref", "h0_steps", "h0_g", "vptr",
                  "rptr", "drptr")
@@ -402,9 +403,9 @@ class DattnStack:
                 raise RuntimeError(f"delta_attnres stacked read: query must be (<= {L.MAX_QUERIES}, {d}), "
                                    f"got {tuple(self.Q.shape)}")
             self.DOTS = torch.empty((max(1, nq), n_steps, b * t), dtype=torch.float32, device=device)
-            if dtype == torch.bfloat16 and nq > 0:   # the queries' bf16 parts: the write's matrix-core operand
-                self.QB = torch.empty((3, nq, d), dtype=torch.bfloat16, device=device)
-                _run("split_queries", _p(self.Q), self.Q.numel(), _p(self.QB), _stream(self.Q.device))
+            if dtype == torch.bfloat16 and nq > 0:   # the queries' bf16 parts: the write's matrix-core operand table
+                self.QB = torch.empty(int(L.LIB.ldr_query_parts_elems(nq, d)), dtype=torch.bfloat16, device=device)
+                _run("split_queries", _p(self.Q), nq, d, _p(self.QB), _stream(self.Q.device))
 
     def write(self, s: int, h: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
         """V[s] = h - x, returned as the update tensor (an alias of the stack's slice, with the autograd edge to
@@ -454,16 +455,14 @@ class _WriteDelta(torch.autograd.Function):
         if (h.is_cuda and h.is_contiguous() and x.is_contiguous() and h.dtype == V.dtype == x.dtype
                 and h.numel() == x.numel() == stack.n_tok * stack.d and h.shape[-1] == stack.d
                 and _aligned(h) and _aligned(x)):
-            nq, qptr, qbptr, qb_stride, dptr, jstride = 0, None, None, 0, None, stack.n_steps * stack.n_tok
+            nq, j_lo, dptr, jstride = 0, 0, None, stack.n_steps * stack.n_tok
             if stack.Q is not None:
-                j_lo = max(0, s - 1)                  # read s' >= s uses query s' - 1
-                nq = max(0, stack.Q.shape[0] - j_lo)
-                if nq > 0:
-                    qptr, dptr = stack.Q[j_lo], stack.DOTS[j_lo, s]
-                    if stack.QB is not None:
-                        qbptr, qb_stride = stack.QB[0, j_lo], stack.QB[0].numel()
-            _run("write_dots", _p(h), _p(x), _p(out), _p(stack.R[s]), _p(qptr), _p(qbptr), qb_stride, _p(dptr),
-                 stack.n_tok, stack.d, nq, jstride, stack.eps, _dtype_code(V.dtype), _stream(V.device))
+                nq = stack.Q.shape[0]
+                j_lo = min(max(0, s - 1), nq)         # read s' >= s uses query s' - 1: queries j_lo .. nq - 1
+                if j_lo < nq:
+                    dptr = stack.DOTS[j_lo, s]
+            _run("write_dots", _p(h), _p(x), _p(out), _p(stack.R[s]), _p(stack.Q), _p(stack.QB), nq, j_lo, _p(dptr),
+                 stack.n_tok, stack.d, jstride, stack.eps, _dtype_code(V.dtype), _stream(V.device))
             stack.r_done[s] = True
         else:
             torch.sub(h, x, out=out)

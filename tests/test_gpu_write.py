@@ -63,12 +63,14 @@ def test_blend_sum_bitwise(dtype, m, T, d):
 
 
 @pytest.mark.parametrize("d", [256, 2048, 8192])
-@pytest.mark.parametrize("nq", [0, 16, 32, 63])
+@pytest.mark.parametrize("nq", [0, 1, 16, 17, 32, 40, 63])
 @pytest.mark.parametrize("T", [1, 77, 333])
 def test_whole_row_write_is_the_matrix_core_write_bitwise(d, nq, T):
     """k_write_rows (rows streamed whole, the write for widths that are multiples of 256) against k_write_mfma (the
-    matrix cores' layout) on the same inputs through the C ABI: V, R and the scores bitwise equal (the same chunks
-    per wave, operands and order of every sum). k_write_mfma comes from the test fixture library built with
+    matrix cores' layout) on the same inputs through the C ABI, scoring the last nq of 64 queries (so the first
+    16-query block scored starts inside the table at every nq not a multiple of 16): V, R and the scores bitwise
+    equal (the same chunks per wave, operands and order of every sum), the scores within 1e-5 x RMS of an fp64
+    product. k_write_mfma comes from the test fixture library built with
     LDR_WM_ROWS=0 (loopback_amd.build builds it beside the product library)."""
     import ctypes
     from loopback_amd import _lib as L
@@ -80,18 +82,19 @@ def test_whole_row_write_is_the_matrix_core_write_bitwise(d, nq, T):
     gen = torch.Generator().manual_seed(d + 7 * nq + T)
     h = torch.randn(T, d, generator=gen).to(torch.bfloat16).to(DEV)
     x = torch.randn(T, d, generator=gen).to(torch.bfloat16).to(DEV)
-    q = (torch.randn(max(nq, 1), d, generator=gen) * 0.3).to(DEV)
-    qb = torch.empty(3, max(nq, 1), d, dtype=torch.bfloat16, device=DEV)
+    NQ = 64                                       # the pass's queries; this write scores the last nq of them
+    q = (torch.randn(NQ, d, generator=gen) * 0.3).to(DEV)
+    qb = torch.empty(int(L.LIB.ldr_query_parts_elems(NQ, d)), dtype=torch.bfloat16, device=DEV)
     st = torch.cuda.current_stream().cuda_stream
-    L.check(L.LIB.ldr_split_queries(q.data_ptr(), q.numel(), qb.data_ptr(), st), "split_queries")
+    L.check(L.LIB.ldr_split_queries(q.data_ptr(), NQ, d, qb.data_ptr(), st), "split_queries")
     outs = []
     print(f"case write layouts d{d} nq{nq} T{T}", flush=True)
     for fn in fns:
         v = torch.empty(T, d, dtype=torch.bfloat16, device=DEV)
         r = torch.empty(T, device=DEV)
         dots = torch.full((max(nq, 1), T), float("nan"), device=DEV)
-        L.check(fn(h.data_ptr(), x.data_ptr(), v.data_ptr(), r.data_ptr(), q.data_ptr(), qb.data_ptr(),
-                   qb[0].numel(), dots.data_ptr(), T, d, nq, T, 1e-6, L.BF16, st), "write_dots")
+        L.check(fn(h.data_ptr(), x.data_ptr(), v.data_ptr(), r.data_ptr(), q.data_ptr(), qb.data_ptr(), NQ,
+                   NQ - nq, dots.data_ptr(), T, d, T, 1e-6, L.BF16, st), "write_dots")
         torch.cuda.synchronize()
         outs.append((v.cpu(), r.cpu(), dots.cpu()))
     (v1, r1, s1), (v2, r2, s2) = outs
@@ -99,3 +102,5 @@ def test_whole_row_write_is_the_matrix_core_write_bitwise(d, nq, T):
     assert torch.equal(v1, h.cpu() - x.cpu())
     if nq > 0:
         assert torch.equal(s1[:nq], s2[:nq])
+        ref = q[NQ - nq:].double().cpu() @ v1.double().T              # the scores against an fp64 product
+        assert ((s1[:nq].double() - ref).abs().max() / ref.pow(2).mean().sqrt()).item() <= 1e-5

@@ -84,14 +84,21 @@ def test_argument_checks_before_launch(lib):
     assert L.ldr_dots_online(one_v, 1, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, lib.F16, null) == -4
     too_many = lib.u64_array([4096] * 65)
     assert L.ldr_dots_online(too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, 1, null) == -1
-    assert L.ldr_write_dots(ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096),
-                            ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096), 65 * 64,
-                            ctypes.c_void_p(4096), 16, 64, 65, 16, 1e-6, 1, null) == -2
-    # bf16 scores need the split query parts
-    assert L.ldr_write_dots(ctypes.c_void_p(4096), ctypes.c_void_p(4096), ctypes.c_void_p(4096),
-                            ctypes.c_void_p(4096), ctypes.c_void_p(4096), null, 0, ctypes.c_void_p(4096), 16, 64, 4,
-                            16, 1e-6, 1, null) == -1
-    assert L.ldr_split_queries(null, 8, ctypes.c_void_p(4096), null) == -1
+    p4 = ctypes.c_void_p(4096)
+    # more queries than a stack holds; a first scored query past the last
+    assert L.ldr_write_dots(p4, p4, p4, p4, p4, p4, 65, 0, p4, 16, 64, 16, 1e-6, 1, null) == -2
+    assert L.ldr_write_dots(p4, p4, p4, p4, p4, p4, 4, 5, p4, 16, 64, 16, 1e-6, 1, null) == -1
+    # bf16 scores need the queries' operand table, fp32 scores the fp32 queries
+    assert L.ldr_write_dots(p4, p4, p4, p4, p4, null, 4, 0, p4, 16, 64, 16, 1e-6, 1, null) == -1
+    assert L.ldr_write_dots(p4, p4, p4, p4, null, p4, 4, 0, p4, 16, 64, 16, 1e-6, 0, null) == -1
+    # no scores (j_lo == nq): neither is needed
+    assert L.ldr_write_dots(null, null, null, null, null, null, 4, 4, null, 0, 64, 0, 1e-6, 1, null) == 0
+    assert L.ldr_split_queries(null, 8, 64, p4, null) == -1
+    assert L.ldr_split_queries(p4, 65, 64, p4, null) == -2
+    assert L.ldr_split_queries(p4, 8, 64, ctypes.c_void_p(4100), null) == -3
+    # the operand table's size: 64-column chunks x 16-query blocks x 3 parts x 2 halves x 64 lanes x 8 values
+    assert L.ldr_query_parts_elems(31, 2048) == 32 * 2 * 3 * 2 * 64 * 8
+    assert L.ldr_query_parts_elems(1, 8) == 3 * 2 * 64 * 8 and L.ldr_query_parts_elems(65, 64) == 0
     assert L.ldr_dv_assemble(too_many, too_many, too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), null,
                              null, 0.0, ctypes.c_void_p(4096), null, 16, 64, 1, null) == -2
     # a misaligned added gradient
