@@ -17,7 +17,8 @@ Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / 
   chain         every library kernel of the pass: this build's compulsory bytes / summed kernel time, and the
                 reference dataflow's bytes (its backward read-modify-writes a gradient stack) over the same time and
                 over the wall time;
-  configs       configs 2 and 3 timed the same way (wall time per pass; --no-extra-configs skips them);
+  configs       configs 2 and 3 timed the same way (wall time per pass), eager and replayed from HIP graphs
+                (--no-extra-configs skips them);
   cpu_baseline  the CPU oracle (the restated reference read, torch on the host cores) on a bounded sample of the
                 same chain (T reduced), fwd+bwd, read-tokens/s and effective GB/s; beside it config 1 (the
                 reference's CPU case: d=768, N=8, 512 tokens, fp32, forward) as the survey plans it.
@@ -47,7 +48,8 @@ def parse():
     ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4"])
     ap.add_argument("--mode", default="scores", choices=["scores", "stack", "list"])
     ap.add_argument("--graph", action="store_true",
-                    help="forward-only configs: time replays of the pass captured in a HIP graph (no host work)")
+                    help="time replays of the pass captured in HIP graphs (no host work per kernel): the forward "
+                         "as one graph, a training pass as a forward and a backward graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra-configs", action="store_true", help="skip the c2 / c3 timings of the default run")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the CPU baseline sample")
@@ -208,6 +210,33 @@ def time_chain(cfg, mode, steps, warmup, timer=None):
     return elapsed, resident, peak
 
 
+def time_graphed(cfg, mode, steps, warmup):
+    """The pass replayed from HIP graphs (forward-only configs: chain.capture_forward; with a backward:
+    chain.capture_training, the loss and its backward eager around the graphs), `steps` passes timed after
+    `warmup`; returns elapsed s."""
+    import torch
+    from loopback_amd.chain import capture_forward, capture_training, make_inputs
+    dev = torch.device("cuda", 0)
+    h0, D, Q, G = make_inputs(cfg, dev)
+    if cfg.backward:
+        step = capture_training(cfg, h0, D, Q, mode)
+        run = lambda: step(G)
+    else:
+        graph, _ = capture_forward(cfg, h0, D, Q, mode)
+        run = graph.replay
+    for _ in range(max(1, warmup)):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    del run, h0, D, Q, G
+    torch.cuda.empty_cache()
+    return elapsed
+
+
 def cpu_model() -> str | None:
     """The host CPU's model name, as lscpu reports it (else /proc/cpuinfo), with its family / model / stepping."""
     name = None
@@ -289,26 +318,15 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
-    from loopback_amd.chain import CONFIGS, capture_forward, make_inputs
+    from loopback_amd.chain import CONFIGS
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
-    if args.graph:   # the forward pass as one HIP graph: no Python or launch work per pass
-        if cfg.backward:
-            print("bench.py: --graph times forward-only configurations (c2)", file=sys.stderr)
-            sys.exit(2)
-        h0, D, Q, G = make_inputs(cfg, dev)
-        graph, _ = capture_forward(cfg, h0, D, Q, args.mode)
-        for _ in range(max(1, args.warmup)):
-            graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            graph.replay()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+    if args.graph:   # the pass replayed from HIP graphs: no Python or launch work per kernel
+        elapsed = time_graphed(cfg, args.mode, args.steps, args.warmup)
         _, ref_bytes = family_bytes(cfg, args.mode)
-        print(json.dumps({"metric": f"depth-read tokens/sec (fwd), {cfg.name}, HIP graph replay",
+        print(json.dumps({"metric": f"depth-read tokens/sec ({'fwd+bwd' if cfg.backward else 'fwd'}), {cfg.name}, "
+                                    "HIP graph replay",
                           "value": cfg.n_tok * args.steps / elapsed, "unit": "read-tokens/s", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "ms_per_step": 1e3 * elapsed / args.steps,
                           "higher_is_better": True, "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
@@ -372,13 +390,14 @@ def main():
         extra = {}
         for key in ("c2", "c3"):
             c = CONFIGS[key]
-            el, _, _ = time_chain(c, args.mode, 20, 5)
             _, rb = family_bytes(c, args.mode)
-            ms = 1e3 * el / 20
-            extra[key] = {"workload": c.name, "ms_per_step": ms, "value": c.n_tok * 20 / el,
-                          "unit": "read-tokens/s", "backward": c.backward,
-                          "formula_wall_gbs": rb / (ms * 1e-3) / 1e9,
-                          "formula_wall_frac": rb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+            for how in ("eager", "graph"):
+                el = time_chain(c, args.mode, 20, 5)[0] if how == "eager" else time_graphed(c, args.mode, 20, 5)
+                ms = 1e3 * el / 20
+                extra[f"{key}_{how}"] = {"workload": c.name, "ms_per_step": ms, "value": c.n_tok * 20 / el,
+                                         "unit": "read-tokens/s", "backward": c.backward,
+                                         "formula_wall_gbs": rb / (ms * 1e-3) / 1e9,
+                                         "formula_wall_frac": rb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         line["configs"] = extra
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)

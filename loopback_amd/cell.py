@@ -85,7 +85,7 @@ class LoopDeltaAttnRes(nn.Module):
                 keys.append(stack.rstd(step, deltas[-1], self.eps))
             R_list = keys if keys is not None else [FD._alias(stack.R, i) for i in range(len(deltas))]
             return FD.FusedCombineStk.apply(stack, step, self.query, proposal, h0 if at_boundary else None,
-                                            coeffs, prior_coeffs, self.beta, at_boundary, *deltas, *R_list)
+                                            coeffs, prior_coeffs, self.beta, at_boundary, *R_list)
         base = proposal + self.beta * (h0 - proposal) if at_boundary else proposal
 
         b, t, _ = proposal.shape

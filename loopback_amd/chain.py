@@ -118,6 +118,42 @@ def capture_forward(cfg: ChainConfig, h0, D, Q, mode: str):
     return graph, out
 
 
+class ChainModule(torch.nn.Module):
+    """The chain's layer loop as a module of its read cell: forward(h0, *D) -> the final state."""
+
+    def __init__(self, cell: LoopDeltaAttnRes, K: int, mode: str):
+        super().__init__()
+        self.cell, self.K, self.mode = cell, int(K), mode
+
+    def forward(self, h0, *D):
+        return chain_forward(self.cell, h0, list(D), self.K, self.mode)
+
+
+def capture_training(cfg: ChainConfig, h0, D, Q, mode: str):
+    """The chain's forward and backward captured as two HIP graphs (torch.cuda.make_graphed_callables): every
+    library launch takes its addresses and sizes by value and allocates nothing, torch's allocations come from the
+    graphs' pool, so a training pass replays with no host work per kernel. Returns step(G) -> (h, loss, grads): one
+    pass on the static inputs h0, D (their contents may change between passes, not their storage) with the loss
+    sum(h.float() * G) and its backward (eager, outside the graphs); grads = {'h0', 'D', 'query'} alias the graphs'
+    output buffers until the next step (clone them to keep them)."""
+    cell = make_cell(cfg, Q)
+    mod = ChainModule(cell, cfg.K, mode)
+    h0s = h0.detach().requires_grad_()
+    Ds = [x.detach().requires_grad_() for x in D]
+    graphed = torch.cuda.make_graphed_callables(mod, (h0s, *Ds))
+
+    def step(G):
+        for t in (h0s, *Ds, cell.query):
+            t.grad = None
+        h = graphed(h0s, *Ds)
+        loss = (h.float() * G).sum()
+        loss.backward()
+        return h.detach(), loss.detach(), {"h0": h0s.grad, "D": [x.grad for x in Ds], "query": cell.query.grad}
+
+    step.cell = cell
+    return step
+
+
 def make_cell(cfg: ChainConfig, Q) -> LoopDeltaAttnRes:
     """The chain's read cell with its query set to Q (on Q's device)."""
     cell = LoopDeltaAttnRes(cfg.d, cfg.R, cfg.K, beta=cfg.beta, eps=cfg.eps).to(Q.device)

@@ -362,7 +362,7 @@ class DattnStack:
     matrix-core product loads them."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
                  "assembled", "neg", "dq_parts", "dq_rows", "wh", "gadd", "h0_ref", "h0_steps", "h0_g", "vptr",
-                 "rptr", "drptr")
+                 "rptr", "drptr", "wout")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
@@ -385,7 +385,8 @@ class DattnStack:
         self.bwd = {}
         self.assembled = set()
         self.neg = {}         # s -> (gradient of the write's h, of its x, the added proposal gradient or None),
-                              # handed from _RstdStk to _WriteDelta
+                              # handed from a separate scale node (_RstdStk) to _WriteDelta
+        self.wout = {}        # s -> (weak reference to the write's update, its scale output), until rstd(s) takes it
         self.dq_parts = None  # the fused combines' query-gradient partials, [part][read][d] fp32, and the reads
         self.dq_rows = set()  # whose backward wrote theirs; summed once, by read 1's backward (the pass's last)
         self.wh = {}          # s -> weak reference to the write's h (a fused combine that takes it as its proposal
@@ -409,11 +410,17 @@ class DattnStack:
 
     def write(self, s: int, h: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
         """V[s] = h - x, returned as the update tensor (an alias of the stack's slice, with the autograd edge to
-        h and x)."""
-        return _WriteDelta.apply(self, s, h, x)
+        h and x). The write also stores the update's scale R[s], which rstd(s, ...) then returns."""
+        v, r = _WriteDelta.apply(self, s, h, x)
+        self.wout[s] = (weakref.ref(v), r)
+        return v
 
     def rstd(self, s: int, delta: torch.Tensor, eps: float) -> torch.Tensor:
-        """R[s] = the RMS scale of V[s], returned as an alias of the stack (differentiable through `delta`)."""
+        """R[s] = the RMS scale of V[s], returned as an alias of the stack (differentiable through `delta`): the
+        scale the write of `delta` stored with it, or computed here for another update or eps."""
+        w = self.wout.pop(s, None)
+        if w is not None and w[0]() is delta and float(eps) == self.eps:
+            return w[1]
         return _RstdStk.apply(self, s, delta, float(eps))
 
     def grads(self):
@@ -441,16 +448,57 @@ def _proposal_grad(added):
     return g - (g * beta).to(g.dtype) if beta else g
 
 
+def _assemble(stack: DattnStack, s: int, gr):
+    """The finished gradient of update s -- every read of it has run its backward -- formed by one kernel from the
+    reads' output gradients and (w, dz r / sqrt(d)) pairs, the scale's gradient gr (dR[s], or None) and, when a read
+    took the write's h as its proposal, that read's proposal gradient (added as autograd would add it). Returns
+    (dv for the write's h, -dv without the proposal's share for its x, the added (g, beta) or None)."""
+    reads = sorted(k for k in stack.bwd if k >= max(s, 1))     # the reads of update s whose backward ran
+    if s in reads:   # read s last: when its output gradient is also the added one, the kernel loads it once
+        reads.remove(s)
+        reads.append(s)
+    v = stack.V[s]
+    dv = torch.empty_like(v)
+    dv_neg = torch.empty_like(v)
+    grc = None if gr is None else gr.float().contiguous()
+    added = stack.gadd.pop(s, None)       # (g, beta): the combine that took the write's h as its proposal
+    if added is not None and (added[0].shape != v.shape or added[0].dtype != v.dtype
+                              or not added[0].is_contiguous()):
+        added = (added[0].to(v.dtype).contiguous().view(v.shape), added[1])
+    bwd = stack.bwd
+    if reads:
+        wz0, wz_row = stack.WZ.data_ptr(), stack.WZ.stride(0) * stack.WZ.element_size()
+        g_ptrs = L.u64_array([bwd[k][2] for k in reads])
+        wz_ptrs = L.u64_array([wz0 + _pair(k, s) * wz_row for k in reads])
+        q_ptrs = L.u64_array([bwd[k][3] for k in reads])
+    else:
+        g_ptrs = wz_ptrs = q_ptrs = None
+    _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(v), _p(stack.R[s]), _p(grc),
+         _p(None if added is None else added[0]), 0.0 if added is None else float(added[1]), _p(dv),
+         _p(dv_neg), stack.n_tok, stack.d, _dtype_code(v.dtype), _stream(v.device))
+    stack.assembled.add(s)
+    for k in [k for k in bwd if all(j in stack.assembled for j in range(k + 1))]:
+        del bwd[k]                        # every update read by read k has its gradient: drop g_k
+    return dv, dv_neg, added
+
+
 class _WriteDelta(torch.autograd.Function):
     """V[s] = round(h - x), R[s] from the rounded update and the scores against the later read queries, in one pass
-    (fused_dattn.py:679-695); a plain subtraction into the slice for layouts the kernel does not take. Backward
-    (g, -g): -g comes ready from the kernel that formed g when it is that kernel's output."""
+    (fused_dattn.py:679-695); a plain subtraction into the slice (and the scale kernel) for layouts the kernel does
+    not take. Outputs the update and its scale as aliases of the stack: the scale is what DattnStack.rstd hands the
+    reads (the reference's separate _RstdStk node, one autograd node fewer per step).
+
+    Backward: every read of update s takes its scale, so this runs after all of them; the update's gradient is
+    assembled here once (_assemble) and returned as (dv, -dv) to (h, x), with any gradient other consumers of the
+    update gave it added. When the update's gradient was already assembled by a separate scale node (_RstdStk, for
+    a scale of another eps), its (dv, -dv) pair comes from there."""
 
     @staticmethod
     def forward(ctx, stack: DattnStack, s: int, h: torch.Tensor, x: torch.Tensor):
         ctx.stack, ctx.s = stack, s
         stack.wh[s] = weakref.ref(h)
         out = _alias(stack.V, s)
+        r = _alias(stack.R, s)
         V = stack.V
         if (h.is_cuda and h.is_contiguous() and x.is_contiguous() and h.dtype == V.dtype == x.dtype
                 and h.numel() == x.numel() == stack.n_tok * stack.d and h.shape[-1] == stack.d
@@ -461,22 +509,29 @@ class _WriteDelta(torch.autograd.Function):
                 j_lo = min(max(0, s - 1), nq)         # read s' >= s uses query s' - 1: queries j_lo .. nq - 1
                 if j_lo < nq:
                     dptr = stack.DOTS[j_lo, s]
-            _run("write_dots", _p(h), _p(x), _p(out), _p(stack.R[s]), _p(stack.Q), _p(stack.QB), nq, j_lo, _p(dptr),
+            _run("write_dots", _p(h), _p(x), _p(out), _p(r), _p(stack.Q), _p(stack.QB), nq, j_lo, _p(dptr),
                  stack.n_tok, stack.d, jstride, stack.eps, _dtype_code(V.dtype), _stream(V.device))
             stack.r_done[s] = True
         else:
             torch.sub(h, x, out=out)
-            stack.r_done[s] = False
-        return out
+            _run("rstd_fwd", _p(out), _p(r), stack.n_tok, stack.d, stack.eps, _dtype_code(V.dtype), _stream(V.device))
+            stack.r_done[s] = False           # the update has no scores (the reads form them online)
+        ctx.set_materialize_grads(False)
+        return out, r
 
     @staticmethod
-    def backward(ctx, g: torch.Tensor):
+    def backward(ctx, g: torch.Tensor | None, gr: torch.Tensor | None):
         stack, s = ctx.stack, ctx.s
         ctx.stack = None
-        if stack is None:
-            return None, None, g, -g
+        if s not in stack.assembled:         # the update's gradient, from every read of it and its scale
+            dh, dx, _ = _assemble(stack, s, gr)
+            if g is not None:                # other consumers of the update: their gradient joins both inputs'
+                dh, dx = dh + g, dx - g
+            return None, None, dh, dx
         prep = stack.neg.pop(s, None)        # (gradient of h, gradient of x, the added proposal gradient or None)
         left = stack.gadd.pop(s, None)       # a proposal gradient no update-gradient kernel took
+        if g is None:
+            return None, None, None, None
         if prep is not None:
             dh, dx, added = prep
             if (g.data_ptr() == dh.data_ptr() and g.shape == dh.shape and g.stride() == dh.stride()
@@ -488,8 +543,10 @@ class _WriteDelta(torch.autograd.Function):
 
 
 class _RstdStk(torch.autograd.Function):
-    """Forward: R[s] (skipped when the write stored it). Backward: the finished gradient of update s -- every read
-    of it has run its backward by then -- returned as the update's one gradient (fused_dattn.py:698-722)."""
+    """The scale of update s as a separate node, for a scale DattnStack.rstd cannot take from the write (an update
+    that is not the write's output, or another eps; fused_dattn.py:698-722). Forward: R[s] (the kernel skipped when
+    the write stored it with this eps). Backward: the finished gradient of update s (_assemble) -- every read of it
+    has run its backward by then -- returned as the update's one gradient."""
 
     @staticmethod
     def forward(ctx, stack: DattnStack, s: int, x: torch.Tensor, eps: float):
@@ -508,29 +565,7 @@ class _RstdStk(torch.autograd.Function):
         stack, s, x = ctx.stack, ctx.s, ctx.x
         if stack.dR is None:
             raise RuntimeError("delta_attnres stacked read: the scale's backward ran before any read's backward")
-        xc = x.contiguous()
-        reads = sorted(k for k in stack.bwd if k >= max(s, 1))     # the reads of update s whose backward ran
-        if s in reads:   # read s last: when its output gradient is also the added one, the kernel loads it once
-            reads.remove(s)
-            reads.append(s)
-        dv = torch.empty_like(xc)
-        dv_neg = torch.empty_like(xc)
-        grc = None if gr is None else gr.float().contiguous()
-        added = stack.gadd.pop(s, None)       # (g, beta): the combine that took the write's h as its proposal
-        if added is not None and (added[0].shape != x.shape or added[0].dtype != xc.dtype
-                                  or not added[0].is_contiguous()):
-            added = (added[0].to(xc.dtype).contiguous().view(x.shape), added[1])
-        bwd = stack.bwd
-        wz0, wz_row = stack.WZ.data_ptr(), stack.WZ.stride(0) * stack.WZ.element_size()
-        g_ptrs = L.u64_array([bwd[k][2] for k in reads])
-        wz_ptrs = L.u64_array([wz0 + _pair(k, s) * wz_row for k in reads])
-        q_ptrs = L.u64_array([bwd[k][3] for k in reads])
-        _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(xc), _p(stack.R[s]), _p(grc),
-             _p(None if added is None else added[0]), 0.0 if added is None else float(added[1]), _p(dv),
-             _p(dv_neg), stack.n_tok, stack.d, _dtype_code(xc.dtype), _stream(xc.device))
-        stack.assembled.add(s)
-        for k in [k for k in stack.bwd if all(j in stack.assembled for j in range(k + 1))]:
-            del stack.bwd[k]              # every update read by read k has its gradient: drop g_k
+        dv, dv_neg, added = _assemble(stack, s, gr)
         if dv.shape == x.shape:
             stack.neg[s] = (dv, dv_neg, added)   # the write's backward returns dv_neg for its x input
         ctx.stack = ctx.x = None          # release the stack from this node
@@ -613,14 +648,15 @@ class FusedCombineStk(torch.autograd.Function):
     fp32 query gradient, which the last backward of the pass (read 1) returns -- one gradient tensor per pass instead
     of a zero-filled one per read.
 
-    (out, tc, next_prior) = apply(stack, step, query, proposal, h0, coeffs, prior, beta, at_boundary, *updates,
-    *scales) with coeffs (b, t, n-1) and prior (n-1,) the previous read's outputs; next_prior carries no gradient
-    (the prior is a constant of the schedule, as in the reference)."""
+    (out, tc, next_prior) = apply(stack, step, query, proposal, h0, coeffs, prior, beta, at_boundary, *scales) with
+    coeffs (b, t, n-1) and prior (n-1,) the previous read's outputs and scales the n sources' scales (DattnStack.rstd:
+    the reads' autograd edges to the updates' gradient nodes; the updates themselves are read from the stack);
+    next_prior carries no gradient (the prior is a constant of the schedule, as in the reference)."""
 
     @staticmethod
     def forward(ctx, stack: DattnStack, step: int, query, proposal, h0, coeffs, prior, beta: float, at_boundary: bool,
-                *srcs):
-        n = len(srcs) // 2
+                *scales):
+        n = len(scales)
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         if (proposal.dtype != stack.V.dtype or not proposal.is_contiguous() or proposal.shape[:-1] != stack.V.shape[1:3]
                 or proposal.shape[-1] != d or not _aligned(proposal)):
@@ -662,9 +698,9 @@ class FusedCombineStk(torch.autograd.Function):
         # the proposal is the write's h of this step and the newest scale comes from that update's scale node: the
         # proposal's gradient then goes to the update's gradient kernel, which adds it (no separate add)
         wr = stack.wh.get(step)
-        scale = srcs[n + step]
+        scale = scales[step]
         ctx.linked = (proposal.requires_grad and wr is not None and wr() is proposal and scale.grad_fn is not None
-                      and type(scale.grad_fn).__name__ == "_RstdStkBackward")
+                      and type(scale.grad_fn).__name__ in ("_WriteDeltaBackward", "_RstdStkBackward"))
         # an iteration end with the pass's h0: its share of h0's gradient is summed with the other ends' at the
         # first of them (the last to run backward) instead of being written here and added by autograd
         ctx.h0_sum = False
@@ -728,6 +764,6 @@ class FusedCombineStk(torch.autograd.Function):
                 dh0 = dh0.view(ctx.shape)
         grads = (None, None, dquery, dprop, dh0,
                  dcoeffs.view(*ctx.shape[:-1], n - 1), None, None, None,
-                 *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
+                 *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
         ctx.stack = None
         return grads

@@ -56,3 +56,40 @@ def test_forward_chain_replays_in_a_graph(mode, dtype):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref2) and not torch.equal(ref2, ref)
+
+
+@pytest.mark.parametrize("mode", ["scores", "stack", "list"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_training_chain_replays_in_graphs(mode, dtype):
+    """The chain's forward and backward captured as HIP graphs (chain.capture_training): every replay -- with eager
+    chains and synchronizations between them, and after the inputs' contents change -- gives the eager pass's final
+    state, loss and every gradient (h0, each update, the query) bitwise."""
+    from loopback_amd.chain import ChainConfig, capture_training, make_inputs, run_chain
+    cfg = ChainConfig(f"graph-train-{mode}", 256, 2, 4, 2, 300, dtype, True, q_std=0.5)
+    h0, D, Q, G = make_inputs(cfg, DEV)
+    print(f"case graph training {mode} {dtype}", flush=True)
+
+    def eager():
+        h, loss, g = run_chain(cfg, h0, D, Q, G, mode)
+        torch.cuda.synchronize()
+        return h.clone(), loss.clone(), [g["h0"].clone(), g["query"].clone()] + [x.clone() for x in g["D"]]
+
+    ref = eager()
+    step = capture_training(cfg, h0, D, Q, mode)
+    for k in range(4):
+        h, loss, g = step(G)
+        torch.cuda.synchronize()
+        got = [g["h0"].clone(), g["query"].clone()] + [x.clone() for x in g["D"]]
+        assert torch.equal(h, ref[0]) and torch.equal(loss, ref[1]), k
+        assert all(torch.equal(a, b) for a, b in zip(got, ref[2])), k
+        again = eager()                                   # eager work between replays
+        assert torch.equal(again[0], ref[0])
+    with torch.no_grad():
+        D[5].mul_(-0.5)
+        h0.add_(0.25)
+    ref2 = eager()
+    h, loss, g = step(G)
+    torch.cuda.synchronize()
+    assert torch.equal(h, ref2[0]) and torch.equal(loss, ref2[1]) and not torch.equal(ref2[0], ref[0])
+    got = [g["h0"].clone(), g["query"].clone()] + [x.clone() for x in g["D"]]
+    assert all(torch.equal(a, b) for a, b in zip(got, ref2[2]))
