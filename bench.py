@@ -17,7 +17,8 @@ Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / 
   chain         every library kernel of the pass: this build's compulsory bytes / summed kernel time, and the
                 reference dataflow's bytes (its backward read-modify-writes a gradient stack) over the same time and
                 over the wall time;
-  configs       configs 2 and 3 timed the same way (wall time per pass), eager and replayed from HIP graphs
+  configs       configs 2 and 3 timed the same way (wall time per pass), eager and replayed from HIP graphs;
+                config 5, the LM training step with the read, and the same model as Plain Loop (the read's cost)
                 (--no-extra-configs skips them);
   cpu_baseline  the CPU oracle (the restated reference read, torch on the host cores) on a bounded sample of the
                 same chain (T reduced), fwd+bwd, read-tokens/s and effective GB/s; beside it config 1 (the
@@ -398,6 +399,12 @@ def main():
                                          "unit": "read-tokens/s", "backward": c.backward,
                                          "formula_wall_gbs": rb / (ms * 1e-3) / 1e9,
                                          "formula_wall_frac": rb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        from loopback_amd import lm
+        for key, residual in (("c5_lm", "delta_attnres"), ("c5_lm_plain_loop", "none")):
+            rec = lm.time_training(10, 3, residual=residual)
+            extra[key] = {"workload": f"LM training step {rec['config']['topology']} d=768 seq 2048 x batch 8 "
+                                      f"vocab 32000 ({'Loopback read' if residual != 'none' else 'Plain Loop'})",
+                          "ms_per_step": rec["ms_per_step"], "value": rec["value"], "unit": rec["unit"]}
         line["configs"] = extra
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens)

@@ -262,32 +262,48 @@ def bench(argv=None):
     if not torch.cuda.is_available():
         print("lm: no GPU visible", file=sys.stderr)
         sys.exit(3)
+    if a.prefill:
+        dev = torch.device("cuda", 0)
+        cfg = LMConfig(residual=None if a.residual == "none" else "delta_attnres")
+        torch.manual_seed(0)
+        model = LoopbackLM(cfg).to(device=dev, dtype=torch.bfloat16)
+        gen = torch.Generator(device=dev).manual_seed(1)
+        ids = torch.randint(0, cfg.vocab_size, (a.batch, a.seq), device=dev, generator=gen)
+        return _prefill(model, cfg, ids, a)
+    print(json.dumps(time_training(a.steps, a.warmup, a.batch, a.seq, a.residual)), flush=True)
+
+
+def time_training(steps: int = 10, warmup: int = 3, batch: int = 8, seq: int = 2048,
+                  residual: str = "delta_attnres") -> dict:
+    """Config 5's training step on cuda:0 -- the random-init LM in bf16, uniform random ids (batch, seq), AdamW --
+    timed over `steps` steps after `warmup`; residual "none" is the same model as Plain Loop. Returns the record."""
     dev = torch.device("cuda", 0)
-    cfg = LMConfig(residual=None if a.residual == "none" else "delta_attnres")
+    cfg = LMConfig(residual=None if residual == "none" else "delta_attnres")
     torch.manual_seed(0)
     model = LoopbackLM(cfg).to(device=dev, dtype=torch.bfloat16)
     gen = torch.Generator(device=dev).manual_seed(1)
-    ids = torch.randint(0, cfg.vocab_size, (a.batch, a.seq), device=dev, generator=gen)
-    if a.prefill:
-        return _prefill(model, cfg, ids, a)
+    ids = torch.randint(0, cfg.vocab_size, (batch, seq), device=dev, generator=gen)
     opt = make_optimizer(model)
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         train_step(model, opt, ids)
     torch.cuda.synchronize()
     gc.collect()
     gc.freeze()
     t0 = time.perf_counter()
-    for _ in range(a.steps):
+    for _ in range(steps):
         loss = train_step(model, opt, ids)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    tokens = a.batch * a.seq
-    print(json.dumps({"metric": "LM training step tokens/sec (config 5)", "value": tokens * a.steps / dt,
-                      "unit": "tokens/s", "ms_per_step": 1e3 * dt / a.steps, "steps": a.steps, "warmup": a.warmup,
-                      "loss": float(loss), "params": model.num_params(), "dtype": "bf16",
-                      "data": "uniform random token ids", "optimizer": "AdamW (foreach)",
-                      "config": {"topology": cfg.topology(), **asdict(cfg), "batch": a.batch, "seq": a.seq}}),
-          flush=True)
+    gc.unfreeze()
+    tokens = batch * seq
+    rec = {"metric": "LM training step tokens/sec (config 5)", "value": tokens * steps / dt, "unit": "tokens/s",
+           "ms_per_step": 1e3 * dt / steps, "steps": steps, "warmup": warmup, "loss": float(loss),
+           "params": model.num_params(), "dtype": "bf16", "data": "uniform random token ids",
+           "optimizer": "AdamW (foreach)",
+           "config": {"topology": cfg.topology(), **asdict(cfg), "batch": batch, "seq": seq}}
+    del model, opt, ids
+    torch.cuda.empty_cache()
+    return rec
 
 
 def _prefill(model: LoopbackLM, cfg: LMConfig, ids: torch.Tensor, a) -> None:

@@ -160,6 +160,7 @@ def main(argv=None):
     from loopback_amd.chain import CONFIGS
     cfg = CONFIGS[a.config]
     fam_bytes, _ = bench.family_bytes(cfg, a.mode)
+    sv_bytes, _ = bench.survey_bytes(cfg, a.mode)
 
     kt, span_ms = trace_pass(a.trace)
     fetch = counter_pass(a.fetch, "FETCH_SIZE")
@@ -174,13 +175,17 @@ def main(argv=None):
         lines += ["Commands:", "", *["    " + c for c in a.commands.split(";;")], ""]
     lines += [f"One pass (the last complete one of the trace): span {span_ms:.2f} ms between pass starts, "
               f"{busy:.2f} ms of kernel time.", "",
-              "| kernel family | launches | total ms | mean us | algorithmic GB | GB/s at the mean |",
-              "|---|---|---|---|---|---|"]
+              "Algorithmic GB: this build's compulsory rows (bench.py `family_bytes`); survey GB: the reference "
+              "dataflow's rows for the same work (bench.py `survey_bytes`, the bytes of the bench line's roofline), "
+              "each over the family's kernel time, against 8000 GB/s.", "",
+              "| kernel family | launches | total ms | mean us | algorithmic GB | GB/s | survey GB | GB/s (survey) "
+              "| of peak (survey) |", "|---|---|---|---|---|---|---|---|---|"]
     for famname, (n, us) in sorted(kt.items(), key=lambda x: -x[1][1]):
-        ab = fam_bytes.get(famname)
-        gbs = f"{ab / (us * 1e-6) / 1e9:.0f}" if ab else "-"
-        lines.append(f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | "
-                     f"{ab / 1e9:.2f} | {gbs} |" if ab else f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | - | - |")
+        ab, sb = fam_bytes.get(famname), sv_bytes.get(famname)
+        cols = [f"{ab / 1e9:.2f}", f"{ab / (us * 1e-6) / 1e9:.0f}"] if ab else ["-", "-"]
+        cols += ([f"{sb / 1e9:.2f}", f"{sb / (us * 1e-6) / 1e9:.0f}", f"{sb / (us * 1e-6) / 1e9 / 8000:.3f}"]
+                 if sb else ["-", "-", "-"])
+        lines.append(f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | " + " | ".join(cols) + " |")
     if a.stats:   # rocprofv3's own per-kernel summary over the whole run (warm-up and timed passes)
         lines += [""] + stats_table(a.stats, 12)
     with open(os.path.join(a.out, f"kernels_chain_{tag}.md"), "w") as f:
