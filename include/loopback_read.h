@@ -14,6 +14,9 @@
  *     every scale, score, coefficient and gradient scalar is fp32;
  *   - per-source arrays (src_v, src_r, ...) are HOST arrays of n device addresses, copied into the kernel
  *     arguments (no device pointer table, no host-to-device copy); n <= LDR_MAX_SOURCES;
+ *   - except for the *_any entry points at the end, which take what the others reject: any width d >= 1, rows
+ *     aligned to their element size only, up to LDR_ANY_MAX_SOURCES sources, whose addresses come as DEVICE arrays
+ *     (n uint64 in device memory, read by the kernels; the caller keeps them until the launch has run);
  *   - stream is a hipStream_t; nothing synchronizes with the host, nothing allocates device memory;
  *   - the return value is 0, a negative LDR_E_* code (rejected before any launch), or a positive hipError_t
  *     from the launch; ldr_strerror() names it.
@@ -36,11 +39,12 @@ extern "C" {
 #define LDR_MAX_SOURCES 64
 #define LDR_MAX_WIDTH 8192
 #define LDR_MAX_QUERIES 64
+#define LDR_ANY_MAX_SOURCES 1024   /* the *_any entry points */
 
 #define LDR_OK 0
 #define LDR_E_ARG (-1)    /* null pointer, negative size, bad flag */
-#define LDR_E_SHAPE (-2)  /* d not a multiple of 8 or too wide; n or nq out of range */
-#define LDR_E_ALIGN (-3)  /* a vector pointer is not 16-byte aligned */
+#define LDR_E_SHAPE (-2)  /* d not a multiple of 8 or too wide; n or nq out of range (*_any: d < 1, n) */
+#define LDR_E_ALIGN (-3)  /* a vector pointer is not 16-byte aligned (*_any: not element-aligned) */
 #define LDR_E_DTYPE (-4)  /* dtype is neither LDR_F32 nor LDR_BF16 (nor LDR_F16 where taken) */
 
 /* Version of this ABI; bumped on any signature change or change of what an entry point accepts. */
@@ -196,6 +200,50 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
  * counterpart (the reference leaves these adds to autograd). */
 int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
                   void* stream);
+
+/* ---- any-shape entry points ----------------------------------------------------------------------------------
+ * The same computations for the shapes the entry points above reject -- the reference's kernels mask any width
+ * and any source count (BLOCK_D = next_pow2(d), BLOCK_N = next_pow2(n): fused_dattn.py:60-63, 191-194) -- with
+ * per-source addresses in device arrays (see the conventions at the top). One wave per token row; they are the
+ * general path, not the fast one (the module routes to them only for such shapes). */
+
+/* ldr_read_fwd (q == NULL: dots holds the stored raw scores) and ldr_read_fwd_online (q != NULL: the scores are
+ * formed and stored into dots) for any shape: the same outputs and formulas; a zero query with cbar == c0 gives
+ * tc == c0 and out == base bitwise. q, when given, is fp32 [d]. Replaces _dattn_fwd_kernel (fused_dattn.py:55-108),
+ * _dattn_fwd_stk_kernel (410-456) and _dattn_fwd_dots_kernel (588-625) at the shapes ldr_read_fwd does not take. */
+int ldr_read_fwd_any(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* q, float* dots,
+                     int64_t dots_stride, const void* base, const void* h0, float beta, const float* cbar,
+                     int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, void* out,
+                     float* tc, float* p, float* next_prior, int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* ldr_read_bwd1 for any shape (dr a device array too): the same outputs, with the query-gradient partials in
+ * dq_parts rows of dq_part (1 <= dq_parts <= 65535, chosen by the caller; every row is written, zeros where a
+ * workgroup had no token; row stride dq_part_stride >= d, so reads' partials can interleave as for ldr_read_bwd1),
+ * summed by ldr_reduce_rows over dq_parts rows. wz must be 8-byte aligned. Replaces _dattn_bwd1_stk_kernel
+ * (fused_dattn.py:459-493) and pass 1 of _dattn_bwd_kernel (111-151) at the shapes ldr_read_bwd1 does not take. */
+int ldr_read_bwd1_any(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const void* g, const float* gt,
+                      const float* p, const float* dots, int64_t dots_stride, const float* tc, const float* cbar,
+                      int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, float* dcbar,
+                      int64_t dcbar_cols, const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride,
+                      float* dq_part, int64_t dq_parts, int64_t dq_part_stride, void* g_prop, void* g_h0, float beta,
+                      int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* ldr_dv_assemble for any shape (g, wz, q device arrays; 0 <= m <= LDR_ANY_MAX_SOURCES): the same roundings in the
+ * same order, so the bits of ldr_dv_assemble for the same tables. Replaces _dattn_bwd2_stk_kernel
+ * (fused_dattn.py:496-536) and _rstd_bwd_acc_kernel (539-552) at the shapes ldr_dv_assemble does not take. */
+int ldr_dv_assemble_any(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
+                        const float* r, const float* gr, const void* add, float add_beta, void* dv, void* dv_neg,
+                        int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* ldr_read_bwd2_list for any shape (dv a device array). Replaces pass 2 of _dattn_bwd_kernel (fused_dattn.py:
+ * 152-181) at the shapes ldr_read_bwd2_list does not take. */
+int ldr_read_bwd2_list_any(const uint64_t* dv, int64_t n, int accum, const void* g, const float* q, const float* wz,
+                           int64_t wz_stride, int64_t n_tok, int64_t d, int dtype, void* stream);
+
+/* ldr_blend_sum for any shape (g a device array): the same sum in the same order. No reference counterpart (the
+ * reference leaves these adds to autograd, looped_transformer.py:380-381). */
+int ldr_blend_sum_any(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,11 +12,12 @@ import torch  # noqa: F401  -- first: the library must bind to the HIP runtime t
 
 from . import build as _build
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 F32, BF16, F16 = 0, 1, 2   # F16: the scale entry points only
 MAX_SOURCES = 64
 MAX_WIDTH = 8192
 MAX_QUERIES = 64
+ANY_MAX_SOURCES = 1024   # the *_any entry points (device address arrays)
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -56,6 +57,19 @@ SIGNATURES = {
     "ldr_dv_assemble": (_i32, [_u64p, _u64p, _u64p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _f32,
                                _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
     "ldr_blend_sum": (_i32, [_u64p, _i64, _f32, _c_void_p, _i64, _i64, _i32, _c_void_p]),
+    # the any-shape entry points: per-source addresses in device arrays (passed as device addresses)
+    "ldr_read_fwd_any": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _f32,
+                                _c_void_p, _i64, _c_void_p, _i64, _f32, _f32, _c_void_p, _c_void_p, _c_void_p,
+                                _c_void_p, _i64, _i64, _i32, _c_void_p]),
+    "ldr_read_bwd1_any": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                 _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _f32, _f32, _c_void_p, _i64, _c_void_p,
+                                 _i32, _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _f32, _i64, _i64,
+                                 _i32, _c_void_p]),
+    "ldr_dv_assemble_any": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                   _f32, _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
+    "ldr_read_bwd2_list_any": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32,
+                                      _c_void_p]),
+    "ldr_blend_sum_any": (_i32, [_c_void_p, _i64, _f32, _c_void_p, _i64, _i64, _i32, _c_void_p]),
 }
 
 

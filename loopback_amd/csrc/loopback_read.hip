@@ -1835,6 +1835,268 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// any-shape kernels (the *_any entry points): rows of any width d >= 1 at element alignment and up to
+// LDR_ANY_MAX_SOURCES sources, whose addresses come from DEVICE arrays. One wave per token row, the row's columns
+// strided over its 64 lanes (each load instruction covers consecutive elements), row sums by the lane reduction
+// above; per-source scalars of the row in LDS. They compute what the row-layout kernels compute (the same formulas,
+// and for the elementwise ones the same order of every rounding), for the shapes those do not take: d not a
+// multiple of 8 or above LDR_MAX_WIDTH, more than LDR_MAX_SOURCES sources, rows not 16-byte aligned.
+// ---------------------------------------------------------------------------------------------------------------
+constexpr int ANY_MAXS = LDR_ANY_MAX_SOURCES;
+constexpr int ANY_WAVES = WG / 64;
+
+// softmax of a[0..n) in place by the 64 lanes of one wave (all active): p = exp(l - max) / sum, as softmax_lanes
+__device__ __forceinline__ void wave_softmax(float* a, int n) {
+  const int lane = (int)threadIdx.x & 63;
+  float mx = -INFINITY;
+  for (int i = lane; i < n; i += 64) mx = fmaxf(mx, a[i]);
+  mx = lanes_reduce(mx, 64, MaxOp());
+  float s = 0.f;
+  for (int i = lane; i < n; i += 64) {
+    const float e = (a[i] == -INFINITY) ? 0.f : expf(a[i] - mx);
+    a[i] = e;
+    s += e;
+  }
+  s = lanes_reduce(s, 64, AddOp());
+  for (int i = lane; i < n; i += 64) a[i] = a[i] / s;
+  wave_lds_sync();
+}
+
+// per-read constants for up to ANY_MAXS sources: c0, lc = log(max(c0, 1e-8)), p0 = softmax(lc) (by the softmax
+// every row uses, so equal logits give equal bits), and M = sum c0 in source order; the whole workgroup calls
+__device__ void any_prior(const Coef& c, int n, float* s_c0, float* s_lc, float* s_p0, float* s_M) {
+  const int tid = (int)threadIdx.x;
+  for (int i = tid; i < n; i += (int)blockDim.x) {
+    const float v = i < c.c0_cols ? c.lam * c.c0[i] : c.lam;
+    s_c0[i] = v;
+    s_lc[i] = logf(fmaxf(v, 1e-8f));
+    s_p0[i] = s_lc[i];
+  }
+  __syncthreads();
+  if (tid < 64) wave_softmax(s_p0, n);
+  if (tid == 0) {
+    float m = 0.f;
+    for (int i = 0; i < n; ++i) m += s_c0[i];
+    *s_M = m;
+  }
+  __syncthreads();
+}
+
+template <typename T> __device__ __forceinline__ const T* any_row(const uint64_t* tab, int i, int64_t off) {
+  return reinterpret_cast<const T*>(tab[i]) + off;
+}
+
+// The read (k_read_fwd / k_read_online): scores (stored, or formed here when q is given and kept in dots), the
+// softmax, tc, p, and out = base + sum_i (tc_i - cbar_i) v_i (base blended with h0 at an iteration end).
+// Dynamic LDS: c0, lc, p0 [n], M, then one [n] row of logits / weights per wave.
+template <typename T, bool BLEND>
+__global__ __launch_bounds__(WG) void k_any_read(const uint64_t* __restrict__ tv, const uint64_t* __restrict__ tr,
+                                                 int n, const float* __restrict__ q, float* __restrict__ dots,
+                                                 int64_t dots_stride, const T* __restrict__ base,
+                                                 const T* __restrict__ h0, float beta, Coef cf, float inv,
+                                                 T* __restrict__ out, float* __restrict__ tc, float* __restrict__ prob,
+                                                 float* __restrict__ next_prior, int64_t n_tok, int64_t d) {
+  extern __shared__ float any_lds[];
+  const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* s_c0 = any_lds;
+  float* s_lc = s_c0 + n;
+  float* s_p0 = s_lc + n;
+  float* s_M = s_p0 + n;
+  float* s_l = s_M + 4 + wave * n;
+  any_prior(cf, n, s_c0, s_lc, s_p0, s_M);
+  const float M = *s_M;
+  if (next_prior && blockIdx.x == 0)
+    for (int i = tid; i < n; i += WG) next_prior[i] = s_c0[i];
+  for (int64_t tok = (int64_t)blockIdx.x * ANY_WAVES + wave; tok < n_tok; tok += (int64_t)gridDim.x * ANY_WAVES) {
+    const int64_t roff = tok * d;
+    if (q) {   // online scores: q . v_i, kept for the backward
+      for (int i = 0; i < n; ++i) {
+        const T* v = any_row<T>(tv, i, roff);
+        float a = 0.f;
+        for (int64_t k = lane; k < d; k += 64) a += q[k] * ld1(v + k);
+        a = lanes_reduce(a, 64, AddOp());
+        if (lane == 0) {
+          dots[(int64_t)i * dots_stride + tok] = a;
+          s_l[i] = a * reinterpret_cast<const float*>(tr[i])[tok] * inv + s_lc[i];
+        }
+      }
+    } else {
+      for (int i = lane; i < n; i += 64)
+        s_l[i] = dots[(int64_t)i * dots_stride + tok] * reinterpret_cast<const float*>(tr[i])[tok] * inv + s_lc[i];
+    }
+    wave_lds_sync();
+    wave_softmax(s_l, n);
+    for (int i = lane; i < n; i += 64) {
+      const float p = s_l[i];
+      const float tcv = s_c0[i] + M * (p - s_p0[i]);
+      tc[tok * n + i] = tcv;
+      if (prob) prob[tok * n + i] = p;   // for the backward only
+      s_l[i] = tcv - coef_cbar(cf, tok, i);
+    }
+    wave_lds_sync();
+    for (int64_t k = lane; k < d; k += 64) {
+      float acc = ld1(base + roff + k);
+      if (BLEND) {   // base = proposal + beta (h0 - proposal), each step rounded as the caller's ops
+#pragma clang fp contract(off)
+        const float hv = ld1(h0 + roff + k);
+        acc = IO<T>::round(acc + IO<T>::round(beta * IO<T>::round(hv - acc)));
+      }
+      for (int i = 0; i < n; ++i) acc += s_l[i] * ld1(any_row<T>(tv, i, roff) + k);
+      st1(out + roff + k, acc);
+    }
+    wave_lds_sync();   // the row's weights are read before the next row overwrites them
+  }
+}
+
+// Backward pass 1 (k_bwd1): g . v_i, then per source dz = p (M (g.v + gt) - Sacc), dcbar = -lam g.v, dr (+)= dz
+// (q . v) / sqrt(d), the (w, dz r / sqrt(d)) pair, and the row's share of dq, sum_i dz_i r_i v_i, added into the
+// wave's partial row dq_part[blockIdx.x] (one wave per workgroup; scaled by 1/sqrt(d) at the end); the blend's
+// gradients when asked. Dynamic LDS: g.v, p, M (g.v + gt), dz r [n].
+template <typename T>
+__global__ __launch_bounds__(64) void k_any_bwd1(const uint64_t* __restrict__ tv, const uint64_t* __restrict__ tr, int n,
+                                                 const T* __restrict__ g, const float* __restrict__ gt,
+                                                 const float* __restrict__ prob, const float* __restrict__ dots,
+                                                 int64_t dots_stride, const float* __restrict__ tcp, Coef cf,
+                                                 float inv, float* __restrict__ dcbar, int dcbar_cols,
+                                                 const uint64_t* __restrict__ tdr, int dr_accum,
+                                                 float* __restrict__ wz, int64_t wz_stride,
+                                                 float* __restrict__ dq_part, int64_t dq_stride,
+                                                 T* __restrict__ g_prop, T* __restrict__ g_h0, float beta,
+                                                 int64_t n_tok, int64_t d) {
+  extern __shared__ float any_lds[];
+  const int lane = (int)threadIdx.x;
+  float* s_gd = any_lds;
+  float* s_p = s_gd + n;
+  float* s_gp = s_p + n;
+  float* s_c = s_gp + n;
+  float M = 0.f;   // sum c0 in source order, as any_prior forms it (each product rounded before the sum)
+  {
+#pragma clang fp contract(off)
+    for (int i = 0; i < n; ++i) M += i < cf.c0_cols ? cf.lam * cf.c0[i] : cf.lam;
+  }
+  float* dqp = dq_part + (int64_t)blockIdx.x * dq_stride;
+  for (int64_t k = lane; k < d; k += 64) dqp[k] = 0.f;
+  for (int64_t tok = blockIdx.x; tok < n_tok; tok += gridDim.x) {
+    const int64_t roff = tok * d;
+    if (g_prop || g_h0) {   // the blend's gradients: beta g to h0, g - beta g to the proposal
+#pragma clang fp contract(off)
+      for (int64_t k = lane; k < d; k += 64) {
+        const float gv = ld1(g + roff + k);
+        const float gb = IO<T>::round(beta * gv);
+        if (g_h0) st1(g_h0 + roff + k, gb);
+        if (g_prop) st1(g_prop + roff + k, gv - gb);
+      }
+    }
+    for (int i = 0; i < n; ++i) {
+      const T* v = any_row<T>(tv, i, roff);
+      float a = 0.f;
+      for (int64_t k = lane; k < d; k += 64) a += ld1(g + roff + k) * ld1(v + k);
+      a = lanes_reduce(a, 64, AddOp());
+      if (lane == 0) s_gd[i] = a;
+    }
+    wave_lds_sync();
+    for (int i = lane; i < n; i += 64) {
+      s_p[i] = prob[tok * n + i];
+      s_gp[i] = M * (s_gd[i] + (gt ? gt[tok * n + i] : 0.f));
+    }
+    wave_lds_sync();
+    float sacc = 0.f;   // every lane forms the same sum, in source order
+    for (int i = 0; i < n; ++i) sacc += s_p[i] * s_gp[i];
+    for (int i = lane; i < n; i += 64) {
+      const float gd = s_gd[i];
+      const float dz = s_p[i] * (s_gp[i] - sacc);
+      if (i < dcbar_cols) dcbar[tok * dcbar_cols + i] = -(cf.lam * gd);
+      float* dri = reinterpret_cast<float*>(tdr[i]);
+      const float drv = dz * dots[(int64_t)i * dots_stride + tok] * inv;
+      dri[tok] = dr_accum ? dri[tok] + drv : drv;
+      const float r = reinterpret_cast<const float*>(tr[i])[tok];
+      *reinterpret_cast<float2*>(wz + 2 * ((int64_t)i * wz_stride + tok)) =
+          make_float2(tcp[tok * n + i] - coef_cbar(cf, tok, i), dz * r * inv);
+      s_c[i] = dz * r;
+    }
+    wave_lds_sync();
+    for (int64_t k = lane; k < d; k += 64) {
+      float a = 0.f;
+      for (int i = 0; i < n; ++i) a += s_c[i] * ld1(any_row<T>(tv, i, roff) + k);
+      dqp[k] += a;
+    }
+    wave_lds_sync();   // the row's scalars are read before the next row overwrites them
+  }
+  for (int64_t k = lane; k < d; k += 64) dqp[k] *= inv;
+}
+
+// The update gradient (k_dv_assemble): per element, the reads' shares w g + dzr q in table order as two explicit
+// fused multiply-adds each, the scale's term, then dv_neg = -dv and the added gradient -- the same roundings in the
+// same order as k_dv_assemble, so the same bits for the same table.
+template <typename T>
+__global__ __launch_bounds__(WG) void k_any_dv_assemble(const uint64_t* __restrict__ tg, const uint64_t* __restrict__ twz,
+                                                        const uint64_t* __restrict__ tq, int m,
+                                                        const T* __restrict__ vsrc, const float* __restrict__ r,
+                                                        const float* __restrict__ gr, const T* __restrict__ add,
+                                                        float add_beta, T* __restrict__ dv, T* __restrict__ dv_neg,
+                                                        int64_t n_tok, int64_t d) {
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  for (int64_t tok = (int64_t)blockIdx.x * ANY_WAVES + wave; tok < n_tok; tok += (int64_t)gridDim.x * ANY_WAVES) {
+    const int64_t roff = tok * d;
+    const float rv = r[tok];
+    const float c = gr ? gr[tok] * (-rv * rv * rv) / (float)d : 0.f;
+    for (int64_t k = lane; k < d; k += 64) {
+      float acc = 0.f;
+      for (int j = 0; j < m; ++j) {
+        const float2 sc = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(twz[j]) + 2 * tok);
+        const float e = ld1(any_row<T>(tg, j, roff) + k);
+        acc = __builtin_fmaf(sc.y, reinterpret_cast<const float*>(tq[j])[k], __builtin_fmaf(sc.x, e, acc));
+      }
+      acc = __builtin_fmaf(c, ld1(vsrc + roff + k), acc);
+      if (dv_neg) st1(dv_neg + roff + k, -acc);
+      if (add) {   // a gradient of the write's h from elsewhere, added as autograd would add it
+        float a = ld1(add + roff + k);
+        if (add_beta != 0.f) {   // the proposal's share of an iteration-end blend's output gradient
+#pragma clang fp contract(off)
+          a = IO<T>::round(a - IO<T>::round(add_beta * a));
+        }
+        acc = IO<T>::round(acc) + a;
+      }
+      st1(dv + roff + k, acc);
+    }
+  }
+}
+
+// Backward pass 2, list layout (k_bwd2_list): dv_i (=|+=) w_i g + dzr_i q, the accumulation rounded as autograd's
+template <typename T>
+__global__ __launch_bounds__(WG) void k_any_bwd2_list(const uint64_t* __restrict__ tdv, int n, int accum,
+                                                      const T* __restrict__ g, const float* __restrict__ q,
+                                                      const float* __restrict__ wz, int64_t wz_stride, int64_t n_tok,
+                                                      int64_t d) {
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  for (int64_t tok = (int64_t)blockIdx.x * ANY_WAVES + wave; tok < n_tok; tok += (int64_t)gridDim.x * ANY_WAVES) {
+    const int64_t roff = tok * d;
+    for (int i = 0; i < n; ++i) {
+      const float2 s = *reinterpret_cast<const float2*>(wz + 2 * ((int64_t)i * wz_stride + tok));
+      T* dvi = reinterpret_cast<T*>(tdv[i]) + roff;
+      for (int64_t k = lane; k < d; k += 64) {
+        float o = s.x * ld1(g + roff + k) + s.y * q[k];
+        if (accum) o = ld1(dvi + k) + IO<T>::round(o);
+        st1(dvi + k, o);
+      }
+    }
+  }
+}
+
+// out = round(sum_j round(beta * g_j)) in table order (k_blend_sum)
+template <typename T>
+__global__ __launch_bounds__(WG) void k_any_blend_sum(const uint64_t* __restrict__ tg, int m, float beta,
+                                                      T* __restrict__ out, int64_t n_tok, int64_t d) {
+#pragma clang fp contract(off)
+  const int64_t total = n_tok * d;
+  for (int64_t e = (int64_t)blockIdx.x * WG + threadIdx.x; e < total; e += (int64_t)gridDim.x * WG) {
+    float acc = 0.f;
+    for (int j = 0; j < m; ++j) acc += IO<T>::round(beta * ld1(reinterpret_cast<const T*>(tg[j]) + e));
+    st1(out + e, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // host side: argument checks, layout choice, dispatch
 // ---------------------------------------------------------------------------------------------------------------
 int row_layout(int64_t d, int* vpt, int* tpr, int max_vpt = 4, bool wave_rows = true, int force_vpt = 0,
@@ -1979,14 +2241,16 @@ __global__ __launch_bounds__(WG) void k_zero(float* __restrict__ p, int64_t n) {
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 11; }
+int ldr_abi_version(void) { return 12; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
     case LDR_OK: return "ok";
     case LDR_E_ARG: return "loopback_read: invalid argument (null pointer, bad count or flag)";
-    case LDR_E_SHAPE: return "loopback_read: unsupported shape (d must be a multiple of 8 and <= 8192; 1 <= n <= 64)";
-    case LDR_E_ALIGN: return "loopback_read: a vector pointer is not 16-byte aligned";
+    case LDR_E_SHAPE:
+      return "loopback_read: unsupported shape (d a multiple of 8 up to 8192 and 1 <= n <= 64; *_any: d >= 1, "
+             "1 <= n <= 1024)";
+    case LDR_E_ALIGN: return "loopback_read: a vector pointer is not 16-byte aligned (*_any: not element-aligned)";
     case LDR_E_DTYPE: return "loopback_read: dtype must be LDR_F32 or LDR_BF16 (or LDR_F16 for the scale)";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "loopback_read: unknown error";
   }
@@ -2371,6 +2635,121 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
     LDR_AS_LAUNCH(false)
   }
 #undef LDR_AS_LAUNCH
+  return launched();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// any-shape entry points: per-source addresses in device arrays, rows of any width at element alignment
+// ---------------------------------------------------------------------------------------------------------------
+static inline bool al_elt(const void* p, int dtype) {
+  return (reinterpret_cast<uintptr_t>(p) & (uintptr_t)(dtype == LDR_BF16 ? 1u : 3u)) == 0;
+}
+static inline unsigned any_row_grid(int64_t n_tok, int64_t cap) { return grid_of(cdiv(n_tok, ANY_WAVES), cap); }
+
+int ldr_read_fwd_any(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const float* q, float* dots,
+                     int64_t dots_stride, const void* base, const void* h0, float beta, const float* cbar,
+                     int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, void* out,
+                     float* tc, float* p, float* next_prior, int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (n < 1 || n > ANY_MAXS || d < 1) return LDR_E_SHAPE;
+  if (!src_v || !src_r || n_tok < 0 || !tok_ptr(dots, n_tok) || dots_stride < n_tok || !tok_ptr(base, n_tok) ||
+      !tok_ptr(cbar, n_tok) || !c0 || !tok_ptr(out, n_tok) || !tok_ptr(tc, n_tok))
+    return LDR_E_ARG;
+  if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1)) return LDR_E_ARG;
+  if (!al_elt(base, dtype) || !al_elt(out, dtype) || (h0 && !al_elt(h0, dtype))) return LDR_E_ALIGN;
+  if (n_tok == 0 && !next_prior) return LDR_OK;
+  const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
+  const size_t lds = sizeof(float) * (size_t)((3 + ANY_WAVES) * n + 4);
+  const unsigned grid = any_row_grid(n_tok, 4096);   // no tokens: one workgroup writes next_prior
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define LDR_ANY_READ(BL)                                                                                          \
+  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_any_read<T, BL>), dim3(grid), dim3(WG), lds, st, src_v, src_r,    \
+                                             (int)n, q, dots, dots_stride, static_cast<const T*>(base),           \
+                                             static_cast<const T*>(h0), beta, cf, inv_sqrt_d, static_cast<T*>(out), \
+                                             tc, p, next_prior, n_tok, d))
+  if (h0) {
+    LDR_ANY_READ(true)
+  } else {
+    LDR_ANY_READ(false)
+  }
+#undef LDR_ANY_READ
+  return launched();
+}
+
+int ldr_read_bwd1_any(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const void* g, const float* gt,
+                      const float* p, const float* dots, int64_t dots_stride, const float* tc, const float* cbar,
+                      int64_t cbar_cols, const float* c0, int64_t c0_cols, float lam, float inv_sqrt_d, float* dcbar,
+                      int64_t dcbar_cols, const uint64_t* dr, int dr_accum, float* wz, int64_t wz_stride,
+                      float* dq_part, int64_t dq_parts, int64_t dq_part_stride, void* g_prop, void* g_h0, float beta,
+                      int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (n < 1 || n > ANY_MAXS || d < 1) return LDR_E_SHAPE;
+  if (!src_v || !src_r || n_tok < 0 || !tok_ptr(g, n_tok) || !tok_ptr(p, n_tok) || !tok_ptr(dots, n_tok) ||
+      dots_stride < n_tok || !tok_ptr(tc, n_tok) || !tok_ptr(cbar, n_tok) || !c0 || !tok_ptr(dcbar, n_tok) || !dr ||
+      !tok_ptr(wz, n_tok) || !dq_part || wz_stride < n_tok || dq_part_stride < d || dq_parts < 1 ||
+      dq_parts > 65535 || (dr_accum != 0 && dr_accum != 1))
+    return LDR_E_ARG;
+  if ((cbar_cols != n && cbar_cols != n - 1) || (c0_cols != n && c0_cols != n - 1) || dcbar_cols < 0 ||
+      dcbar_cols > n)
+    return LDR_E_ARG;
+  if (!al_elt(g, dtype) || (g_prop && !al_elt(g_prop, dtype)) || (g_h0 && !al_elt(g_h0, dtype)) ||
+      (reinterpret_cast<uintptr_t>(wz) & 7u))
+    return LDR_E_ALIGN;
+  const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
+  const size_t lds = sizeof(float) * (size_t)(4 * n);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // every partial row is written (zeros for a workgroup without tokens), so the caller sums dq_parts rows
+  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_any_bwd1<T>), dim3((unsigned)dq_parts), dim3(64), lds, st, src_v,
+                                             src_r, (int)n, static_cast<const T*>(g), gt, p, dots, dots_stride, tc,
+                                             cf, inv_sqrt_d, dcbar, (int)dcbar_cols, dr, dr_accum, wz, wz_stride,
+                                             dq_part, dq_part_stride, static_cast<T*>(g_prop), static_cast<T*>(g_h0),
+                                             beta, n_tok, d))
+  return launched();
+}
+
+int ldr_dv_assemble_any(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
+                        const float* r, const float* gr, const void* add, float add_beta, void* dv, void* dv_neg,
+                        int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (m < 0 || m > ANY_MAXS || d < 1) return LDR_E_SHAPE;
+  if ((m > 0 && (!g || !wz || !q)) || !tok_ptr(v, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(dv, n_tok) || n_tok < 0)
+    return LDR_E_ARG;
+  if (!al_elt(v, dtype) || !al_elt(dv, dtype) || (dv_neg && !al_elt(dv_neg, dtype)) || (add && !al_elt(add, dtype)))
+    return LDR_E_ALIGN;
+  if (n_tok == 0) return LDR_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_any_dv_assemble<T>), dim3(any_row_grid(n_tok, 8192)), dim3(WG), 0, st,
+                                             g, wz, q, (int)m, static_cast<const T*>(v), r, gr,
+                                             static_cast<const T*>(add), add_beta, static_cast<T*>(dv),
+                                             static_cast<T*>(dv_neg), n_tok, d))
+  return launched();
+}
+
+int ldr_read_bwd2_list_any(const uint64_t* dv, int64_t n, int accum, const void* g, const float* q, const float* wz,
+                           int64_t wz_stride, int64_t n_tok, int64_t d, int dtype, void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (n < 1 || n > ANY_MAXS || d < 1) return LDR_E_SHAPE;
+  if (!dv || !tok_ptr(g, n_tok) || !q || !tok_ptr(wz, n_tok) || wz_stride < n_tok || n_tok < 0 ||
+      (accum != 0 && accum != 1))
+    return LDR_E_ARG;
+  if (!al_elt(g, dtype) || (reinterpret_cast<uintptr_t>(wz) & 7u)) return LDR_E_ALIGN;
+  if (n_tok == 0) return LDR_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_any_bwd2_list<T>), dim3(any_row_grid(n_tok, 8192)), dim3(WG), 0, st,
+                                             dv, (int)n, accum, static_cast<const T*>(g), q, wz, wz_stride, n_tok, d))
+  return launched();
+}
+
+int ldr_blend_sum_any(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
+                      void* stream) {
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (m < 1 || m > ANY_MAXS || d < 1) return LDR_E_SHAPE;
+  if (!g || !tok_ptr(out, n_tok) || n_tok < 0) return LDR_E_ARG;
+  if (!al_elt(out, dtype)) return LDR_E_ALIGN;
+  if (n_tok == 0) return LDR_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_any_blend_sum<T>), dim3(grid_of(cdiv(n_tok * d, WG), 8192)), dim3(WG),
+                                             0, st, g, (int)m, beta, static_cast<T*>(out), n_tok, d))
   return launched();
 }
 

@@ -46,6 +46,7 @@ __all__ = ["rstd_ref", "rstd", "fused_read_supported", "FusedDattnRead", "DattnG
 
 _LIB = L.LIB
 MAX_SOURCES = L.MAX_SOURCES
+ANY_MAX_SOURCES = L.ANY_MAX_SOURCES
 
 
 # ---------------------------------------------------------------------------------------------------------------
@@ -99,6 +100,70 @@ def _f32(t: torch.Tensor) -> torch.Tensor:
 
 def _inv_sqrt(d: int) -> float:
     return 1.0 / (d ** 0.5)
+
+
+def _fast(d: int, n: int, *rows) -> bool:
+    """Whether the row-layout entry points take a call: width d a multiple of 8 up to MAX_WIDTH, at most
+    MAX_SOURCES sources, every row tensor 16-byte aligned. Other calls go to the any-shape entry points (rows of any
+    width at element alignment, up to ANY_MAX_SOURCES sources, per-source addresses in device arrays)."""
+    if d % 8 or d > L.MAX_WIDTH or n > MAX_SOURCES:
+        return False
+    for t in rows:
+        if t is not None and t.data_ptr() % 16:
+            return False
+    return True
+
+
+def _dev_addrs(addrs, dev: torch.device) -> torch.Tensor:
+    """A device array of addresses for an any-shape entry point, copied on the current stream from pinned host
+    memory (torch keeps the host buffer until the copy has run; the device array is freed in stream order)."""
+    host = torch.tensor(list(addrs), dtype=torch.int64).pin_memory()
+    return host.to(dev, non_blocking=True)
+
+
+def _b1_parts(n_tok: int, d: int) -> int:
+    """Rows of backward pass 1's query-gradient partials: the row-layout kernel's workgroups (which the any-shape
+    kernel then also uses), or for widths that layout does not take one per 64 tokens, up to 512."""
+    p = L.bwd1_parts(n_tok, d)
+    return p if p > 0 else max(1, min(512, -(-n_tok // 64)))
+
+
+class _Src:
+    """The sources of one read: host address arrays (v, r; dr for the scale gradients) for the row-layout entry
+    points when `fast`, else device address arrays for the any-shape ones."""
+    __slots__ = ("fast", "v", "r", "dr")
+
+    def __init__(self, fast: bool, v, r, dr=None):
+        self.fast, self.v, self.r, self.dr = fast, v, r, dr
+
+    @staticmethod
+    def of(fast: bool, values, rstds, dev, drs=None):
+        addrs = (lambda ts: L.u64_array(t.data_ptr() for t in ts)) if fast else \
+                (lambda ts: _dev_addrs((t.data_ptr() for t in ts), dev))
+        return _Src(fast, addrs(values), addrs(rstds), None if drs is None else addrs(drs))
+
+    def ptrs(self):
+        """(v, r) as entry-point arguments: host arrays, or the device arrays' addresses."""
+        return (self.v, self.r) if self.fast else (self.v.data_ptr(), self.r.data_ptr())
+
+    def dr_ptr(self):
+        return self.dr if self.fast else self.dr.data_ptr()
+
+
+def _read(src: _Src, n: int, q, dots, stored: bool, base, h0, beta: float, cbar, cols: int, c0, lam: float, out, tc,
+          prob, next_prior, n_tok: int, d: int, dt: int, st) -> None:
+    """One read forward from stored raw scores (stored: dots[i, tok]) or with the scores formed from the fp32 query q
+    and kept in dots: the row-layout kernels when src.fast, else the any-shape kernel. cols: n (cbar, c0 as the read
+    takes them) or n - 1 (the previous read's coefficients and prior, scaled by lam, the newest entry implied)."""
+    v, r = src.ptrs()
+    tail = (_p(base), _p(h0), float(beta), _p(cbar), cols, _p(c0), cols, float(lam), _inv_sqrt(d), _p(out), _p(tc),
+            _p(prob), _p(next_prior), n_tok, d, dt, st)
+    if not src.fast:
+        _run("read_fwd_any", v, r, n, None if stored else _p(q), _p(dots), n_tok, *tail)
+    elif stored:
+        _run("read_fwd", v, r, n, _p(dots), n_tok, *tail)
+    else:
+        _run("read_fwd_online", v, r, n, _p(q), _p(dots), n_tok, *tail)
 
 
 # Optional launch observer: a callable name -> context manager, entered around every library call (the bench uses it
@@ -166,19 +231,19 @@ def rstd(delta: torch.Tensor, eps: float) -> torch.Tensor:
 # ---------------------------------------------------------------------------------------------------------------
 def fused_read_supported(base, values, rstds, cbar) -> bool:
     """The reference's gate (fused_dattn.py:379-395) -- GPU, contiguous, same-shape same-dtype bf16/fp32 sources and
-    base, contiguous fp32 (b, t, 1) rstds, contiguous fp32 (b, t, n) cbar -- plus this build's kernel limits:
-    d a multiple of 8 and at most 8192, at most 64 sources, 16-byte aligned rows."""
+    base, contiguous fp32 (b, t, 1) rstds, contiguous fp32 (b, t, n) cbar -- plus the kernels' source count (at most
+    ANY_MAX_SOURCES) and one device. Any width and alignment: rows the row-layout kernels do not take go to the
+    any-shape kernels."""
     v0 = values[0]
     if not v0.is_cuda or v0.dtype not in (torch.bfloat16, torch.float32):
         return False
     shape = v0.shape
-    d = shape[-1]
-    if d % 8 or d > L.MAX_WIDTH or len(values) > MAX_SOURCES or len(rstds) != len(values):
+    if shape[-1] < 1 or len(values) > ANY_MAX_SOURCES or len(rstds) != len(values):
         return False
-    if base.dtype != v0.dtype or base.shape != shape or not base.is_contiguous() or not _aligned(base):
+    if base.dtype != v0.dtype or base.shape != shape or base.device != v0.device:
         return False
     for v in values:
-        if v.dtype != v0.dtype or v.shape != shape or not v.is_contiguous() or not _aligned(v) or v.device != v0.device:
+        if v.dtype != v0.dtype or v.shape != shape or not v.is_contiguous() or v.device != v0.device:
             return False
     rshape = shape[:-1] + (1,)
     for r in rstds:
@@ -211,19 +276,19 @@ def _forward_impl(ctx, q, base, cbar, c0, srcs):
     grad = any(ctx.needs_input_grad)      # else no backward: the probabilities are not stored
     prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
     dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
-    vp = L.u64_array(v.data_ptr() for v in values)
-    rp = L.u64_array(r.data_ptr() for r in rstds)
-    _run("read_fwd_online", vp, rp, n, _p(qc), _p(dots), n_tok, _p(base_c), _p(None), 0.0, _p(cbar_c), n, _p(c0c),
-         n, 1.0, _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
+    src = _Src.of(_fast(d, n, base_c, qc, *values), values, rstds, dev)
+    _read(src, n, qc, dots, False, base_c, None, 0.0, cbar_c, n, c0c, 1.0, out, tc, prob, None, n_tok, d, dt, st)
     if grad:
         ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc, *values, *rstds)
     ctx.n, ctx.q_dtype, ctx.base_shape = n, q.dtype, base.shape
     return out, tc.view(*base.shape[:-1], n)
 
 
-def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_ptrs, dr_accum, wz, wz_stride, n_tok, d,
+def _bwd1(src: _Src, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_accum, wz, wz_stride, n_tok, d,
           dtype, dev, cols=None, lam=1.0, g_prop=None, g_h0=None, beta=0.0, dq=None, part=None):
-    """Pass 1 of the backward plus the dq reduction; returns (dq fp32, dcbar [n_tok, cols]). prob and dots are the
+    """Pass 1 of the backward plus the dq reduction; returns (dq fp32, dcbar [n_tok, cols]). src: the sources with the
+    scale gradients' addresses (src.dr), on the row-layout kernel when src.fast (and g, g_prop, g_h0 are 16-byte
+    aligned), else on the any-shape kernel. prob and dots are the
     forward's probabilities [n_tok, n] and raw scores [n, >= n_tok] (row stride dots.stride(0)). cols = n: cbar_c and c0c
     are the read's own; cols = n - 1: they are the previous read's coefficients and prior (scaled by lam, the newest
     entry implied) and dcbar is the gradient of those coefficients. g_prop / g_h0 receive the iteration-end blend's
@@ -234,12 +299,16 @@ def _bwd1(values_ptrs, rstd_ptrs, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_ptrs
     cols = n if cols is None else cols
     gt_c = None if gt is None else gt.reshape(n_tok, n).float().contiguous()
     dcbar = torch.empty((n_tok, cols), device=dev, dtype=torch.float32)
-    parts = L.bwd1_parts(n_tok, d)
-    dq_part = torch.empty((max(1, parts), d), device=dev, dtype=torch.float32) if part is None else part
-    _run("read_bwd1", values_ptrs, rstd_ptrs, n, _p(g), _p(gt_c), _p(prob), _p(dots), dots.stride(0), _p(tc),
-         _p(cbar_c), cols,
-         _p(c0c), cols, float(lam), _inv_sqrt(d), _p(dcbar), cols, dr_ptrs, int(dr_accum), _p(wz), wz_stride,
-         _p(dq_part), dq_part.stride(0), _p(g_prop), _p(g_h0), float(beta), n_tok, d, dtype, st)
+    parts = _b1_parts(n_tok, d) if part is None else part.shape[0]
+    dq_part = torch.empty((parts, d), device=dev, dtype=torch.float32) if part is None else part
+    v, r = src.ptrs()
+    head = (v, r, n, _p(g), _p(gt_c), _p(prob), _p(dots), dots.stride(0), _p(tc), _p(cbar_c), cols, _p(c0c), cols,
+            float(lam), _inv_sqrt(d), _p(dcbar), cols, src.dr_ptr(), int(dr_accum), _p(wz), wz_stride, _p(dq_part))
+    tail = (_p(g_prop), _p(g_h0), float(beta), n_tok, d, dtype, st)
+    if src.fast and _fast(d, n, g, g_prop, g_h0):
+        _run("read_bwd1", *head, dq_part.stride(0), *tail)
+    else:
+        _run("read_bwd1_any", *head, parts, dq_part.stride(0), *tail)
     if part is not None:
         return None, dcbar
     dq = torch.empty(d, device=dev, dtype=torch.float32) if dq is None else dq
@@ -261,17 +330,21 @@ def _backward_impl(ctx, g, gt, dv, accum):
     dev = v0.device
     dt = _dtype_code(v0.dtype)
     g = g.to(v0.dtype).contiguous()
-    vp = L.u64_array(v.data_ptr() for v in values)
-    rp = L.u64_array(r.data_ptr() for r in rstds)
     dr = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
     wz = torch.empty((n, n_tok, 2), device=dev, dtype=torch.float32)
-    dq, dcbar = _bwd1(vp, rp, n, g, gt, prob, dots, tc, cbar_c, c0c, L.u64_array(dr[i].data_ptr() for i in range(n)),
-                      False, wz, n_tok, n_tok, d, dt, dev)
+    fast = _fast(d, n, g, qc, *values, *dv)
+    src = _Src.of(fast, values, rstds, dev, drs=[dr[i] for i in range(n)])
+    dq, dcbar = _bwd1(src, n, g, gt, prob, dots, tc, cbar_c, c0c, False, wz, n_tok, n_tok, d, dt, dev)
     for t in dv:
-        if t.dtype != v0.dtype or not t.is_contiguous() or t.numel() != v0.numel() or not _aligned(t):
+        if t.dtype != v0.dtype or not t.is_contiguous() or t.numel() != v0.numel():
             raise RuntimeError("delta_attnres HIP read: gradient buffers must match the sources")
-    _run("read_bwd2_list", L.u64_array(t.data_ptr() for t in dv), n, int(bool(accum)), _p(g), _p(qc), _p(wz),
-                                    n_tok, n_tok, d, dt, _stream(dev))
+    if fast:
+        _run("read_bwd2_list", L.u64_array(t.data_ptr() for t in dv), n, int(bool(accum)), _p(g), _p(qc), _p(wz),
+             n_tok, n_tok, d, dt, _stream(dev))
+    else:
+        dvt = _dev_addrs((t.data_ptr() for t in dv), dev)
+        _run("read_bwd2_list_any", _p(dvt), n, int(bool(accum)), _p(g), _p(qc), _p(wz), n_tok, n_tok, d, dt,
+             _stream(dev))
     return dq.to(ctx.q_dtype), g, dcbar.view(*ctx.base_shape[:-1], n), [dr[i].view_as(rstds[i]) for i in range(n)]
 
 
@@ -362,17 +435,21 @@ class DattnStack:
     matrix-core product loads them."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
                  "assembled", "neg", "dq_parts", "dq_rows", "wh", "gadd", "h0_ref", "h0_steps", "h0_g", "vptr",
-                 "rptr", "drptr", "wout")
+                 "rptr", "drptr", "wout", "fast_d", "src_fast", "src_any")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
         n_steps = int(n_steps)
         if dtype not in (torch.bfloat16, torch.float32):
             raise RuntimeError(f"delta_attnres stacked read: dtype must be bfloat16 or float32, got {dtype}")
-        if d % 8 or d > L.MAX_WIDTH or n_steps < 1 or n_steps > MAX_SOURCES:
-            raise RuntimeError(f"delta_attnres stacked read: unsupported shape d={d} n_steps={n_steps} (d a multiple "
-                               f"of 8 up to {L.MAX_WIDTH}, at most {MAX_SOURCES} steps)")
+        if d < 1 or n_steps < 1 or n_steps > ANY_MAX_SOURCES:
+            raise RuntimeError(f"delta_attnres stacked read: unsupported shape d={d} n_steps={n_steps} (d >= 1, "
+                               f"1 to {ANY_MAX_SOURCES} steps)")
         self.n_steps, self.n_tok, self.d = n_steps, b * t, d
+        # rows the row-layout kernels take (the slices of V are then 16-byte aligned); other widths, and reads of
+        # more than MAX_SOURCES sources, run on the any-shape kernels
+        self.fast_d = d % 8 == 0 and d <= L.MAX_WIDTH
+        self.src_fast = self.src_any = None
         self.V = torch.empty((n_steps, b, t, d), dtype=dtype, device=device)
         self.R = torch.empty((n_steps, b, t, 1), dtype=torch.float32, device=device)
         _require_gpu(self.V, "the stack")
@@ -400,9 +477,12 @@ class DattnStack:
         if query is not None:
             self.Q = _f32(query)
             nq = self.Q.shape[0]
-            if nq > L.MAX_QUERIES or self.Q.shape[-1] != d:
-                raise RuntimeError(f"delta_attnres stacked read: query must be (<= {L.MAX_QUERIES}, {d}), "
+            if self.Q.dim() != 2 or self.Q.shape[-1] != d:
+                raise RuntimeError(f"delta_attnres stacked read: query must be (n_steps - 1, {d}), "
                                    f"got {tuple(self.Q.shape)}")
+        # the write kernel stores the scores of rows it takes against up to MAX_QUERIES queries; otherwise the reads
+        # form their scores as they read (the same read, as with LOOP_DATTN_DOTS=0)
+        if query is not None and self.fast_d and nq <= L.MAX_QUERIES:
             self.DOTS = torch.empty((max(1, nq), n_steps, b * t), dtype=torch.float32, device=device)
             if dtype == torch.bfloat16 and nq > 0:   # the queries' bf16 parts: the write's matrix-core operand table
                 self.QB = torch.empty(int(L.LIB.ldr_query_parts_elems(nq, d)), dtype=torch.bfloat16, device=device)
@@ -422,6 +502,20 @@ class DattnStack:
         if w is not None and w[0]() is delta and float(eps) == self.eps:
             return w[1]
         return _RstdStk.apply(self, s, delta, float(eps))
+
+    def src(self, n: int, *rows) -> _Src:
+        """The stack's sources for a read of n of them (with the scale gradients' addresses once the backward state
+        exists): the host tables for the row-layout kernels when they take the read (n <= MAX_SOURCES, the other
+        rows 16-byte aligned), else device arrays of the same addresses, made on first use."""
+        if self.fast_d and _fast(self.d, n, *rows):
+            if self.src_fast is None or (self.src_fast.dr is None and self.drptr is not None):
+                self.src_fast = _Src(True, self.vptr, self.rptr, self.drptr)
+            return self.src_fast
+        if self.src_any is None or (self.src_any.dr is None and self.dR is not None):
+            dev = self.V.device
+            self.src_any = _Src(False, _dev_addrs(self.vptr, dev), _dev_addrs(self.rptr, dev),
+                                None if self.dR is None else _dev_addrs(self.drptr, dev))
+        return self.src_any
 
     def grads(self):
         """Allocate the backward state on the first backward of the pass; False then, True afterwards."""
@@ -466,16 +560,20 @@ def _assemble(stack: DattnStack, s: int, gr):
                               or not added[0].is_contiguous()):
         added = (added[0].to(v.dtype).contiguous().view(v.shape), added[1])
     bwd = stack.bwd
+    fast = stack.fast_d and _fast(stack.d, len(reads), None if added is None else added[0],
+                                  *[bwd[k][0] for k in reads], *[bwd[k][1] for k in reads])
+    tables = None
     if reads:
         wz0, wz_row = stack.WZ.data_ptr(), stack.WZ.stride(0) * stack.WZ.element_size()
-        g_ptrs = L.u64_array([bwd[k][2] for k in reads])
-        wz_ptrs = L.u64_array([wz0 + _pair(k, s) * wz_row for k in reads])
-        q_ptrs = L.u64_array([bwd[k][3] for k in reads])
+        tables = ([bwd[k][2] for k in reads], [wz0 + _pair(k, s) * wz_row for k in reads], [bwd[k][3] for k in reads])
+    args = (len(reads), _p(v), _p(stack.R[s]), _p(grc), _p(None if added is None else added[0]),
+            0.0 if added is None else float(added[1]), _p(dv), _p(dv_neg), stack.n_tok, stack.d,
+            _dtype_code(v.dtype), _stream(v.device))
+    if fast:
+        _run("dv_assemble", *([L.u64_array(t) for t in tables] if tables else [None] * 3), *args)
     else:
-        g_ptrs = wz_ptrs = q_ptrs = None
-    _run("dv_assemble", g_ptrs, wz_ptrs, q_ptrs, len(reads), _p(v), _p(stack.R[s]), _p(grc),
-         _p(None if added is None else added[0]), 0.0 if added is None else float(added[1]), _p(dv),
-         _p(dv_neg), stack.n_tok, stack.d, _dtype_code(v.dtype), _stream(v.device))
+        dev_tabs = [_dev_addrs(t, v.device) for t in tables] if tables else None
+        _run("dv_assemble_any", *([t.data_ptr() for t in dev_tabs] if dev_tabs else [None] * 3), *args)
     stack.assembled.add(s)
     for k in [k for k in bwd if all(j in stack.assembled for j in range(k + 1))]:
         del bwd[k]                        # every update read by read k has its gradient: drop g_k
@@ -500,11 +598,11 @@ class _WriteDelta(torch.autograd.Function):
         out = _alias(stack.V, s)
         r = _alias(stack.R, s)
         V = stack.V
-        if (h.is_cuda and h.is_contiguous() and x.is_contiguous() and h.dtype == V.dtype == x.dtype
+        if (stack.fast_d and h.is_cuda and h.is_contiguous() and x.is_contiguous() and h.dtype == V.dtype == x.dtype
                 and h.numel() == x.numel() == stack.n_tok * stack.d and h.shape[-1] == stack.d
                 and _aligned(h) and _aligned(x)):
             nq, j_lo, dptr, jstride = 0, 0, None, stack.n_steps * stack.n_tok
-            if stack.Q is not None:
+            if stack.DOTS is not None:
                 nq = stack.Q.shape[0]
                 j_lo = min(max(0, s - 1), nq)         # read s' >= s uses query s' - 1: queries j_lo .. nq - 1
                 if j_lo < nq:
@@ -585,8 +683,8 @@ class FusedDattnReadStk(torch.autograd.Function):
             raise RuntimeError("delta_attnres stacked read: base must be contiguous, the stack's dtype and shape")
         if not 1 <= n <= stack.n_steps:
             raise RuntimeError(f"delta_attnres stacked read: {n} sources for a stack of {stack.n_steps}")
-        if base.shape[-1] != d or not _aligned(base):
-            raise RuntimeError(f"delta_attnres stacked read: base must have width {d} and 16-byte aligned rows")
+        if base.shape[-1] != d:
+            raise RuntimeError(f"delta_attnres stacked read: base must have width {d}")
         dt = _dtype_code(stack.V.dtype)
         st = _stream(dev)
         qc = _f32(q)
@@ -598,15 +696,11 @@ class FusedDattnReadStk(torch.autograd.Function):
         tc = torch.empty((n_tok, n), device=dev, dtype=torch.float32)
         grad = any(ctx.needs_input_grad)
         prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
-        vp, rp = stack.vptr, stack.rptr
-        if stack.DOTS is not None and step >= 1 and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
-            dots = stack.DOTS[step - 1]          # the stored scores of query step - 1, [source, token]
-            _run("read_fwd", vp, rp, n, _p(dots), n_tok, _p(base), _p(None), 0.0, _p(cbar_c), n, _p(c0c), n, 1.0,
-                 _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
-        else:                                    # online scores, formed (and kept for the backward) as it reads
-            dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
-            _run("read_fwd_online", vp, rp, n, _p(qc), _p(dots), n_tok, _p(base), _p(None), 0.0, _p(cbar_c), n,
-                 _p(c0c), n, 1.0, _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(None), n_tok, d, dt, st)
+        src = stack.src(n, base, qc)
+        stored = stack.DOTS is not None and step >= 1 and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]
+        # the stored scores of query step - 1 [source, token], else formed (and kept for the backward) as it reads
+        dots = stack.DOTS[step - 1] if stored else torch.empty((n, n_tok), device=dev, dtype=torch.float32)
+        _read(src, n, qc, dots, stored, base, None, 0.0, cbar_c, n, c0c, 1.0, out, tc, prob, None, n_tok, d, dt, st)
         if grad:
             ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc)
         ctx.stack, ctx.step, ctx.n, ctx.q_dtype, ctx.base_shape = stack, int(step), n, q.dtype, base.shape
@@ -619,9 +713,8 @@ class FusedDattnReadStk(torch.autograd.Function):
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         stack.grads()
         g = g.to(stack.V.dtype).contiguous()
-        vp, rp, drp = stack.vptr, stack.rptr, stack.drptr
         wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
-        dq, dcbar = _bwd1(vp, rp, n, g, gt, prob, dots, tc, cbar_c, c0c, drp, True, wz, n_tok, n_tok, d,
+        dq, dcbar = _bwd1(stack.src(n, g), n, g, gt, prob, dots, tc, cbar_c, c0c, True, wz, n_tok, n_tok, d,
                           _dtype_code(stack.V.dtype), dev)
         # for the updates' gradients, formed once per update (the tensors, and their addresses for the kernel tables)
         stack.bwd[step] = (g, qc, g.data_ptr(), qc.data_ptr())
@@ -659,10 +752,10 @@ class FusedCombineStk(torch.autograd.Function):
         n = len(scales)
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         if (proposal.dtype != stack.V.dtype or not proposal.is_contiguous() or proposal.shape[:-1] != stack.V.shape[1:3]
-                or proposal.shape[-1] != d or not _aligned(proposal)):
+                or proposal.shape[-1] != d):
             raise RuntimeError("delta_attnres fused combine: proposal must be contiguous, the stack's dtype and shape")
         if at_boundary and (h0 is None or h0.dtype != proposal.dtype or h0.shape != proposal.shape
-                            or not h0.is_contiguous() or not _aligned(h0)):
+                            or not h0.is_contiguous()):
             raise RuntimeError("delta_attnres fused combine: h0 must match the proposal at an iteration end")
         if not 2 <= n <= stack.n_steps or n != step + 1:
             raise RuntimeError(f"delta_attnres fused combine: {n} sources at step {step} of a stack of {stack.n_steps}")
@@ -681,15 +774,12 @@ class FusedCombineStk(torch.autograd.Function):
         grad = any(ctx.needs_input_grad)      # else no backward: the probabilities are not stored
         prob = torch.empty((n_tok, n), device=dev, dtype=torch.float32) if grad else None
         next_prior = torch.empty(n, device=dev, dtype=torch.float32)
-        vp, rp = stack.vptr, stack.rptr
-        blend = (_p(proposal), _p(h0 if at_boundary else None), float(beta), _p(coeffs_c), n - 1, _p(prior_c), n - 1,
-                 lam, _inv_sqrt(d), _p(out), _p(tc), _p(prob), _p(next_prior), n_tok, d, dt, st)
-        if stack.DOTS is not None and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]:
-            dots = stack.DOTS[step - 1]
-            _run("read_fwd", vp, rp, n, _p(dots), n_tok, *blend)
-        else:
-            dots = torch.empty((n, n_tok), device=dev, dtype=torch.float32)
-            _run("read_fwd_online", vp, rp, n, _p(qc), _p(dots), n_tok, *blend)
+        h0b = h0 if at_boundary else None
+        src = stack.src(n, proposal, h0b, qc)
+        stored = stack.DOTS is not None and all(stack.r_done[:n]) and step - 1 < stack.Q.shape[0]
+        dots = stack.DOTS[step - 1] if stored else torch.empty((n, n_tok), device=dev, dtype=torch.float32)
+        _read(src, n, qc, dots, stored, proposal, h0b, beta, coeffs_c, n - 1, prior_c, lam, out, tc, prob, next_prior,
+              n_tok, d, dt, st)
         if grad:
             ctx.save_for_backward(qc, coeffs_c, prior_c, prob, dots, tc)
         ctx.stack, ctx.step, ctx.n, ctx.shape = stack, int(step), n, proposal.shape
@@ -719,19 +809,18 @@ class FusedCombineStk(torch.autograd.Function):
         d, n_tok, dev = stack.d, stack.n_tok, stack.V.device
         stack.grads()
         nq = ctx.q_shape[0]
-        parts = L.bwd1_parts(n_tok, d)
-        if stack.dq_parts is None or stack.dq_parts.shape != (max(1, parts), nq, d):
+        parts = _b1_parts(n_tok, d)
+        if stack.dq_parts is None or stack.dq_parts.shape != (parts, nq, d):
             # every read's dq partials, interleaved [part][read][d]: one reduction at the pass's last read
-            stack.dq_parts = torch.empty((max(1, parts), nq, d), device=dev, dtype=torch.float32)
+            stack.dq_parts = torch.empty((parts, nq, d), device=dev, dtype=torch.float32)
             stack.dq_rows = set()
         g = torch.zeros(ctx.shape, device=dev, dtype=stack.V.dtype) if g is None else g.to(stack.V.dtype).contiguous()
         # the blend's gradients are written only where no later kernel forms them from g
         need_prop, need_h0 = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
         g_prop = torch.empty_like(g) if ctx.at_boundary and not ctx.linked and need_prop else None
         g_h0 = torch.empty_like(g) if ctx.at_boundary and not ctx.h0_sum and need_h0 else None
-        vp, rp, drp = stack.vptr, stack.rptr, stack.drptr
         wz = stack.WZ[_pair(step, 0):_pair(step, 0) + n]
-        _, dcoeffs = _bwd1(vp, rp, n, g, gt, prob, dots, tc, coeffs_c, prior_c, drp, True, wz, n_tok, n_tok, d,
+        _, dcoeffs = _bwd1(stack.src(n, g), n, g, gt, prob, dots, tc, coeffs_c, prior_c, True, wz, n_tok, n_tok, d,
                            _dtype_code(stack.V.dtype), dev, cols=n - 1, lam=ctx.lam, g_prop=g_prop, g_h0=g_h0,
                            beta=ctx.beta, part=stack.dq_parts[:, step - 1, :])
         stack.dq_rows.add(step - 1)
@@ -758,8 +847,12 @@ class FusedCombineStk(torch.autograd.Function):
             if step == min(stack.h0_steps):   # every other iteration end ran its backward: their sum, once
                 gs = [stack.h0_g[k] for k in sorted(stack.h0_g)]
                 dh0 = torch.empty_like(g)
-                _run("blend_sum", L.u64_array(x.data_ptr() for x in gs), len(gs), ctx.beta, _p(dh0), n_tok, d,
-                     _dtype_code(stack.V.dtype), _stream(dev))
+                tail = (len(gs), ctx.beta, _p(dh0), n_tok, d, _dtype_code(stack.V.dtype), _stream(dev))
+                if stack.fast_d and _fast(d, len(gs), dh0, *gs):
+                    _run("blend_sum", L.u64_array(x.data_ptr() for x in gs), *tail)
+                else:
+                    gt_ = _dev_addrs((x.data_ptr() for x in gs), dev)
+                    _run("blend_sum_any", gt_.data_ptr(), *tail)
                 stack.h0_g, stack.h0_steps = {}, []
                 dh0 = dh0.view(ctx.shape)
         grads = (None, None, dquery, dprop, dh0,

@@ -89,7 +89,7 @@ def test_chain_matches_oracle(monkeypatch, K, R, dtype, mode, glue):
 @pytest.mark.parametrize("K,R,d,t", [(8, 8, 64, 33), (2, 2, 8192, 20), (1, 3, 8, 5), (2, 2, 64, 40001)])
 @pytest.mark.parametrize("glue", ["1", "0"])
 def test_stack_extremes_match_oracle(monkeypatch, K, R, d, t, glue):
-    """The stacked layout at its limits in fp32: 64 steps (the most a stack holds; reads of up to 64 sources),
+    """The stacked layout at the row-layout kernels' limits in fp32: 64 steps (reads of up to 64 sources),
     the widest row, the narrowest row with one token per tile row, and a ragged 40001 tokens (several tiles per
     workgroup of the grid-capped kernels); glue as in test_chain_matches_oracle. Against the exact (fp64) chain:
     norm-relative and max-abs / RMS <= 1e-5, final state and every gradient."""
@@ -452,7 +452,7 @@ def test_misuse_raises():
     """The reference module's RuntimeError cases (fused_dattn.py:371, 714, 733-734) and this build's limits, each
     raised before any launch: a stacked read whose base is not the stack's dtype or is not contiguous; a scale's
     backward before any read's; accumulating list reads run backward out of order (a source without a buffer); an
-    rstd input of an unsupported dtype; a list read of a width the kernels do not take."""
+    rstd input of an unsupported dtype; a list read whose sources differ in dtype (the gate's refusal)."""
     from loopback_amd import fused_dattn as FD
     d, t, n = 64, 8, 2
     stack = FD.DattnStack(3, (1, t, d), torch.bfloat16, DEV)
@@ -489,11 +489,11 @@ def test_misuse_raises():
 
     with pytest.raises(RuntimeError, match="float64"):
         FD.rstd(torch.randn(1, t, d, device=DEV, dtype=torch.float64), 1e-6)
-    odd = [torch.randn(1, t, 12, device=DEV) for _ in range(2)]
+    mixed = [torch.randn(1, t, d, device=DEV), torch.randn(1, t, d, device=DEV, dtype=torch.bfloat16)]
     with pytest.raises(RuntimeError, match="unsupported"):
-        FD.FusedDattnRead.apply(torch.zeros(12, device=DEV), torch.randn(1, t, 12, device=DEV),
-                                torch.ones(1, t, 2, device=DEV), torch.ones(2, device=DEV), *odd,
-                                *[FD.rstd(x, 1e-6) for x in odd])
+        FD.FusedDattnRead.apply(torch.zeros(d, device=DEV), torch.randn(1, t, d, device=DEV),
+                                torch.ones(1, t, 2, device=DEV), torch.ones(2, device=DEV), *mixed,
+                                *[FD.rstd(x, 1e-6) for x in mixed])
 
 
 @pytest.mark.parametrize("mode", ["list", "stack", "scores"])

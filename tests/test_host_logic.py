@@ -34,12 +34,15 @@ def test_rstd_refuses_cpu_tensors():
 
 
 def test_stack_refuses_cpu_and_bad_shapes():
-    with pytest.raises(RuntimeError):
+    """Any width >= 1 and up to ANY_MAX_SOURCES steps are shapes the stack takes (on a GPU); a CPU device, no
+    width, no steps or more steps than the kernels take are refused."""
+    with pytest.raises(RuntimeError, match="GPU"):
         FD.DattnStack(4, (1, 8, 64), torch.bfloat16, "cpu")
-    with pytest.raises(RuntimeError):
-        FD.DattnStack(4, (1, 8, 60), torch.bfloat16, "cpu")
-    with pytest.raises(RuntimeError):
-        FD.DattnStack(65, (1, 8, 64), torch.bfloat16, "cpu")
+    with pytest.raises(RuntimeError, match="GPU"):
+        FD.DattnStack(70, (1, 8, 60), torch.bfloat16, "cpu")
+    for steps, d in ((4, 0), (0, 64), (FD.ANY_MAX_SOURCES + 1, 64)):
+        with pytest.raises(RuntimeError, match="unsupported shape"):
+            FD.DattnStack(steps, (1, 8, d), torch.bfloat16, "cpu")
 
 
 def test_pair_rows_cover_the_triangle():

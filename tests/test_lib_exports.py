@@ -153,3 +153,32 @@ def test_argument_checks_before_launch(lib):
                              0, 64, 1, null) == 0
     assert L.ldr_read_bwd1(nulls, nulls, 2, null, null, null, null, 0, null, null, 2, p, 2, 1.0, 0.125, null, 2,
                            nulls, 0, null, 0, p, 64, null, null, 0.0, 0, 64, 1, null) == 0
+
+
+def test_any_shape_argument_checks_before_launch(lib):
+    """The any-shape entry points take any width >= 1 and up to LDR_ANY_MAX_SOURCES sources at element alignment,
+    and refuse the rest before any launch (their device address arrays are not read on the host)."""
+    L = lib.LIB
+    null = None
+    p = 4096                         # a stand-in address: every call below is refused or has no tokens
+    odd = 4097                       # not element-aligned for bf16
+    many = lib.ANY_MAX_SOURCES + 1
+    rd = lambda n, d, base=p, tab=p, n_tok=16, cols=None: L.ldr_read_fwd_any(
+        tab, tab, n, p, p, 16, base, null, 0.0, p, n if cols is None else cols, p, n if cols is None else cols, 1.0,
+        0.1, p, p, p, null, n_tok, d, 1, null)
+    assert rd(0, 64) == -2 and rd(many, 64) == -2 and rd(2, 0) == -2
+    assert rd(2, 64, tab=null) == -1 and rd(2, 64, cols=5) == -1
+    assert rd(2, 64, base=odd) == -3
+    assert rd(70, 100, n_tok=0) == 0 and rd(3, 8200, n_tok=0) == 0 and rd(2, 1, n_tok=0) == 0
+    b1 = lambda n, parts=4, wz=p, g=p: L.ldr_read_bwd1_any(
+        p, p, n, g, null, p, p, 16, p, p, n, p, n, 1.0, 0.1, p, n, p, 0, wz, 16, p, parts, 100, null, null, 0.0, 16,
+        100, 1, null)
+    assert b1(many) == -2 and b1(2, parts=0) == -1 and b1(2, wz=4100) == -3 and b1(2, g=odd) == -3
+    dv = lambda m, d=100, v=p: L.ldr_dv_assemble_any(p, p, p, m, v, p, null, null, 0.0, p, null, 16, d, 1, null)
+    assert dv(many) == -2 and dv(2, d=0) == -2 and dv(2, v=odd) == -3
+    assert L.ldr_dv_assemble_any(null, null, null, 2, p, p, null, null, 0.0, p, null, 16, 100, 1, null) == -1
+    assert L.ldr_read_bwd2_list_any(p, many, 0, p, p, p, 16, 16, 100, 1, null) == -2
+    assert L.ldr_read_bwd2_list_any(p, 2, 2, p, p, p, 16, 16, 100, 1, null) == -1
+    assert L.ldr_blend_sum_any(p, 0, 0.5, p, 16, 100, 1, null) == -2
+    assert L.ldr_blend_sum_any(p, 2, 0.5, odd, 16, 100, 1, null) == -3
+    assert L.ldr_blend_sum_any(p, 2, 0.5, p, 0, 100, 1, null) == 0
