@@ -164,7 +164,8 @@ def make_cell(cfg: ChainConfig, Q) -> LoopDeltaAttnRes:
 
 def run_chain(cfg: ChainConfig, h0, D, Q, G, mode: str, grad: bool | None = None, cell=None):
     """One pass of the chain through the HIP read in `mode` ('scores', 'stack' or 'list'). Returns
-    (h_final, loss, grads) with grads = {'h0', 'D': [...], 'query'} when grad (default cfg.backward). `cell` (from
+    (h_final, loss, grads) with grads = {'h0', 'D': [...], 'query'} when grad (default cfg.backward); without grad
+    the pass is the forward alone (a forward-only configuration has no loss: loss and grads are None). `cell` (from
     make_cell) is reused across passes, as a training loop keeps its model: its query gradient is reset each pass;
     without one, a cell is made from Q."""
     grad = cfg.backward if grad is None else grad
@@ -176,9 +177,9 @@ def run_chain(cfg: ChainConfig, h0, D, Q, G, mode: str, grad: bool | None = None
     D = [x.detach().requires_grad_(grad) for x in D]
     with torch.set_grad_enabled(grad):
         h = chain_forward(cell, h0, D, cfg.K, mode)
-        loss = (h.float() * G).sum()
-        grads = None
+        loss = grads = None
         if grad:
+            loss = (h.float() * G).sum()
             loss.backward()
             grads = {"h0": h0.grad, "D": [x.grad for x in D], "query": cell.query.grad}
-    return h.detach(), loss.detach(), grads
+    return h.detach(), None if loss is None else loss.detach(), grads
