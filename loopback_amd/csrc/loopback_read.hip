@@ -29,6 +29,18 @@
 #ifndef LDR_RF_STAGE
 #define LDR_RF_STAGE 65536   // read forward: LDS bytes for a tile's output rows (0: rows stored as they finish)
 #endif
+#ifndef LDR_RF_TT
+#define LDR_RF_TT 16         // read forward: tokens per tile (more when a workgroup holds more rows side by side)
+#endif
+#ifndef LDR_RF_BIG
+#define LDR_RF_BIG 1         // read forward: 512-lane workgroups with 32-token tiles, their output staged in 128 KiB of
+#endif                       // LDS and written as one burst, one workgroup per CU (when the tile's rows fit)
+#ifndef LDR_RF_BIG_MIN_ROW_BYTES
+#define LDR_RF_BIG_MIN_ROW_BYTES 28672   // read forward: fewest bytes read and written per token ((n + 2) rows) for the
+#endif                                   // 512-lane launch, whose fixed cost is higher (7 rows of 2048 bf16)
+#ifndef LDR_RF_BIG_GRID
+#define LDR_RF_BIG_GRID 256  // read forward, 512-lane workgroups: one per CU, each takes tiles in turn
+#endif
 #ifndef LDR_RF_STAGE_U
 #define LDR_RF_STAGE_U 6     // read forward with staged output: sources loaded per batch (the registers of 8 leave
 #endif                       // one wave per SIMD beside the staging code)
@@ -103,6 +115,9 @@ constexpr int SP = MAXS + 1;            // padded LDS row of per-source scalars
 static_assert(LDR_RF_UNROLL >= 1 && LDR_RF_STAGE_U >= 1 && LDR_RF_UNROLL <= 8 && LDR_RF_STAGE_U <= 8,
               "read forward: 1..8 sources per batch");
 static_assert(LDR_RF_STAGE >= 0, "read forward: staging bytes must be >= 0");
+static_assert(LDR_RF_TT >= 1 && LDR_RF_TT <= TT_MAX, "read forward: 1..32 tokens per tile (the LDS planes' rows)");
+static_assert(LDR_RF_BIG == 0 || LDR_RF_BIG == 1, "read forward: LDR_RF_BIG is 0 or 1");
+static_assert(LDR_RF_BIG_MIN_ROW_BYTES >= 0, "read forward: LDR_RF_BIG_MIN_ROW_BYTES >= 0");
 static_assert(LDR_RF_MAX_VPT >= 1 && LDR_RF_MAX_VPT <= 4 && LDR_AS_MAX_VPT >= 1 && LDR_AS_MAX_VPT <= 4 &&
               LDR_B1_MAX_VPT >= 1 && LDR_B1_MAX_VPT <= 4, "vectors per lane: 1..4 (the kernels' instantiations)");
 static_assert(LDR_RF_VPT >= 0 && LDR_RF_VPT <= 4 && LDR_AS_VPT >= 0 && LDR_AS_VPT <= 4 && LDR_B1_VPT >= 0 &&
@@ -110,7 +125,8 @@ static_assert(LDR_RF_VPT >= 0 && LDR_RF_VPT <= 4 && LDR_AS_VPT >= 0 && LDR_AS_VP
 static_assert(LDR_AS_RB >= 1 && LDR_AS_JB >= 1, "update gradient: at least one row per lane and one read per batch");
 static_assert(LDR_B1_C >= 0 && LDR_B1_C <= 8, "backward pass 1: 0 (by vectors per lane) or 1..8 sources per chunk");
 static_assert(LDR_ON_PD >= 1 && LDR_ON_WAVES >= 1, "online read: at least one source in flight, one wave per SIMD");
-static_assert(LDR_AS_GRID >= 1 && LDR_RF_GRID >= 1 && LDR_ON_GRID >= 1 && LDR_B1_GRID >= 1, "grids: >= 1 workgroup");
+static_assert(LDR_AS_GRID >= 1 && LDR_RF_GRID >= 1 && LDR_ON_GRID >= 1 && LDR_B1_GRID >= 1 && LDR_RF_BIG_GRID >= 1,
+              "grids: >= 1 workgroup");
 
 typedef uint16_t bf16_t;                // bf16 storage (raw bits)
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -213,8 +229,8 @@ __device__ __forceinline__ void load_f32x8(const float* p, float (&o)[8]) { IO<f
 // ---------------------------------------------------------------------------------------------------------------
 struct Rows {
   int d8, tpr, rpw, rs, lr;
-  __device__ __forceinline__ Rows(int d, int tpr_)
-      : d8(d >> 3), tpr(tpr_), rpw(WG / tpr_), rs((int)threadIdx.x / tpr_), lr((int)threadIdx.x % tpr_) {}
+  __device__ __forceinline__ Rows(int d, int tpr_, int block = WG)
+      : d8(d >> 3), tpr(tpr_), rpw(block / tpr_), rs((int)threadIdx.x / tpr_), lr((int)threadIdx.x % tpr_) {}
   __device__ __forceinline__ int c8(int v) const { return lr + v * tpr; }
   __device__ __forceinline__ bool act(int v) const { return c8(v) < d8; }
   // element offset of vector v inside a row, clamped to the row for lanes past its end: loads stay unconditional
@@ -1033,8 +1049,11 @@ __global__ __launch_bounds__(WG) void k_dots(SrcTab src, int n, const float* __r
 // come once per tile instead of once per row (a stream probe: 6.3 TB/s with 64 KiB bursts against 5.6 TB/s with
 // each row written after its reads).
 // ---------------------------------------------------------------------------------------------------------------
-template <typename T, int VPT, bool BLEND, bool STAGE>
-__global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float* __restrict__ dots, int64_t dots_stride,
+// big-tile launch: workgroups of RF_BIG_LANES lanes, tiles of RF_BIG_TT tokens staged in RF_BIG_STAGE bytes
+constexpr int RF_BIG_LANES = 512, RF_BIG_TT = 32, RF_BIG_STAGE = 131072;
+
+template <typename T, int VPT, bool BLEND, bool STAGE, int NTH = WG>
+__global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float* __restrict__ dots, int64_t dots_stride,
                                                  const T* __restrict__ base, const T* __restrict__ h0, float beta,
                                                  Coef cf, float inv, T* __restrict__ out, float* __restrict__ tc,
                                                  float* __restrict__ prob, float* __restrict__ next_prior,
@@ -1042,17 +1061,18 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
                                                  int tt) {
   // the logits [i][t] during a tile's prologue; with STAGE, then the tile's output rows, written out together at
   // its end (the launch picks STAGE when the tile's rows fit)
-  constexpr int SL = MAXS * (TT_MAX + 1), SB = STAGE && RF_STAGE_BYTES / 4 > SL ? RF_STAGE_BYTES / 4 : SL;
+  constexpr int STAGE_BYTES = NTH > WG ? RF_BIG_STAGE : RF_STAGE_BYTES;
+  constexpr int SL = MAXS * (TT_MAX + 1), SB = STAGE && STAGE_BYTES / 4 > SL ? STAGE_BYTES / 4 : SL;
   __shared__ __align__(16) float s_big[SB];
   float* s_l = s_big;
   __shared__ float s_w[TT_MAX * SP];           // cbar, then the weights [t][i]
   __shared__ float s_c0[MAXS], s_lc[MAXS], s_p0[MAXS], s_M;
-  const Rows R(d, tpr);
+  const Rows R(d, tpr, NTH);
   const int tid = (int)threadIdx.x;
   load_prior(cf, n, s_c0, s_lc, &s_M);
   const float M = s_M;
   if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
-  const int lpt = WG / tt;   // lanes per token in the softmax
+  const int lpt = NTH / tt;   // lanes per token in the softmax
   const int ns = (n + lpt - 1) / lpt;
   if (tid < lpt) {   // p0 = softmax(lc), a per-read constant: once, by the lanes of one token
     float p0[8];
@@ -1071,14 +1091,14 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
   const int64_t tiles = (n_tok + tt - 1) / tt;
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int64_t t0 = tile * tt;
-    for (int idx = tid; idx < n * tt; idx += WG) {   // source-major: coalesced over tokens
+    for (int idx = tid; idx < n * tt; idx += NTH) {   // source-major: coalesced over tokens
       const int i = idx / tt, t = idx - i * tt;
       const int64_t tok = t0 + t;
       float l = s_lc[i];
       if (tok < n_tok) l = dots[(int64_t)i * dots_stride + tok] * src.r[i][tok] * inv + s_lc[i];
       s_l[i * (TT_MAX + 1) + t] = l;
     }
-    for (int idx = tid; idx < n * tt; idx += WG) {   // token-major: coalesced over [tok][i]
+    for (int idx = tid; idx < n * tt; idx += NTH) {   // token-major: coalesced over [tok][i]
       const int t = idx / n, i = idx - t * n;
       const int64_t tok = t0 + t;
       s_w[t * SP + i] = tok < n_tok ? coef_cbar(cf, tok, i) : 0.f;
@@ -1148,14 +1168,16 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
           }
         }
       }
-      if (U > 4 && i + 4 <= n) {
-        Raw raw[4][VPT];
+      // the rest (fewer than U sources) in batches of 4, 2 and 1, each batch's loads in flight together
+      auto batch = [&](auto nb_tag) {
+        constexpr int NB = decltype(nb_tag)::value;
+        Raw raw[NB][VPT];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < NB; ++u)
 #pragma unroll
           for (int v = 0; v < VPT; ++v) raw[u][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i + u]) + roff + R.off(v));
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < NB; ++u) {
           const float w = wrow[i + u];
 #pragma unroll
           for (int v = 0; v < VPT; ++v) {
@@ -1165,18 +1187,11 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
             for (int k = 0; k < 8; ++k) acc[v][k] += w * e[k];
           }
         }
-        i += 4;
-      }
-      for (; i < n; ++i) {
-        const float w = wrow[i];
-#pragma unroll
-        for (int v = 0; v < VPT; ++v) {
-          float e[8];
-          IO<T>::load(static_cast<const T*>(src.v[i]) + roff + R.off(v), e);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) acc[v][k] += w * e[k];
-        }
-      }
+        i += NB;
+      };
+      if (U > 4 && i + 4 <= n) batch(std::integral_constant<int, 4>());
+      if (U > 2 && i + 2 <= n) batch(std::integral_constant<int, 2>());
+      if (i < n) batch(std::integral_constant<int, 1>());
 #pragma unroll
       for (int v = 0; v < VPT; ++v)
         if (R.act(v))
@@ -1188,7 +1203,7 @@ __global__ __launch_bounds__(WG) void k_read_fwd(SrcTab src, int n, const float*
       const int64_t nv = rows * d * (int64_t)sizeof(T) / 16;
       const uint4* src4 = reinterpret_cast<const uint4*>(s_big);
       uint4* dst4 = reinterpret_cast<uint4*>(out + t0 * (int64_t)d);
-      for (int64_t e = tid; e < nv; e += WG) dst4[e] = src4[e];
+      for (int64_t e = tid; e < nv; e += NTH) dst4[e] = src4[e];
     }
     __syncthreads();
   }
@@ -2145,6 +2160,7 @@ inline int tile_tokens(int tpr) { const int rpw = WG / tpr; return rpw > 16 ? rp
 static_assert(LDR_B1_TT >= 1 && LDR_B1_TT <= TT_MAX && (LDR_B1_TT & (LDR_B1_TT - 1)) == 0,
               "backward pass 1: tokens per tile must be a power of two <= 32");
 inline int b1_tile(int tpr) { const int t = tile_tokens(tpr); return t > LDR_B1_TT ? t : LDR_B1_TT; }
+inline int rf_tile(int tpr) { const int t = tile_tokens(tpr); return t > LDR_RF_TT ? t : LDR_RF_TT; }
 
 int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n, int64_t n_tok) {
   if (!v || n < 1 || n > MAXS) return LDR_E_ARG;
@@ -2408,26 +2424,36 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
   if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, true, LDR_RF_VPT))) return e;
   if (n_tok == 0 && !next_prior) return LDR_OK;
   const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
-  const int tt = tile_tokens(tpr);
-  const unsigned grid = grid_of(cdiv(n_tok, tt), LDR_RF_GRID);   // no tokens: one workgroup writes next_prior
+  const int64_t row_bytes = d * (int64_t)(dtype == LDR_BF16 ? 2 : 4);
+  // 512-lane workgroups with 32-token tiles whose output (at most 128 KiB) is written as one burst, one workgroup
+  // per CU, whenever the tile's rows fit and the read has enough sources to repay the launch's higher fixed cost;
+  // else 256-lane workgroups, 16-token tiles, 64 KiB bursts when they fit
+  const bool big = LDR_RF_BIG && (n + 2) * row_bytes >= LDR_RF_BIG_MIN_ROW_BYTES && RF_BIG_LANES / tpr <= RF_BIG_TT &&
+                   RF_BIG_TT * row_bytes <= RF_BIG_STAGE;
+  const int tt = big ? RF_BIG_TT : rf_tile(tpr);
+  const unsigned grid = big ? grid_of(cdiv(n_tok, tt), LDR_RF_BIG_GRID)
+                            : grid_of(cdiv(n_tok, tt), LDR_RF_GRID);   // no tokens: one workgroup writes next_prior
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // the tile's output rows staged in LDS and written in one burst when they fit
-  const bool stage = RF_STAGE_BYTES > 0 && (int64_t)tt * d * (dtype == LDR_BF16 ? 2 : 4) <= RF_STAGE_BYTES;
-#define LDR_RF_LAUNCH(BL, SG)                                                                                      \
-  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_fwd<T, VPT, BL, SG>), dim3(grid), dim3(WG), 0, \
-                                                                  st, s, (int)n, dots, dots_stride,                 \
+  const bool stage = big || (RF_STAGE_BYTES > 0 && tt * row_bytes <= RF_STAGE_BYTES);
+#define LDR_RF_LAUNCH(BL, SG, NTH)                                                                                 \
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_read_fwd<T, VPT, BL, SG, NTH>), dim3(grid),       \
+                                                                  dim3(NTH), 0, st, s, (int)n, dots, dots_stride,  \
                                                                   static_cast<const T*>(base),                     \
                                                                   static_cast<const T*>(h0), beta, cf, inv_sqrt_d, \
                                                                   static_cast<T*>(out), tc, p, next_prior, n_tok,  \
                                                                   (int)d, tpr, tt)))
-  if (h0 && stage) {
-    LDR_RF_LAUNCH(true, true);
+  if (big && h0) {
+    LDR_RF_LAUNCH(true, true, RF_BIG_LANES);
+  } else if (big) {
+    LDR_RF_LAUNCH(false, true, RF_BIG_LANES);
+  } else if (h0 && stage) {
+    LDR_RF_LAUNCH(true, true, WG);
   } else if (h0) {
-    LDR_RF_LAUNCH(true, false);
+    LDR_RF_LAUNCH(true, false, WG);
   } else if (stage) {
-    LDR_RF_LAUNCH(false, true);
+    LDR_RF_LAUNCH(false, true, WG);
   } else {
-    LDR_RF_LAUNCH(false, false);
+    LDR_RF_LAUNCH(false, false, WG);
   }
 #undef LDR_RF_LAUNCH
   return launched();

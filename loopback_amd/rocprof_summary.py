@@ -176,14 +176,18 @@ def main(argv=None):
     lines += [f"One pass (the last complete one of the trace): span {span_ms:.2f} ms between pass starts, "
               f"{busy:.2f} ms of kernel time.", "",
               "Algorithmic GB: this build's compulsory rows (bench.py `family_bytes`); survey GB: the reference "
-              "dataflow's rows for the same work (bench.py `survey_bytes`, the bytes of the bench line's roofline), "
-              "each over the family's kernel time, against 8000 GB/s.", "",
+              "dataflow's rows for the same work (bench.py `survey_bytes`), each over the family's kernel time. "
+              "The survey's figure for the update gradient counts the reference's read-modify-written gradient "
+              "stack, bytes this kernel does not move; the last column is the bench line's roofline fraction: the "
+              "survey's bytes where its dataflow is the kernel's, the kernel's own for the update gradient, against "
+              "8000 GB/s.", "",
               "| kernel family | launches | total ms | mean us | algorithmic GB | GB/s | survey GB | GB/s (survey) "
-              "| of peak (survey) |", "|---|---|---|---|---|---|---|---|---|"]
+              "| of peak (roofline bytes) |", "|---|---|---|---|---|---|---|---|---|"]
     for famname, (n, us) in sorted(kt.items(), key=lambda x: -x[1][1]):
         ab, sb = fam_bytes.get(famname), sv_bytes.get(famname)
         cols = [f"{ab / 1e9:.2f}", f"{ab / (us * 1e-6) / 1e9:.0f}"] if ab else ["-", "-"]
-        cols += ([f"{sb / 1e9:.2f}", f"{sb / (us * 1e-6) / 1e9:.0f}", f"{sb / (us * 1e-6) / 1e9 / 8000:.3f}"]
+        rb = ab if famname == "dv_assemble" else sb
+        cols += ([f"{sb / 1e9:.2f}", f"{sb / (us * 1e-6) / 1e9:.0f}", f"{rb / (us * 1e-6) / 1e9 / 8000:.3f}"]
                  if sb else ["-", "-", "-"])
         lines.append(f"| `{famname}` | {n} | {us / 1e3:.3f} | {us / n:.1f} | " + " | ".join(cols) + " |")
     if a.stats:   # rocprofv3's own per-kernel summary over the whole run (warm-up and timed passes)
