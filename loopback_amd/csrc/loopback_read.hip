@@ -53,6 +53,9 @@
 #ifndef LDR_AS_JB
 #define LDR_AS_JB 1          // update gradient: reads whose rows are loaded together
 #endif
+#ifndef LDR_AS_STORES
+#define LDR_AS_STORES 0      // update gradient: bit 0 stores dv through the caches, bit 1 dv_neg (else non-temporal)
+#endif
 #ifndef LDR_AS_MAX_VPT
 #define LDR_AS_MAX_VPT 3
 #endif
@@ -122,6 +125,7 @@ static_assert(LDR_RF_MAX_VPT >= 1 && LDR_RF_MAX_VPT <= 4 && LDR_AS_MAX_VPT >= 1 
               LDR_B1_MAX_VPT >= 1 && LDR_B1_MAX_VPT <= 4, "vectors per lane: 1..4 (the kernels' instantiations)");
 static_assert(LDR_RF_VPT >= 0 && LDR_RF_VPT <= 4 && LDR_AS_VPT >= 0 && LDR_AS_VPT <= 4 && LDR_B1_VPT >= 0 &&
               LDR_B1_VPT <= 4, "fixed vectors per lane: 0 (chosen from d) or 1..4");
+static_assert(LDR_AS_STORES >= 0 && LDR_AS_STORES <= 3, "update gradient: LDR_AS_STORES is 0..3");
 static_assert(LDR_AS_RB >= 1 && LDR_AS_JB >= 1, "update gradient: at least one row per lane and one read per batch");
 static_assert(LDR_B1_C >= 0 && LDR_B1_C <= 8, "backward pass 1: 0 (by vectors per lane) or 1..8 sources per chunk");
 static_assert(LDR_ON_PD >= 1 && LDR_ON_WAVES >= 1, "online read: at least one source in flight, one wave per SIMD");
@@ -181,7 +185,13 @@ template <> struct IO<bf16_t> {
     const u32x4 u{pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7])};
     __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(p));
   }
-  // stores -o (rounded), non-temporal: the sign bits of the rounded values flipped, exact
+  // stores -o (rounded): the sign bits of the rounded values flipped, exact (cached, and non-temporal)
+  static __device__ __forceinline__ void store_neg(bf16_t* p, const float (&o)[8]) {
+    uint4 u;
+    u.x = pack2(o[0], o[1]) ^ 0x80008000u; u.y = pack2(o[2], o[3]) ^ 0x80008000u;
+    u.z = pack2(o[4], o[5]) ^ 0x80008000u; u.w = pack2(o[6], o[7]) ^ 0x80008000u;
+    *reinterpret_cast<uint4*>(p) = u;
+  }
   static __device__ __forceinline__ void store_neg_nt(bf16_t* p, const float (&o)[8]) {
     const u32x4 u{pack2(o[0], o[1]) ^ 0x80008000u, pack2(o[2], o[3]) ^ 0x80008000u,
                   pack2(o[4], o[5]) ^ 0x80008000u, pack2(o[6], o[7]) ^ 0x80008000u};
@@ -210,6 +220,10 @@ template <> struct IO<float> {
                                       __float_as_uint(o[3])}, reinterpret_cast<u32x4*>(p));
     __builtin_nontemporal_store(u32x4{__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]),
                                       __float_as_uint(o[7])}, reinterpret_cast<u32x4*>(p) + 1);
+  }
+  static __device__ __forceinline__ void store_neg(float* p, const float (&o)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(-o[0], -o[1], -o[2], -o[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(-o[4], -o[5], -o[6], -o[7]);
   }
   static __device__ __forceinline__ void store_neg_nt(float* p, const float (&o)[8]) {
     __builtin_nontemporal_store(u32x4{__float_as_uint(o[0]) ^ 0x80000000u, __float_as_uint(o[1]) ^ 0x80000000u,
@@ -1837,12 +1851,16 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 #pragma unroll
         for (int x = 0; x < 8; ++x) acc[k][v][x] = __builtin_fmaf(c, e[v][x], acc[k][v][x]);
         if (tok[k] < n_tok && R.act(v)) {
-          if (dv_neg) IO<T>::store_neg_nt(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
+          if (dv_neg) {
+            if (LDR_AS_STORES & 2) IO<T>::store_neg(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
+            else IO<T>::store_neg_nt(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
+          }
           if (add) {
 #pragma unroll
             for (int x = 0; x < 8; ++x) acc[k][v][x] = IO<T>::round(acc[k][v][x]) + a[v][x];
           }
-          IO<T>::store_nt(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
+          if (LDR_AS_STORES & 1) IO<T>::store(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
+          else IO<T>::store_nt(dv + roff[k] + R.c8(v) * 8, acc[k][v]);
         }
       }
     }
