@@ -287,8 +287,8 @@ def _forward_impl(ctx, q, base, cbar, c0, srcs):
 def _bwd1(src: _Src, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_accum, wz, wz_stride, n_tok, d,
           dtype, dev, cols=None, lam=1.0, g_prop=None, g_h0=None, beta=0.0, dq=None, part=None):
     """Pass 1 of the backward plus the dq reduction; returns (dq fp32, dcbar [n_tok, cols]). src: the sources with the
-    scale gradients' addresses (src.dr), on the row-layout kernel when src.fast (and g, g_prop, g_h0 are 16-byte
-    aligned), else on the any-shape kernel. prob and dots are the
+    scale gradients' addresses (src.dr), on the row-layout kernel when src.fast (chosen with g among its rows;
+    g_prop and g_h0 are fresh, aligned allocations), else on the any-shape kernel. prob and dots are the
     forward's probabilities [n_tok, n] and raw scores [n, >= n_tok] (row stride dots.stride(0)). cols = n: cbar_c and c0c
     are the read's own; cols = n - 1: they are the previous read's coefficients and prior (scaled by lam, the newest
     entry implied) and dcbar is the gradient of those coefficients. g_prop / g_h0 receive the iteration-end blend's
@@ -305,7 +305,9 @@ def _bwd1(src: _Src, n, g, gt, prob, dots, tc, cbar_c, c0c, dr_accum, wz, wz_str
     head = (v, r, n, _p(g), _p(gt_c), _p(prob), _p(dots), dots.stride(0), _p(tc), _p(cbar_c), cols, _p(c0c), cols,
             float(lam), _inv_sqrt(d), _p(dcbar), cols, src.dr_ptr(), int(dr_accum), _p(wz), wz_stride, _p(dq_part))
     tail = (_p(g_prop), _p(g_h0), float(beta), n_tok, d, dtype, st)
-    if src.fast and _fast(d, n, g, g_prop, g_h0):
+    if src.fast:
+        if not _fast(d, n, g, g_prop, g_h0):   # the caller chose src with g among its rows
+            raise RuntimeError("delta_attnres HIP read: host source tables with rows the row-layout kernels refuse")
         _run("read_bwd1", *head, dq_part.stride(0), *tail)
     else:
         _run("read_bwd1_any", *head, parts, dq_part.stride(0), *tail)
