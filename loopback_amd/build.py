@@ -22,9 +22,11 @@ ROOT = os.path.dirname(HERE)
 SRC = os.path.join(HERE, "csrc", "loopback_read.hip")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libloopback_read.so")
-# A test fixture: the same source built with the write's matrix-core layout for every width (LDR_WM_ROWS=0), so the
-# GPU tests can check that the whole-row write kernel gives the matrix-core kernel's bits. Nothing else loads it.
-TEST_LIB_MFMA_WRITE = os.path.join(HERE, "libloopback_read_mfma_write.so")
+# A test fixture: the same source built with the alternative kernel shapes -- the write in the matrix cores' layout
+# for every width (LDR_WM_ROWS=0), the read forward in 256-lane workgroups for every read (LDR_RF_BIG=0) -- so the
+# GPU tests can check that the shapes the product library picks give the same bits. Nothing else loads it.
+TEST_LIB_ALT = os.path.join(HERE, "libloopback_read_alt_shapes.so")
+ALT_DEFINES = ["LDR_WM_ROWS=0", "LDR_RF_BIG=0"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code (plain fp32 VALU instead).
@@ -68,10 +70,10 @@ def _finish(job) -> None:
 
 def build(verbose: bool = True, defines=None) -> str:
     """Compile the library (always; a stale build never survives a call) and, beside it, the test fixture
-    TEST_LIB_MFMA_WRITE (the two compiles run in parallel); returns the library's path.
+    TEST_LIB_ALT (the two compiles run in parallel); returns the library's path.
     defines: NAME=VALUE launch settings (see the module docstring)."""
     jobs = [_start(SRC, LIB, verbose, defines),
-            _start(SRC, TEST_LIB_MFMA_WRITE, verbose, list(defines or []) + ["LDR_WM_ROWS=0"])]
+            _start(SRC, TEST_LIB_ALT, verbose, list(defines or []) + ALT_DEFINES)]
     for job in jobs:
         _finish(job)
     return LIB
