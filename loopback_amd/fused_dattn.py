@@ -116,7 +116,11 @@ def _fast(d: int, n: int, *rows) -> bool:
 
 def _dev_addrs(addrs, dev: torch.device) -> torch.Tensor:
     """A device array of addresses for an any-shape entry point, copied on the current stream from pinned host
-    memory (torch keeps the host buffer until the copy has run; the device array is freed in stream order)."""
+    memory (torch keeps the host buffer until the copy has run; the device array is freed in stream order). Not
+    under HIP graph capture: a replay would copy from a host buffer torch may since have reused."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("delta_attnres HIP read: shapes the row-layout kernels do not take (d not a multiple of 8 "
+                           "or above 8192, more than 64 sources, unaligned rows) cannot be captured in a HIP graph")
     host = torch.tensor(list(addrs), dtype=torch.int64).pin_memory()
     return host.to(dev, non_blocking=True)
 

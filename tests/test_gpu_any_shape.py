@@ -262,3 +262,23 @@ def test_entry_points_agree_with_row_layout(dtype):
         torch.cuda.synchronize()
         sums.append(out)
     assert torch.equal(sums[0], sums[1])
+
+
+def test_any_shape_refuses_graph_capture():
+    """The any-shape path copies its address tables from host memory on the launch stream; under HIP graph capture
+    it raises instead (a replay would read a host buffer torch may have reused), and nothing is launched."""
+    from loopback_amd.cell import LoopDeltaAttnRes
+    d, n = 36, 3
+    cell = LoopDeltaAttnRes(d, num_loops=2, num_blocks=n + 1, beta=0.75, eps=1e-6).to(DEV)
+    xs = [torch.randn(1, 8, d, device=DEV) for _ in range(n)]
+    prop, h0 = torch.randn(1, 8, d, device=DEV), torch.randn(1, 8, d, device=DEV)
+    coeffs, prior = torch.ones(1, 8, n - 1, device=DEV), torch.ones(n - 1, device=DEV)
+    print("case any-shape under capture", flush=True)
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with pytest.raises(RuntimeError, match="HIP graph"):
+            with torch.cuda.graph(graph, stream=side):
+                cell.combine(prop, h0, xs, coeffs, prior, 0, n - 1)
+    torch.cuda.synchronize()
