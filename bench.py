@@ -404,6 +404,15 @@ def main():
                                          "unit": "read-tokens/s", "backward": c.backward,
                                          "formula_wall_gbs": rb / (ms * 1e-3) / 1e9,
                                          "formula_wall_frac": rb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        # config 2 runs both score modes: the table stored at the write (above) and the reads forming the scores
+        # as they stream (LOOP_DATTN_DOTS=0, the stack without a score table)
+        c = CONFIGS["c2"]
+        _, rb = family_bytes(c, "stack")
+        el = time_chain(c, "stack", 20, 5)[0]
+        extra["c2_dots_off_eager"] = {"workload": c.name + " DOTS off", "ms_per_step": 1e3 * el / 20,
+                                      "value": c.n_tok * 20 / el, "unit": "read-tokens/s", "backward": False,
+                                      "formula_wall_gbs": rb / (el / 20) / 1e9,
+                                      "formula_wall_frac": rb / (el / 20) / 1e9 / HBM_PEAK_GBS}
         from loopback_amd import lm
         for key, residual in (("c5_lm", "delta_attnres"), ("c5_lm_plain_loop", "none")):
             rec = lm.time_training(10, 3, residual=residual)
