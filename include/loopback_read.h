@@ -188,11 +188,16 @@ int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, 
  * gradient of the write's h, e.g. the read that took h as its proposal) dv holds round(dv + a) instead, the sum
  * autograd would form, with a = add, or, when add_beta != 0 (add being the output gradient g of a read whose base
  * was the iteration-end blend), the blend's share of it a = round(add - round(add_beta * add)); dv_neg stays -dv.
+ * per_read = 1 rounds as the list layout does instead: each read's share round(w_e g_e + dzr_e q_e) (one fused
+ * multiply-add over the rounded product dzr q, as ldr_read_bwd2_list) added to the running gradient in dtype, in
+ * table order, then round(gr (-r^3) / d * v) added last -- autograd's accumulation of the per-read gradients when the
+ * table lists the reads from the last to the first (the reference's stack read-modify-writes dV the same way,
+ * fused_dattn.py:528-531); per_read = 0 (the default) forms one fp32 sum rounded once.
  * Replaces the dV read-modify-write of _dattn_bwd2_stk_kernel (fused_dattn.py:496-536, launched at 781-784) and
  * _rstd_bwd_acc_kernel (539-552, launched at 717-719). */
 int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                    const float* r, const float* gr, const void* add, float add_beta, void* dv, void* dv_neg,
-                    int64_t n_tok, int64_t d, int dtype, void* stream);
+                    const float* r, const float* gr, const void* add, float add_beta, int per_read, void* dv,
+                    void* dv_neg, int64_t n_tok, int64_t d, int dtype, void* stream);
 
 /* out = round( sum_j round(beta * g_j) ) over m update-shaped tensors (fp32 sum): the gradient of h0 from the m
  * iteration-end blends of a pass (looped_transformer.py:380-381, base = proposal + beta (h0 - proposal)), formed
@@ -232,8 +237,8 @@ int ldr_read_bwd1_any(const uint64_t* src_v, const uint64_t* src_r, int64_t n, c
  * same order, so the bits of ldr_dv_assemble for the same tables. Replaces _dattn_bwd2_stk_kernel
  * (fused_dattn.py:496-536) and _rstd_bwd_acc_kernel (539-552) at the shapes ldr_dv_assemble does not take. */
 int ldr_dv_assemble_any(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                        const float* r, const float* gr, const void* add, float add_beta, void* dv, void* dv_neg,
-                        int64_t n_tok, int64_t d, int dtype, void* stream);
+                        const float* r, const float* gr, const void* add, float add_beta, int per_read, void* dv,
+                        void* dv_neg, int64_t n_tok, int64_t d, int dtype, void* stream);
 
 /* ldr_read_bwd2_list for any shape (dv a device array). Replaces pass 2 of _dattn_bwd_kernel (fused_dattn.py:
  * 152-181) at the shapes ldr_read_bwd2_list does not take. */

@@ -7,7 +7,9 @@ stack creation, modeling_looped_transformer.py:437-444):
     LOOP_DATTN_DOTS=1 (default): the stack also stores each update's scores at its write;
   * LOOP_DATTN_STACK=0: the list layout (FusedDattnRead), one tensor per update;
   * LOOP_DATTN_FUSE_GLUE=1 (default, this build's own switch): in the stacked layout the glue below runs inside the
-    read's kernels (FusedCombineStk); 0 keeps it as torch ops.
+    read's kernels (FusedCombineStk); 0 keeps it as torch ops;
+  * LOOP_DATTN_GRAD_ROUNDING=once (default, this build's own switch) or per_read: how the stacked layout rounds the
+    updates' gradients (fused_dattn.grad_rounding).
 The glue around the kernels -- the iteration-end blend base = proposal + beta (h0 - proposal), the coefficient
 bookkeeping (cat, lambda scaling) -- is the reference's, op for op. Unlike the reference, the cell has no PyTorch
 read of its own: an unsupported layout raises instead of falling back (that read lives in oracle/ as the checker).

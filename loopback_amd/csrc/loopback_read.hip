@@ -1694,6 +1694,10 @@ __global__ __launch_bounds__(WG) void k_reduce_rows(const float* __restrict__ pa
   }
 }
 
+// One read's share of a source's gradient, w g + dzr q, with one explicit fused multiply-add (the product dzr q
+// rounded first): the list layout's per-read term, and the stacked layout's when it rounds per read.
+__device__ __forceinline__ float bwd2_term(float w, float g, float dzr, float q) { return __builtin_fmaf(w, g, dzr * q); }
+
 // ---------------------------------------------------------------------------------------------------------------
 // backward pass 2, list layout: dv_i (=|+=) w_i g + dzr_i q
 // ---------------------------------------------------------------------------------------------------------------
@@ -1725,7 +1729,7 @@ __global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, c
       for (int v = 0; v < VPT; ++v) {
         float o[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) o[k] = s.x * gv[v][k] + s.y * qv[v][k];
+        for (int k = 0; k < 8; ++k) o[k] = bwd2_term(s.x, gv[v][k], s.y, qv[v][k]);
         if (accum) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) o[k] = prev[v][k] + IO<T>::round(o[k]);
@@ -1743,7 +1747,11 @@ __global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, c
 constexpr int as_rb(int vpt) { return vpt >= 3 ? 2 : LDR_AS_RB; }
 constexpr int AS_JB = LDR_AS_JB;   // reads per batch of loads
 
-template <typename T, int VPT, bool ADD_LAST>   // ADD_LAST: add is the output gradient of the last read in tab
+// ADD_LAST: add is the output gradient of the last read in tab. PER_READ: each read's share rounded to T and added
+// to the running gradient in T, in table order, then the scale's term rounded and added -- the roundings of the list
+// layout, whose per-read gradients autograd adds in backward order (the host orders the table so) -- instead of one
+// fp32 sum rounded once.
+template <typename T, int VPT, bool ADD_LAST, bool PER_READ>
 __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* __restrict__ vsrc,
                                                     const float* __restrict__ r, const float* __restrict__ gr,
                                                     const T* __restrict__ add, float add_beta,
@@ -1770,6 +1778,7 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
         for (int e = 0; e < 8; ++e) acc[k][v][e] = 0.f;
     // one read's share: w g + dzr q for the tile's rows, as two explicit fused multiply-adds (so every kernel
     // variant and every read accumulate with the same roundings, whatever the compiler would contract)
+    int taken = 0;   // reads added so far (PER_READ: the first share is the running gradient itself)
     auto take_row = [&](const typename IO<T>::Raw (&raw)[AS_RB][VPT], const float2 (&sc)[AS_RB],
                         const float (&qv)[VPT][8]) {
 #pragma unroll
@@ -1779,9 +1788,16 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
           float e[8];
           IO<T>::unpack(raw[k][v], e);
 #pragma unroll
-          for (int x = 0; x < 8; ++x)
-            acc[k][v][x] = __builtin_fmaf(sc[k].y, qv[v][x], __builtin_fmaf(sc[k].x, e[x], acc[k][v][x]));
+          for (int x = 0; x < 8; ++x) {
+            if (PER_READ) {
+              const float t = IO<T>::round(bwd2_term(sc[k].x, e[x], sc[k].y, qv[v][x]));
+              acc[k][v][x] = taken == 0 ? t : IO<T>::round(acc[k][v][x] + t);
+            } else {
+              acc[k][v][x] = __builtin_fmaf(sc[k].y, qv[v][x], __builtin_fmaf(sc[k].x, e[x], acc[k][v][x]));
+            }
+          }
         }
+      ++taken;
     };
     // JB reads per batch: their g rows (and query columns) are all in flight before the first multiply-add
     auto batch = [&](int j0, auto jb_tag) {
@@ -1849,7 +1865,17 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
 #pragma unroll
       for (int v = 0; v < VPT; ++v) {
 #pragma unroll
-        for (int x = 0; x < 8; ++x) acc[k][v][x] = __builtin_fmaf(c, e[v][x], acc[k][v][x]);
+        for (int x = 0; x < 8; ++x) {
+          if (PER_READ) {   // the scale's term as the scale node's backward rounds it, added last
+#pragma clang fp contract(off)   // the product rounded on its own (in fp32 too), as that node stores it
+            if (gr) {
+              const float gx = IO<T>::round(c * e[v][x]);
+              acc[k][v][x] = m == 0 ? gx : IO<T>::round(acc[k][v][x] + gx);
+            }
+          } else {
+            acc[k][v][x] = __builtin_fmaf(c, e[v][x], acc[k][v][x]);
+          }
+        }
         if (tok[k] < n_tok && R.act(v)) {
           if (dv_neg) {
             if (LDR_AS_STORES & 2) IO<T>::store_neg(dv_neg + roff[k] + R.c8(v) * 8, acc[k][v]);
@@ -2061,7 +2087,7 @@ __global__ __launch_bounds__(64) void k_any_bwd1(const uint64_t* __restrict__ tv
 // The update gradient (k_dv_assemble): per element, the reads' shares w g + dzr q in table order as two explicit
 // fused multiply-adds each, the scale's term, then dv_neg = -dv and the added gradient -- the same roundings in the
 // same order as k_dv_assemble, so the same bits for the same table.
-template <typename T>
+template <typename T, bool PER_READ>
 __global__ __launch_bounds__(WG) void k_any_dv_assemble(const uint64_t* __restrict__ tg, const uint64_t* __restrict__ twz,
                                                         const uint64_t* __restrict__ tq, int m,
                                                         const T* __restrict__ vsrc, const float* __restrict__ r,
@@ -2078,9 +2104,23 @@ __global__ __launch_bounds__(WG) void k_any_dv_assemble(const uint64_t* __restri
       for (int j = 0; j < m; ++j) {
         const float2 sc = *reinterpret_cast<const float2*>(reinterpret_cast<const float*>(twz[j]) + 2 * tok);
         const float e = ld1(any_row<T>(tg, j, roff) + k);
-        acc = __builtin_fmaf(sc.y, reinterpret_cast<const float*>(tq[j])[k], __builtin_fmaf(sc.x, e, acc));
+        const float q = reinterpret_cast<const float*>(tq[j])[k];
+        if (PER_READ) {
+          const float t = IO<T>::round(bwd2_term(sc.x, e, sc.y, q));
+          acc = j == 0 ? t : IO<T>::round(acc + t);
+        } else {
+          acc = __builtin_fmaf(sc.y, q, __builtin_fmaf(sc.x, e, acc));
+        }
       }
-      acc = __builtin_fmaf(c, ld1(vsrc + roff + k), acc);
+      if (PER_READ) {
+#pragma clang fp contract(off)
+        if (gr) {
+          const float gx = IO<T>::round(c * ld1(vsrc + roff + k));
+          acc = m == 0 ? gx : IO<T>::round(acc + gx);
+        }
+      } else {
+        acc = __builtin_fmaf(c, ld1(vsrc + roff + k), acc);
+      }
       if (dv_neg) st1(dv_neg + roff + k, -acc);
       if (add) {   // a gradient of the write's h from elsewhere, added as autograd would add it
         float a = ld1(add + roff + k);
@@ -2108,7 +2148,7 @@ __global__ __launch_bounds__(WG) void k_any_bwd2_list(const uint64_t* __restrict
       const float2 s = *reinterpret_cast<const float2*>(wz + 2 * ((int64_t)i * wz_stride + tok));
       T* dvi = reinterpret_cast<T*>(tdv[i]) + roff;
       for (int64_t k = lane; k < d; k += 64) {
-        float o = s.x * ld1(g + roff + k) + s.y * q[k];
+        float o = bwd2_term(s.x, ld1(g + roff + k), s.y, q[k]);
         if (accum) o = ld1(dvi + k) + IO<T>::round(o);
         st1(dvi + k, o);
       }
@@ -2275,7 +2315,7 @@ __global__ __launch_bounds__(WG) void k_zero(float* __restrict__ p, int64_t n) {
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 12; }
+int ldr_abi_version(void) { return 13; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -2643,9 +2683,10 @@ int ldr_read_bwd2_list(const uint64_t* dv, int64_t n, int accum, const void* g, 
 }
 
 int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                    const float* r, const float* gr, const void* add, float add_beta, void* dv, void* dv_neg,
-                    int64_t n_tok, int64_t d, int dtype, void* stream) {
+                    const float* r, const float* gr, const void* add, float add_beta, int per_read, void* dv,
+                    void* dv_neg, int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (per_read != 0 && per_read != 1) return LDR_E_ARG;
   if (m < 0 || m > MAXS) return LDR_E_SHAPE;
   if ((m > 0 && (!g || !wz || !q)) || !tok_ptr(v, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(dv, n_tok) || n_tok < 0)
     return LDR_E_ARG;
@@ -2667,16 +2708,20 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
   // the added gradient is often the last read's output gradient itself (the proposal of that read is this write's
   // h): then its rows are read once
   const bool add_last = add && m > 0 && add == t.g[m - 1];
-#define LDR_AS_LAUNCH(AL)                                                                                         \
-  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT, AL>), dim3(grid), dim3(WG), 0, \
-                                                                  st, t, (int)m, static_cast<const T*>(v), r, gr,  \
+#define LDR_AS_LAUNCH(AL, PR)                                                                                     \
+  LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_dv_assemble<T, VPT, AL, PR>), dim3(grid), dim3(WG),\
+                                                                  0, st, t, (int)m, static_cast<const T*>(v), r, gr, \
                                                                   static_cast<const T*>(add), add_beta,            \
                                                                   static_cast<T*>(dv), static_cast<T*>(dv_neg),    \
                                                                   n_tok, (int)d, tpr)))
-  if (add_last) {
-    LDR_AS_LAUNCH(true)
+  if (add_last && per_read) {
+    LDR_AS_LAUNCH(true, true)
+  } else if (add_last) {
+    LDR_AS_LAUNCH(true, false)
+  } else if (per_read) {
+    LDR_AS_LAUNCH(false, true)
   } else {
-    LDR_AS_LAUNCH(false)
+    LDR_AS_LAUNCH(false, false)
   }
 #undef LDR_AS_LAUNCH
   return launched();
@@ -2752,9 +2797,10 @@ int ldr_read_bwd1_any(const uint64_t* src_v, const uint64_t* src_r, int64_t n, c
 }
 
 int ldr_dv_assemble_any(const uint64_t* g, const uint64_t* wz, const uint64_t* q, int64_t m, const void* v,
-                        const float* r, const float* gr, const void* add, float add_beta, void* dv, void* dv_neg,
-                        int64_t n_tok, int64_t d, int dtype, void* stream) {
+                        const float* r, const float* gr, const void* add, float add_beta, int per_read, void* dv,
+                        void* dv_neg, int64_t n_tok, int64_t d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (per_read != 0 && per_read != 1) return LDR_E_ARG;
   if (m < 0 || m > ANY_MAXS || d < 1) return LDR_E_SHAPE;
   if ((m > 0 && (!g || !wz || !q)) || !tok_ptr(v, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(dv, n_tok) || n_tok < 0)
     return LDR_E_ARG;
@@ -2762,10 +2808,17 @@ int ldr_dv_assemble_any(const uint64_t* g, const uint64_t* wz, const uint64_t* q
     return LDR_E_ALIGN;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_any_dv_assemble<T>), dim3(any_row_grid(n_tok, 8192)), dim3(WG), 0, st,
-                                             g, wz, q, (int)m, static_cast<const T*>(v), r, gr,
-                                             static_cast<const T*>(add), add_beta, static_cast<T*>(dv),
+#define LDR_ANY_AS(PR)                                                                                            \
+  LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_any_dv_assemble<T, PR>), dim3(any_row_grid(n_tok, 8192)), dim3(WG), 0, \
+                                             st, g, wz, q, (int)m, static_cast<const T*>(v), r, gr,                 \
+                                             static_cast<const T*>(add), add_beta, static_cast<T*>(dv),             \
                                              static_cast<T*>(dv_neg), n_tok, d))
+  if (per_read) {
+    LDR_ANY_AS(true)
+  } else {
+    LDR_ANY_AS(false)
+  }
+#undef LDR_ANY_AS
   return launched();
 }
 

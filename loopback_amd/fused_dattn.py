@@ -26,7 +26,10 @@ Layouts:
     backward keeps its output gradient g_s and its per-(source, token) scalars (w, dz r / sqrt(d)); the gradient of
     update i is formed once, when its scale's backward runs (after every read of it), as
     sum_s (w_si g_s + dzr_si q_s) + the scale's term, in fp32 with one rounding. Same gradients, at least as
-    accurate as the per-read bf16 adds, and about a quarter less HBM traffic over a pass;
+    accurate as the per-read bf16 adds, and about a quarter less HBM traffic over a pass. With
+    LOOP_DATTN_GRAD_ROUNDING=per_read the same kernel rounds each read's share and adds them in the update dtype from
+    the last read to the first, then the scale's term: the list layout's gradients bit for bit, as the reference's
+    stack (which read-modify-writes a bf16 gradient stack) promises;
   * FusedCombineStk (this module's extension, no reference counterpart): the stacked read with the caller's glue
     (LoopDeltaAttnRes.combine's iteration-end blend and coefficient bookkeeping) inside the kernels, and the
     gradient hand-offs that spare autograd's own glue (one query gradient per pass, the proposal's gradient added
@@ -35,6 +38,7 @@ Layouts:
 from __future__ import annotations
 
 import ctypes
+import os
 import weakref
 
 import torch
@@ -100,6 +104,16 @@ def _f32(t: torch.Tensor) -> torch.Tensor:
 
 def _inv_sqrt(d: int) -> float:
     return 1.0 / (d ** 0.5)
+
+
+def grad_rounding() -> str:
+    """LOOP_DATTN_GRAD_ROUNDING (this build's switch, read when a stack is made): 'once' (default) forms each update's
+    gradient as one fp32 sum rounded once; 'per_read' rounds each read's share and adds them in the update dtype in
+    the order autograd adds the list layout's per-read gradients, so the stacked gradients are the list layout's."""
+    mode = os.environ.get("LOOP_DATTN_GRAD_ROUNDING", "once")
+    if mode not in ("once", "per_read"):
+        raise ValueError(f"LOOP_DATTN_GRAD_ROUNDING must be 'once' or 'per_read', got {mode!r}")
+    return mode
 
 
 def _fast(d: int, n: int, *rows) -> bool:
@@ -441,7 +455,7 @@ class DattnStack:
     matrix-core product loads them."""
     __slots__ = ("V", "R", "dV", "dR", "n_steps", "n_tok", "d", "eps", "Q", "QT", "QB", "DOTS", "r_done", "WZ", "bwd",
                  "assembled", "neg", "dq_parts", "dq_rows", "wh", "gadd", "h0_ref", "h0_steps", "h0_g", "vptr",
-                 "rptr", "drptr", "wout", "fast_d", "src_fast", "src_any")
+                 "rptr", "drptr", "wout", "fast_d", "src_fast", "src_any", "per_read")
 
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
@@ -456,6 +470,9 @@ class DattnStack:
         # more than MAX_SOURCES sources, run on the any-shape kernels
         self.fast_d = d % 8 == 0 and d <= L.MAX_WIDTH
         self.src_fast = self.src_any = None
+        # the updates' gradients: one fp32 sum rounded once (default), or rounded per read as the list layout's
+        # per-read gradients are when autograd adds them (LOOP_DATTN_GRAD_ROUNDING=per_read: bitwise the list layout)
+        self.per_read = grad_rounding() == "per_read"
         self.V = torch.empty((n_steps, b, t, d), dtype=dtype, device=device)
         self.R = torch.empty((n_steps, b, t, 1), dtype=torch.float32, device=device)
         _require_gpu(self.V, "the stack")
@@ -553,7 +570,9 @@ def _assemble(stack: DattnStack, s: int, gr):
     reads' output gradients and (w, dz r / sqrt(d)) pairs, the scale's gradient gr (dR[s], or None) and, when a read
     took the write's h as its proposal, that read's proposal gradient (added as autograd would add it). Returns
     (dv for the write's h, -dv without the proposal's share for its x, the added (g, beta) or None)."""
-    reads = sorted(k for k in stack.bwd if k >= max(s, 1))     # the reads of update s whose backward ran
+    # the reads of update s whose backward ran; rounding per read, from the last read to the first (the order in which
+    # autograd adds the list layout's per-read gradients), which puts read s last
+    reads = sorted((k for k in stack.bwd if k >= max(s, 1)), reverse=stack.per_read)
     if s in reads:   # read s last: when its output gradient is also the added one, the kernel loads it once
         reads.remove(s)
         reads.append(s)
@@ -573,7 +592,7 @@ def _assemble(stack: DattnStack, s: int, gr):
         wz0, wz_row = stack.WZ.data_ptr(), stack.WZ.stride(0) * stack.WZ.element_size()
         tables = ([bwd[k][2] for k in reads], [wz0 + _pair(k, s) * wz_row for k in reads], [bwd[k][3] for k in reads])
     args = (len(reads), _p(v), _p(stack.R[s]), _p(grc), _p(None if added is None else added[0]),
-            0.0 if added is None else float(added[1]), _p(dv), _p(dv_neg), stack.n_tok, stack.d,
+            0.0 if added is None else float(added[1]), int(stack.per_read), _p(dv), _p(dv_neg), stack.n_tok, stack.d,
             _dtype_code(v.dtype), _stream(v.device))
     if fast:
         _run("dv_assemble", *([L.u64_array(t) for t in tables] if tables else [None] * 3), *args)

@@ -87,7 +87,7 @@ class _Bufs:
             qp = L.u64_array([self.Q[i].data_ptr() for i in range(n)])
             return (lambda: check(lib.ldr_dv_assemble(
                 gp, wp, qp, n, self.V[0].data_ptr(), self.R[0].data_ptr(), self.R[1].data_ptr(),
-                self.G[n - 1].data_ptr(), 0.0, self.dv.data_ptr(), self.dvn.data_ptr(), T, d, L.BF16, st))), n + 3
+                self.G[n - 1].data_ptr(), 0.0, 0, self.dv.data_ptr(), self.dvn.data_ptr(), T, d, L.BF16, st))), n + 3
         raise ValueError(kind)
 
 

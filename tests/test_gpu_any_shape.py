@@ -16,6 +16,8 @@ takes any shape (fused_dattn.py:647-661); these tests hold the same paths to the
      any-shape kernels are bitwise those of the row-layout kernels on the same tables; the read and backward pass 1
      agree with them to fp32 round-off.
 """
+import itertools
+
 import pytest
 import torch
 
@@ -149,8 +151,8 @@ def _dev(vals):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_entry_points_agree_with_row_layout(dtype):
-    """At d = 256, n = 6 (both families take it): ldr_dv_assemble_any and ldr_blend_sum_any give the row-layout
-    kernels' bits; ldr_read_fwd_any (stored and online scores) and ldr_read_bwd1_any agree with ldr_read_fwd /
+    """At d = 256, n = 6 (both families take it): ldr_dv_assemble_any (rounding once and per read) and
+    ldr_blend_sum_any give the row-layout kernels' bits; ldr_read_fwd_any (stored and online scores) and ldr_read_bwd1_any agree with ldr_read_fwd /
     ldr_read_fwd_online / ldr_read_bwd1 within fp32 round-off (max-abs <= 1e-5 x RMS; bf16 outputs 1e-2, one
     rounding), their scalars too, and the blend gradients bitwise."""
     from loopback_amd import _lib as L
@@ -236,12 +238,12 @@ def test_entry_points_agree_with_row_layout(dtype):
     qs = [(torch.randn(d, generator=g_) * 0.3).to(DEV) for _ in range(3)]
     wzp = [wz[i].data_ptr() for i in range(3)]
     gr = torch.randn(T, generator=g_).to(DEV)
-    for add, beta in ((None, 0.0), (gs[2], 0.0), (gs[2], 0.75), (gs[0], 0.0)):
+    for (add, beta), per_read in itertools.product(((None, 0.0), (gs[2], 0.0), (gs[2], 0.75), (gs[0], 0.0)), (0, 1)):
         dvs = {}
         for name in ("fast", "any"):
             dv, dvn = torch.empty_like(V[0]), torch.empty_like(V[0])
             tail = (3, V[1].data_ptr(), R[1].data_ptr(), gr.data_ptr(), None if add is None else add.data_ptr(), beta,
-                    dv.data_ptr(), dvn.data_ptr(), T, d, dt, st)
+                    per_read, dv.data_ptr(), dvn.data_ptr(), T, d, dt, st)
             if name == "fast":
                 check(lib.ldr_dv_assemble(_u64(L, (x.data_ptr() for x in gs)), _u64(L, wzp),
                                           _u64(L, (x.data_ptr() for x in qs)), *tail))

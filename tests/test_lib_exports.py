@@ -100,11 +100,11 @@ def test_argument_checks_before_launch(lib):
     assert L.ldr_query_parts_elems(31, 2048) == 32 * 2 * 3 * 2 * 64 * 8
     assert L.ldr_query_parts_elems(1, 8) == 3 * 2 * 64 * 8 and L.ldr_query_parts_elems(65, 64) == 0
     assert L.ldr_dv_assemble(too_many, too_many, too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), null,
-                             null, 0.0, ctypes.c_void_p(4096), null, 16, 64, 1, null) == -2
+                             null, 0.0, 0, ctypes.c_void_p(4096), null, 16, 64, 1, null) == -2
     # a misaligned added gradient
     assert L.ldr_dv_assemble(one_src := lib.u64_array([4096]), one_src, one_src, 1, ctypes.c_void_p(4096),
-                             ctypes.c_void_p(4096), null, ctypes.c_void_p(4100), 0.0, ctypes.c_void_p(4096), null, 16,
-                             64, 1, null) == -3
+                             ctypes.c_void_p(4096), null, ctypes.c_void_p(4100), 0.0, 0, ctypes.c_void_p(4096), null,
+                             16, 64, 1, null) == -3
     # a misaligned blend-gradient output
     one = lib.u64_array([4096])
     p = ctypes.c_void_p(4096)
@@ -133,7 +133,9 @@ def test_argument_checks_before_launch(lib):
         assert L.ldr_read_fwd_online(two, two, 2, p, p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.01, p, p, p, null, 0,
                                      width, 1, null) == 0
     # the widest row (8192) is a shape every stacked entry point takes (no tokens: checked, nothing launched)
-    assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, p, null, 0, 8192, 1, null) == 0
+    assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, 0, p, null, 0, 8192, 1, null) == 0
+    assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, 1, p, null, 0, 8192, 1, null) == 0
+    assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, 2, p, null, 0, 8192, 1, null) == -1
     assert L.ldr_blend_sum(one, 1, 0.5, p, 0, 8192, 1, null) == 0
     assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.01, p, p, p, null, 0, 8192, 1,
                           null) == 0
@@ -149,8 +151,8 @@ def test_argument_checks_before_launch(lib):
                           null, 0, 64, 1, null) == 0
     assert L.ldr_read_fwd(nulls, nulls, 2, null, 0, null, null, 0.0, null, 2, p, 2, 1.0, 0.125, null, null, null,
                           null, 1, 64, 1, null) == -1
-    assert L.ldr_dv_assemble(lib.u64_array([0]), lib.u64_array([0]), one, 1, null, null, null, null, 0.0, null, null,
-                             0, 64, 1, null) == 0
+    assert L.ldr_dv_assemble(lib.u64_array([0]), lib.u64_array([0]), one, 1, null, null, null, null, 0.0, 0, null,
+                             null, 0, 64, 1, null) == 0
     assert L.ldr_read_bwd1(nulls, nulls, 2, null, null, null, null, 0, null, null, 2, p, 2, 1.0, 0.125, null, 2,
                            nulls, 0, null, 0, p, 64, null, null, 0.0, 0, 64, 1, null) == 0
 
@@ -174,9 +176,10 @@ def test_any_shape_argument_checks_before_launch(lib):
         p, p, n, g, null, p, p, 16, p, p, n, p, n, 1.0, 0.1, p, n, p, 0, wz, 16, p, parts, 100, null, null, 0.0, 16,
         100, 1, null)
     assert b1(many) == -2 and b1(2, parts=0) == -1 and b1(2, wz=4100) == -3 and b1(2, g=odd) == -3
-    dv = lambda m, d=100, v=p: L.ldr_dv_assemble_any(p, p, p, m, v, p, null, null, 0.0, p, null, 16, d, 1, null)
+    dv = lambda m, d=100, v=p: L.ldr_dv_assemble_any(p, p, p, m, v, p, null, null, 0.0, 0, p, null, 16, d, 1, null)
     assert dv(many) == -2 and dv(2, d=0) == -2 and dv(2, v=odd) == -3
-    assert L.ldr_dv_assemble_any(null, null, null, 2, p, p, null, null, 0.0, p, null, 16, 100, 1, null) == -1
+    assert L.ldr_dv_assemble_any(null, null, null, 2, p, p, null, null, 0.0, 0, p, null, 16, 100, 1, null) == -1
+    assert L.ldr_dv_assemble_any(p, p, p, 2, p, p, null, null, 0.0, 3, p, null, 16, 100, 1, null) == -1
     assert L.ldr_read_bwd2_list_any(p, many, 0, p, p, p, 16, 16, 100, 1, null) == -2
     assert L.ldr_read_bwd2_list_any(p, 2, 2, p, p, p, 16, 16, 100, 1, null) == -1
     assert L.ldr_blend_sum_any(p, 0, 0.5, p, 16, 100, 1, null) == -2
