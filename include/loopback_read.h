@@ -201,10 +201,11 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
 
 /* out = round( sum_j round(beta * g_j) ) over m update-shaped tensors (fp32 sum): the gradient of h0 from the m
  * iteration-end blends of a pass (looped_transformer.py:380-381, base = proposal + beta (h0 - proposal)), formed
- * once from the reads' output gradients instead of one tensor per blend added up by autograd. No reference
- * counterpart (the reference leaves these adds to autograd). */
-int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
-                  void* stream);
+ * once from the reads' output gradients instead of one tensor per blend added up by autograd; per_read = 1 adds the
+ * rounded shares in dtype in table order instead, as autograd adds them (list the blends from the last to the
+ * first). No reference counterpart (the reference leaves these adds to autograd). */
+int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, int per_read, void* out, int64_t n_tok, int64_t d,
+                  int dtype, void* stream);
 
 /* ---- any-shape entry points ----------------------------------------------------------------------------------
  * The same computations for the shapes the entry points above reject -- the reference's kernels mask any width
@@ -247,8 +248,8 @@ int ldr_read_bwd2_list_any(const uint64_t* dv, int64_t n, int accum, const void*
 
 /* ldr_blend_sum for any shape (g a device array): the same sum in the same order. No reference counterpart (the
  * reference leaves these adds to autograd, looped_transformer.py:380-381). */
-int ldr_blend_sum_any(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
-                      void* stream);
+int ldr_blend_sum_any(const uint64_t* g, int64_t m, float beta, int per_read, void* out, int64_t n_tok, int64_t d,
+                      int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ import torch  # noqa: F401  -- first: the library must bind to the HIP runtime t
 
 from . import build as _build
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 F32, BF16, F16 = 0, 1, 2   # F16: the scale entry points only
 MAX_SOURCES = 64
 MAX_WIDTH = 8192
@@ -56,7 +56,7 @@ SIGNATURES = {
                                   _c_void_p]),
     "ldr_dv_assemble": (_i32, [_u64p, _u64p, _u64p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _f32, _i32,
                                _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
-    "ldr_blend_sum": (_i32, [_u64p, _i64, _f32, _c_void_p, _i64, _i64, _i32, _c_void_p]),
+    "ldr_blend_sum": (_i32, [_u64p, _i64, _f32, _i32, _c_void_p, _i64, _i64, _i32, _c_void_p]),
     # the any-shape entry points: per-source addresses in device arrays (passed as device addresses)
     "ldr_read_fwd_any": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _f32,
                                 _c_void_p, _i64, _c_void_p, _i64, _f32, _f32, _c_void_p, _c_void_p, _c_void_p,
@@ -69,7 +69,7 @@ SIGNATURES = {
                                    _f32, _i32, _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
     "ldr_read_bwd2_list_any": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32,
                                       _c_void_p]),
-    "ldr_blend_sum_any": (_i32, [_c_void_p, _i64, _f32, _c_void_p, _i64, _i64, _i32, _c_void_p]),
+    "ldr_blend_sum_any": (_i32, [_c_void_p, _i64, _f32, _i32, _c_void_p, _i64, _i64, _i32, _c_void_p]),
 }
 
 

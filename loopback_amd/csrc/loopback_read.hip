@@ -1636,10 +1636,11 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
 }
 
 // out[c] = sum_p part[p][c]: 16 columns per workgroup, 16 row groups (rows p = group mod 16) added in a fixed order
-// out = round(sum_j round(beta * g_j)): the iteration-end blends' shares of h0's gradient, summed once in fp32
+// out = round(sum_j round(beta * g_j)): the iteration-end blends' shares of h0's gradient, summed once in fp32;
+// per_read: each share added in T (rounded after every addition), in table order, as autograd adds them
 template <typename T, int VPT>
-__global__ __launch_bounds__(WG) void k_blend_sum(PtrTab g, int m, float beta, T* __restrict__ out, int64_t n_tok,
-                                                  int d, int tpr) {
+__global__ __launch_bounds__(WG) void k_blend_sum(PtrTab g, int m, float beta, int per_read, T* __restrict__ out,
+                                                  int64_t n_tok, int d, int tpr) {
 #pragma clang fp contract(off)
   const Rows R(d, tpr);
   const int64_t groups = (n_tok + R.rpw - 1) / R.rpw;
@@ -1658,7 +1659,10 @@ __global__ __launch_bounds__(WG) void k_blend_sum(PtrTab g, int m, float beta, T
 #pragma unroll
       for (int v = 0; v < VPT; ++v)
 #pragma unroll
-        for (int x = 0; x < 8; ++x) acc[v][x] += IO<T>::round(beta * e[v][x]);
+        for (int x = 0; x < 8; ++x) {
+          const float t = IO<T>::round(beta * e[v][x]);
+          acc[v][x] = !per_read ? acc[v][x] + t : (j == 0 ? t : IO<T>::round(acc[v][x] + t));
+        }
     }
     if (tok < n_tok) {
 #pragma unroll
@@ -2156,15 +2160,18 @@ __global__ __launch_bounds__(WG) void k_any_bwd2_list(const uint64_t* __restrict
   }
 }
 
-// out = round(sum_j round(beta * g_j)) in table order (k_blend_sum)
+// out = round(sum_j round(beta * g_j)) in table order, or with per_read each addition rounded (k_blend_sum)
 template <typename T>
-__global__ __launch_bounds__(WG) void k_any_blend_sum(const uint64_t* __restrict__ tg, int m, float beta,
+__global__ __launch_bounds__(WG) void k_any_blend_sum(const uint64_t* __restrict__ tg, int m, float beta, int per_read,
                                                       T* __restrict__ out, int64_t n_tok, int64_t d) {
 #pragma clang fp contract(off)
   const int64_t total = n_tok * d;
   for (int64_t e = (int64_t)blockIdx.x * WG + threadIdx.x; e < total; e += (int64_t)gridDim.x * WG) {
     float acc = 0.f;
-    for (int j = 0; j < m; ++j) acc += IO<T>::round(beta * ld1(reinterpret_cast<const T*>(tg[j]) + e));
+    for (int j = 0; j < m; ++j) {
+      const float t = IO<T>::round(beta * ld1(reinterpret_cast<const T*>(tg[j]) + e));
+      acc = !per_read ? acc + t : (j == 0 ? t : IO<T>::round(acc + t));
+    }
     st1(out + e, acc);
   }
 }
@@ -2315,7 +2322,7 @@ __global__ __launch_bounds__(WG) void k_zero(float* __restrict__ p, int64_t n) {
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 13; }
+int ldr_abi_version(void) { return 14; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -2635,9 +2642,10 @@ int ldr_reduce_rows(const float* part, int64_t rows, int64_t d, float* out, void
   return launched();
 }
 
-int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
-                  void* stream) {
+int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, int per_read, void* out, int64_t n_tok, int64_t d,
+                  int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (per_read != 0 && per_read != 1) return LDR_E_ARG;
   if (m < 1 || m > MAXS) return LDR_E_SHAPE;
   if (!g || !tok_ptr(out, n_tok) || n_tok < 0) return LDR_E_ARG;
   if (!al16(out)) return LDR_E_ALIGN;
@@ -2653,8 +2661,8 @@ int ldr_blend_sum(const uint64_t* g, int64_t m, float beta, void* out, int64_t n
   const unsigned grid = grid_of(cdiv(n_tok, WG / tpr), 4096);
   hipStream_t st = static_cast<hipStream_t>(stream);
   LDR_DTYPE_SWITCH(dtype, LDR_VPT_SWITCH(vpt, hipLaunchKernelGGL((k_blend_sum<T, VPT>), dim3(grid), dim3(WG), 0, st,
-                                                                  t, (int)m, beta, static_cast<T*>(out), n_tok,
-                                                                  (int)d, tpr)))
+                                                                  t, (int)m, beta, per_read, static_cast<T*>(out),
+                                                                  n_tok, (int)d, tpr)))
   return launched();
 }
 
@@ -2837,16 +2845,17 @@ int ldr_read_bwd2_list_any(const uint64_t* dv, int64_t n, int accum, const void*
   return launched();
 }
 
-int ldr_blend_sum_any(const uint64_t* g, int64_t m, float beta, void* out, int64_t n_tok, int64_t d, int dtype,
-                      void* stream) {
+int ldr_blend_sum_any(const uint64_t* g, int64_t m, float beta, int per_read, void* out, int64_t n_tok, int64_t d,
+                      int dtype, void* stream) {
   if (!dtype_ok(dtype)) return LDR_E_DTYPE;
+  if (per_read != 0 && per_read != 1) return LDR_E_ARG;
   if (m < 1 || m > ANY_MAXS || d < 1) return LDR_E_SHAPE;
   if (!g || !tok_ptr(out, n_tok) || n_tok < 0) return LDR_E_ARG;
   if (!al_elt(out, dtype)) return LDR_E_ALIGN;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_any_blend_sum<T>), dim3(grid_of(cdiv(n_tok * d, WG), 8192)), dim3(WG),
-                                             0, st, g, (int)m, beta, static_cast<T*>(out), n_tok, d))
+                                             0, st, g, (int)m, beta, per_read, static_cast<T*>(out), n_tok, d))
   return launched();
 }
 

@@ -870,9 +870,11 @@ class FusedCombineStk(torch.autograd.Function):
         if ctx.h0_sum:
             stack.h0_g[step] = g
             if step == min(stack.h0_steps):   # every other iteration end ran its backward: their sum, once
-                gs = [stack.h0_g[k] for k in sorted(stack.h0_g)]
+                # rounding per read: from the last iteration end to the first, as autograd adds the blends' shares
+                gs = [stack.h0_g[k] for k in sorted(stack.h0_g, reverse=stack.per_read)]
                 dh0 = torch.empty_like(g)
-                tail = (len(gs), ctx.beta, _p(dh0), n_tok, d, _dtype_code(stack.V.dtype), _stream(dev))
+                tail = (len(gs), ctx.beta, int(stack.per_read), _p(dh0), n_tok, d, _dtype_code(stack.V.dtype),
+                        _stream(dev))
                 if stack.fast_d and _fast(d, len(gs), dh0, *gs):
                     _run("blend_sum", L.u64_array(x.data_ptr() for x in gs), *tail)
                 else:

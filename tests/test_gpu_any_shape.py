@@ -253,17 +253,24 @@ def test_entry_points_agree_with_row_layout(dtype):
             torch.cuda.synchronize()
             dvs[name] = (dv, dvn)
         assert torch.equal(dvs["any"][0], dvs["fast"][0]) and torch.equal(dvs["any"][1], dvs["fast"][1])
-    sums = []
-    for name in ("fast", "any"):
-        out = torch.empty_like(V[0])
-        if name == "fast":
-            check(lib.ldr_blend_sum(_u64(L, (x.data_ptr() for x in gs)), 3, 0.75, out.data_ptr(), T, d, dt, st))
-        else:
-            tab = _dev(x.data_ptr() for x in gs)
-            check(lib.ldr_blend_sum_any(tab.data_ptr(), 3, 0.75, out.data_ptr(), T, d, dt, st))
-        torch.cuda.synchronize()
-        sums.append(out)
-    assert torch.equal(sums[0], sums[1])
+    for pr in (0, 1):
+        sums = []
+        for name in ("fast", "any"):
+            out = torch.empty_like(V[0])
+            if name == "fast":
+                check(lib.ldr_blend_sum(_u64(L, (x.data_ptr() for x in gs)), 3, 0.75, pr, out.data_ptr(), T, d, dt,
+                                        st))
+            else:
+                tab = _dev(x.data_ptr() for x in gs)
+                check(lib.ldr_blend_sum_any(tab.data_ptr(), 3, 0.75, pr, out.data_ptr(), T, d, dt, st))
+            torch.cuda.synchronize()
+            sums.append(out)
+        assert torch.equal(sums[0], sums[1])
+        if pr:   # rounded after every addition, in table order, as torch adds the rounded shares
+            ref = (gs[0] * 0.75).to(gs[0].dtype)
+            for x in gs[1:]:
+                ref = ref + (x * 0.75).to(x.dtype)
+            assert torch.equal(sums[0], ref)
 
 
 def test_any_shape_refuses_graph_capture():

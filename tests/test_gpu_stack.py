@@ -525,17 +525,19 @@ def test_chain_on_a_side_stream_is_bitwise_the_default_one(mode):
 @pytest.mark.parametrize("K,R", [(2, 4), (3, 3), (1, 4)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("d", [256, 100])
-def test_per_read_rounding_is_the_list_layout_bitwise(monkeypatch, K, R, dtype, d):
-    """LOOP_DATTN_GRAD_ROUNDING=per_read: the stacked layout (online scores, the caller's torch glue -- the reference
-    trainer's own call sequence) rounds each read's share of an update's gradient and adds the shares in the update
-    dtype from the last read to the first, then the scale's term, as autograd adds the list layout's per-read
-    gradients: the final state and every gradient (h0, each update, the query) are the list layout's bit for bit,
-    fp32 and bf16 -- the reference's contract (tests/test_dattn_stack.py:102-107), at a width of the row-layout
-    kernels and one of the any-shape kernels (the default rounding is held to test_layouts_agree's bars)."""
+@pytest.mark.parametrize("glue", ["0", "1"])
+def test_per_read_rounding_is_the_list_layout_bitwise(monkeypatch, K, R, dtype, d, glue):
+    """LOOP_DATTN_GRAD_ROUNDING=per_read: the stacked layout (online scores; the caller's torch glue -- the reference
+    trainer's own call sequence -- or the glue in the kernels) rounds each read's share of an update's gradient and
+    adds the shares in the update dtype from the last read to the first, then the scale's term, as autograd adds the
+    list layout's per-read gradients (and the iteration ends' shares of h0's gradient the same way): the final state
+    and every gradient (h0, each update, the query) are the list layout's bit for bit, fp32 and bf16 -- the
+    reference's contract (tests/test_dattn_stack.py:102-107), at a width of the row-layout kernels and one of the
+    any-shape kernels (the default rounding is held to test_layouts_agree's bars)."""
     from loopback_amd.chain import ChainConfig
-    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", "0")
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
     cfg = ChainConfig(f"per-read-K{K}R{R}d{d}", d, K, R, 1, 160, dtype, True, q_std=0.5)
-    print(f"case per-read rounding K{K} R{R} {dtype} d{d}", flush=True)
+    print(f"case per-read rounding K{K} R{R} {dtype} d{d} glue={glue}", flush=True)
     hl, gl = hip_chain(cfg, "list")
     monkeypatch.setenv("LOOP_DATTN_GRAD_ROUNDING", "per_read")
     hs, gs = hip_chain(cfg, "stack")

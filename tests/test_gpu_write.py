@@ -45,17 +45,25 @@ def test_write_scores(dtype, T, d, N):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("m,T,d", [(1, 5, 64), (8, 77, 768), (3, 16, 8192)])
-def test_blend_sum_bitwise(dtype, m, T, d):
-    """ldr_blend_sum: round(sum_j round(beta g_j)) in fp32, j in order -- bitwise the same sequence in torch."""
+@pytest.mark.parametrize("per_read", [0, 1])
+def test_blend_sum_bitwise(dtype, m, T, d, per_read):
+    """ldr_blend_sum: round(sum_j round(beta g_j)) in fp32, j in order -- or with per_read each addition in the
+    update dtype, as torch adds the rounded shares -- bitwise the same sequence in torch."""
     from loopback_amd import _lib as L
     gen = torch.Generator().manual_seed(m * 1000 + d)
     gs = [torch.randn(T, d, generator=gen).to(dtype).to(DEV) for _ in range(m)]
     out = torch.empty(T, d, dtype=dtype, device=DEV)
-    code = L.LIB.ldr_blend_sum(L.u64_array(g.data_ptr() for g in gs), m, 0.75, out.data_ptr(), T, d,
+    code = L.LIB.ldr_blend_sum(L.u64_array(g.data_ptr() for g in gs), m, 0.75, per_read, out.data_ptr(), T, d,
                                L.BF16 if dtype == torch.bfloat16 else L.F32,
                                torch.cuda.current_stream().cuda_stream)
     L.check(code, "blend_sum")
     torch.cuda.synchronize()
+    if per_read:
+        ref = (gs[0] * 0.75).to(dtype)
+        for g in gs[1:]:
+            ref = ref + (g * 0.75).to(dtype)
+        assert torch.equal(out, ref)
+        return
     acc = torch.zeros(T, d, dtype=torch.float32, device=DEV)
     for g in gs:
         acc = acc + (g * 0.75).to(dtype).float()

@@ -110,8 +110,9 @@ def test_argument_checks_before_launch(lib):
     p = ctypes.c_void_p(4096)
     assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, 64,
                            ctypes.c_void_p(4104), null, 0.5, 16, 64, 1, null) == -3
-    assert L.ldr_blend_sum(too_many, 65, 0.5, p, 16, 64, 1, null) == -2
-    assert L.ldr_blend_sum(one, 1, 0.5, ctypes.c_void_p(4100), 16, 64, 1, null) == -3
+    assert L.ldr_blend_sum(too_many, 65, 0.5, 0, p, 16, 64, 1, null) == -2
+    assert L.ldr_blend_sum(one, 1, 0.5, 0, ctypes.c_void_p(4100), 16, 64, 1, null) == -3
+    assert L.ldr_blend_sum(one, 1, 0.5, 2, p, 16, 64, 1, null) == -1
     # the raw scores' row stride covers the tokens
     assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 8, p, p, 1, p, 1, 1.0, 0.125, p, 1, one, 0, p, 16, p, 64,
                            null, null, 0.0, 16, 64, 1, null) == -1
@@ -136,7 +137,7 @@ def test_argument_checks_before_launch(lib):
     assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, 0, p, null, 0, 8192, 1, null) == 0
     assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, 1, p, null, 0, 8192, 1, null) == 0
     assert L.ldr_dv_assemble(one_src, one_src, one_src, 1, p, p, null, null, 0.0, 2, p, null, 0, 8192, 1, null) == -1
-    assert L.ldr_blend_sum(one, 1, 0.5, p, 0, 8192, 1, null) == 0
+    assert L.ldr_blend_sum(one, 1, 0.5, 0, p, 0, 8192, 1, null) == 0
     assert L.ldr_read_fwd(two, two, 2, p, 16, p, null, 0.0, p, 2, p, 2, 1.0, 0.01, p, p, p, null, 0, 8192, 1,
                           null) == 0
     assert L.ldr_read_bwd1(one, one, 1, p, null, p, p, 16, p, p, 1, p, 1, 1.0, 0.01, p, 1, one, 0, p, 16, p, 8192,
@@ -182,6 +183,7 @@ def test_any_shape_argument_checks_before_launch(lib):
     assert L.ldr_dv_assemble_any(p, p, p, 2, p, p, null, null, 0.0, 3, p, null, 16, 100, 1, null) == -1
     assert L.ldr_read_bwd2_list_any(p, many, 0, p, p, p, 16, 16, 100, 1, null) == -2
     assert L.ldr_read_bwd2_list_any(p, 2, 2, p, p, p, 16, 16, 100, 1, null) == -1
-    assert L.ldr_blend_sum_any(p, 0, 0.5, p, 16, 100, 1, null) == -2
-    assert L.ldr_blend_sum_any(p, 2, 0.5, odd, 16, 100, 1, null) == -3
-    assert L.ldr_blend_sum_any(p, 2, 0.5, p, 0, 100, 1, null) == 0
+    assert L.ldr_blend_sum_any(p, 0, 0.5, 0, p, 16, 100, 1, null) == -2
+    assert L.ldr_blend_sum_any(p, 2, 0.5, 0, odd, 16, 100, 1, null) == -3
+    assert L.ldr_blend_sum_any(p, 2, 0.5, 1, p, 0, 100, 1, null) == 0
+    assert L.ldr_blend_sum_any(p, 2, 0.5, 5, p, 0, 100, 1, null) == -1
