@@ -74,7 +74,7 @@ class LMConfig:
         return f"[{self.prelude}->{self.loop_blocks}x{self.loops}->{self.coda}]"
 
 
-CONFIG5 = LMConfig()   # d=768, 12 heads, SwiGLU 8/3 (2048), [2 -> 4x4 -> 2], vocab 32000
+CONFIG5 = LMConfig()   # the benchmark's config 5: d=768, 12 heads, SwiGLU 8/3 (2048), [2 -> 4x4 -> 2], vocab 32000
 
 
 class Rotary(nn.Module):

@@ -35,7 +35,7 @@ def flat(x):
 @pytest.mark.parametrize("mode,glue", [("list", "1"), ("stack", "1"), ("scores", "1"), ("stack", "0"),
                                        ("scores", "0")])
 def test_config1_forward_matches_oracle(monkeypatch, mode, glue):
-    """BASELINE config 1, the reference's CPU case: d=768, K=2, R=4 (8 updates, 7 reads), 2 x 256 tokens, fp32,
+    """Benchmark config 1, the reference's CPU case: d=768, K=2, R=4 (8 updates, 7 reads), 2 x 256 tokens, fp32,
     forward only; updates and h0 N(0,1), queries N(0, 0.02^2), lambda = 1/4. Through every read path, every state of
     the chain and every read's installed coefficients against the oracle chain: max-abs <= 1e-5 x RMS against the
     exact (fp64) chain and against the fp32 chain."""

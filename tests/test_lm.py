@@ -1,4 +1,4 @@
-"""The minimal Loopback LM (loopback_amd/lm.py) with the HIP read integrated (BASELINE config 5's model).
+"""The minimal Loopback LM (loopback_amd/lm.py) with the HIP read integrated (the benchmark's config 5 model).
 
 CPU (no GPU): the model's wiring with the oracle read in fp64 -- topology and sharing, the Plain-Loop identity of
 Loopback at beta = 0 with zero queries (the reference audit's C6: every coefficient is then 1, so the read is the
@@ -200,7 +200,7 @@ def test_lm_read_modes_agree(monkeypatch, dtype):
 
 @pytest.mark.gpu
 def test_config5_lm_at_full_shape():
-    """BASELINE config 5 at its own shape: d=768, 12 heads, SwiGLU intermediate 2048, [2 -> 4x4 -> 2], vocab 32000,
+    """Benchmark config 5 at its own shape: d=768, 12 heads, SwiGLU intermediate 2048, [2 -> 4x4 -> 2], vocab 32000,
     batch 8 x seq 2048, bf16 weights, uniform random ids, the HIP read on the stacked layout with stored scores.
       * at init (zero queries) the loss equals bitwise that of the same model with the reference read (the oracle
         cell on the same GPU: every other op is the same kernel), as the reference's whole-model check;
