@@ -39,6 +39,18 @@ def test_list_read_any_width(b, t, d, n, boundary):
     assert max(e64.values()) <= 1e-5, e64
 
 
+def test_list_read_any_width_many_tokens():
+    """A ragged 40001 tokens at d = 100: every any-shape kernel takes several rows per wave (grid-stride loops) and
+    backward pass 1 spreads the tokens over its 512 partial rows; fp32 against the exact read, 1e-5 x RMS."""
+    b, t, d, n = 1, 40001, 100, 5
+    args = make(b, t, d, n, torch.float32, seed=401)
+    print(f"case any-width read t{t} d{d} n{n}", flush=True)
+    hip = run_hip(d, n, args, True)
+    ref64 = run_oracle(d, n, args, True, dtype=torch.float64)
+    e64 = compare(hip, ref64, err_rms)
+    assert max(e64.values()) <= 1e-5, e64
+
+
 def test_list_read_many_sources():
     """A read of 80 sources (more than the row-layout kernels' 64)."""
     b, t, d, n = 1, 7, 64, 80
