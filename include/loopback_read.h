@@ -9,8 +9,8 @@
  *   - n_tok = b * t tokens, d the width (a multiple of 8, at most LDR_MAX_WIDTH); n_tok = 0 is a valid batch, for
  *     which the token-sized buffers may be NULL (as empty tensors give them): nothing is read or written but the
  *     per-read outputs (next_prior);
- *   - dtype is LDR_F32 or LDR_BF16 (the scale entry points also take LDR_F16) and applies to the update-shaped
- *     tensors (updates, base, out, g, dv, h, x);
+ *   - dtype is LDR_F32, LDR_BF16 or LDR_F16 and applies to the update-shaped tensors (updates, base, out, g, dv,
+ *     h, x), which are loaded into fp32 and rounded back to dtype (round to nearest even, the fp32 result rounded);
  *     every scale, score, coefficient and gradient scalar is fp32;
  *   - per-source arrays (src_v, src_r, ...) are HOST arrays of n device addresses, copied into the kernel
  *     arguments (no device pointer table, no host-to-device copy); n <= LDR_MAX_SOURCES;
@@ -34,7 +34,7 @@ extern "C" {
 
 #define LDR_F32 0
 #define LDR_BF16 1
-#define LDR_F16 2   /* the scale entry points only (ldr_rstd_fwd / ldr_rstd_bwd), as the reference's rstd */
+#define LDR_F16 2
 
 #define LDR_MAX_SOURCES 64
 #define LDR_MAX_WIDTH 8192
@@ -45,7 +45,7 @@ extern "C" {
 #define LDR_E_ARG (-1)    /* null pointer, negative size, bad flag */
 #define LDR_E_SHAPE (-2)  /* d not a multiple of 8 or too wide; n or nq out of range (*_any: d < 1, n) */
 #define LDR_E_ALIGN (-3)  /* a vector pointer is not 16-byte aligned (*_any: not element-aligned) */
-#define LDR_E_DTYPE (-4)  /* dtype is neither LDR_F32 nor LDR_BF16 (nor LDR_F16 where taken) */
+#define LDR_E_DTYPE (-4)  /* dtype is none of LDR_F32, LDR_BF16, LDR_F16 */
 
 /* Version of this ABI; bumped on any signature change or change of what an entry point accepts. */
 int ldr_abi_version(void);
@@ -63,7 +63,7 @@ int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d);
 /* r[tok] = rsqrt(sum_k x[tok,k]^2 / d + eps).
  * Replaces _rstd_fwd_kernel and its launches (fused_dattn.py:206-215, 240, 705). Any d >= 1 and any alignment, as
  * the reference's masked kernel: rows the vector layout does not take (d not a multiple of 8 or above
- * LDR_MAX_WIDTH, x not 16-byte aligned) run on scalar loads. dtype may also be LDR_F16 (scalar loads). */
+ * LDR_MAX_WIDTH, x not 16-byte aligned) run on scalar loads. */
 int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream);
 
 /* gx[tok,:] = gr[tok] * (-r[tok]^3) / d * x[tok,:], rounded to dtype.
@@ -75,8 +75,8 @@ int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64
  * (summed in ldr_rstd_fwd's order, so the same bits); and the scores of the update against the read queries
  * j_lo .. nq - 1 of the pass: dots[(j - j_lo) * dots_jstride + tok] = q[j, :] . v_out[tok, :] (dots points at query
  * j_lo's score slice for source s; j_lo == nq: no scores). bf16 updates take the scores on the matrix cores from
- * qb, the operand table ldr_split_queries made of the nq fp32 queries; fp32 updates take them on the vector units
- * from q, the fp32 queries [nq, d]. Replaces _write_stk_kernel (fused_dattn.py:561-585, launched at 684-687; its
+ * qb, the operand table ldr_split_queries made of the nq fp32 queries; fp32 and fp16 updates take them on the
+ * vector units from q, the fp32 queries [nq, d]. Replaces _write_stk_kernel (fused_dattn.py:561-585, launched at 684-687; its
  * tensor-core product is tl.dot with tf32x3, 583). */
 int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, const void* qb,
                    int64_t nq, int64_t j_lo, float* dots, int64_t n_tok, int64_t d, int64_t dots_jstride, float eps,
@@ -123,7 +123,7 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
  * sources stream and stored into dots[i * dots_stride + tok] (for the backward; required), and the outputs are
  * those of ldr_read_fwd on those scores (out up to fp32 summation order: the weighted sum runs as an online softmax
  * against a running maximum; tc and p from the same softmax as ldr_read_fwd, so a zero query with cbar == c0 gives
- * tc == c0 and out == base bitwise). q is the read's query, fp32 [d]. Rows wider than one wave (d > 2048 for bf16)
+ * tc == c0 and out == base bitwise). q is the read's query, fp32 [d]. Rows wider than one wave (d > 2048)
  * take two passes inside the call (ldr_dots_online, then ldr_read_fwd). Replaces _dattn_fwd_stk_kernel
  * (fused_dattn.py:410-456, the stacked read with LOOP_DATTN_DOTS=0) and the list layout's _dattn_fwd_kernel
  * (55-108), each one pass over the sources. */

@@ -12,8 +12,8 @@ import torch  # noqa: F401  -- first: the library must bind to the HIP runtime t
 
 from . import build as _build
 
-ABI_VERSION = 14
-F32, BF16, F16 = 0, 1, 2   # F16: the scale entry points only
+ABI_VERSION = 15
+F32, BF16, F16 = 0, 1, 2
 MAX_SOURCES = 64
 MAX_WIDTH = 8192
 MAX_QUERIES = 64

@@ -1,10 +1,10 @@
 // loopback_read.hip -- MI355X (gfx950, CDNA4) kernels of the Loopback depth-attention read.
 //
-// One read at destination s has n = s + 1 sources v_i (bf16 or fp32 updates, one row of d elements per token) and
-// per-token fp32 RMS scales r_i. Every kernel here is HBM-bound streaming over token rows; the design rules are:
-//   * a row of d elements is d/8 sixteen-byte (bf16) vectors, covered by `tpr` lanes holding `vpt` vectors each
-//     (ldr_row_layout); 256-lane workgroups hold 256/tpr rows side by side, so any d that is a multiple of 8 runs
-//     without padding the row to a power of two;
+// One read at destination s has n = s + 1 sources v_i (bf16, fp16 or fp32 updates, one row of d elements per token)
+// and per-token fp32 RMS scales r_i. Every kernel here is HBM-bound streaming over token rows; the design rules are:
+//   * a row of d elements is d/8 eight-element vectors (16 bytes in bf16 and fp16, 32 in fp32), covered by `tpr`
+//     lanes holding `vpt` vectors each (ldr_row_layout); 256-lane workgroups hold 256/tpr rows side by side, so any
+//     d that is a multiple of 8 runs without padding the row to a power of two;
 //   * per-(token, source) scalars (scores, probabilities, weights) are staged through LDS per tile of tokens with
 //     coalesced loads, then broadcast to the lanes of a row;
 //   * row reductions are 64-wide wavefront butterflies, plus one LDS exchange when a row spans several waves;
@@ -140,23 +140,54 @@ struct PtrTab { void* p[MAXS]; };
 struct AsmTab { const void* g[MAXS]; const float* wz[MAXS]; const float* q[MAXS]; };
 
 // ---------------------------------------------------------------------------------------------------------------
-// element I/O: 8 elements (one 16-byte bf16 vector, or two fp32 float4) <-> 8 fp32 registers
+// element I/O: 8 elements (one 16-byte bf16 or fp16 vector, or two fp32 float4) <-> 8 fp32 registers
 // ---------------------------------------------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  // v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN
-  bf16x2_t v = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
 template <typename T> struct IO;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-template <> struct IO<bf16_t> {
+// bf16 <-> fp32: the upper 16 bits of the fp32 pattern; v_cvt_pk_bf16_f32 rounds to nearest even, NaN stays NaN
+struct Bf16Cvt {
+  static __device__ __forceinline__ void unpack2(uint32_t w, float& a, float& b) {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    bf16x2_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  static __device__ __forceinline__ float round(float x) { return (float)(__bf16)x; }
+};
+__device__ __forceinline__ uint32_t pack2(float a, float b) { return Bf16Cvt::pack2(a, b); }
+
+// fp32 -> fp16 of the fp32 value: v_cvt_f16_f32 (round to nearest even; subnormals kept, overflow to inf). The empty
+// asm holds x as an fp32 register value, so the compiler cannot fold the conversion into the operation that produced
+// x (a v_fma_mixlo_f16 rounds the exact product or sum once, straight to fp16, which differs from rounding the fp32
+// result in rare cases): every fp16 result is the fp32 result rounded, as torch's conversions round it.
+__device__ __forceinline__ _Float16 to_f16(float x) {
+  asm("" : "+v"(x));
+  return (_Float16)x;
+}
+
+// fp16 <-> fp32: v_cvt_f32_f16 (exact) and to_f16
+struct F16Cvt {
+  static __device__ __forceinline__ void unpack2(uint32_t w, float& a, float& b) {
+    a = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+    b = (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, to_f16(a)) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, to_f16(b)) << 16);
+  }
+  static __device__ __forceinline__ float round(float x) { return (float)to_f16(x); }
+};
+
+// 16-bit elements (bf16, fp16): one 16-byte vector of 8 elements; the sign is bit 15 of each half-word in both
+template <typename T, typename Cvt> struct IO16 {
   struct Raw { uint4 u; };
-  static __device__ __forceinline__ Raw raw(const bf16_t* p) { Raw r; r.u = *reinterpret_cast<const uint4*>(p); return r; }
+  static __device__ __forceinline__ Raw raw(const T* p) { Raw r; r.u = *reinterpret_cast<const uint4*>(p); return r; }
   // non-temporal: for data read once per kernel and not again soon (the update stack, the output gradient)
-  static __device__ __forceinline__ Raw raw_nt(const bf16_t* p) {
+  static __device__ __forceinline__ Raw raw_nt(const T* p) {
     Raw r;
 #if LDR_NT
     const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -168,37 +199,39 @@ template <> struct IO<bf16_t> {
   }
   static __device__ __forceinline__ Raw zero() { Raw r; r.u = make_uint4(0u, 0u, 0u, 0u); return r; }
   static __device__ __forceinline__ void unpack(const Raw& r, float (&o)[8]) {
-    o[0] = __uint_as_float(r.u.x << 16); o[1] = __uint_as_float(r.u.x & 0xffff0000u);
-    o[2] = __uint_as_float(r.u.y << 16); o[3] = __uint_as_float(r.u.y & 0xffff0000u);
-    o[4] = __uint_as_float(r.u.z << 16); o[5] = __uint_as_float(r.u.z & 0xffff0000u);
-    o[6] = __uint_as_float(r.u.w << 16); o[7] = __uint_as_float(r.u.w & 0xffff0000u);
+    Cvt::unpack2(r.u.x, o[0], o[1]); Cvt::unpack2(r.u.y, o[2], o[3]);
+    Cvt::unpack2(r.u.z, o[4], o[5]); Cvt::unpack2(r.u.w, o[6], o[7]);
   }
-  static __device__ __forceinline__ void load(const bf16_t* p, float (&o)[8]) { unpack(raw(p), o); }
-  static __device__ __forceinline__ void store(bf16_t* p, const float (&o)[8]) {
+  static __device__ __forceinline__ void load(const T* p, float (&o)[8]) { unpack(raw(p), o); }
+  static __device__ __forceinline__ void store(T* p, const float (&o)[8]) {
     uint4 u;
-    u.x = pack2(o[0], o[1]); u.y = pack2(o[2], o[3]); u.z = pack2(o[4], o[5]); u.w = pack2(o[6], o[7]);
+    u.x = Cvt::pack2(o[0], o[1]); u.y = Cvt::pack2(o[2], o[3]);
+    u.z = Cvt::pack2(o[4], o[5]); u.w = Cvt::pack2(o[6], o[7]);
     *reinterpret_cast<uint4*>(p) = u;
   }
   // non-temporal stores, for results not read again soon (the update gradients): they stream to HBM instead of
   // displacing the rows the next launches re-read from the caches
-  static __device__ __forceinline__ void store_nt(bf16_t* p, const float (&o)[8]) {
-    const u32x4 u{pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7])};
+  static __device__ __forceinline__ void store_nt(T* p, const float (&o)[8]) {
+    const u32x4 u{Cvt::pack2(o[0], o[1]), Cvt::pack2(o[2], o[3]), Cvt::pack2(o[4], o[5]), Cvt::pack2(o[6], o[7])};
     __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(p));
   }
   // stores -o (rounded): the sign bits of the rounded values flipped, exact (cached, and non-temporal)
-  static __device__ __forceinline__ void store_neg(bf16_t* p, const float (&o)[8]) {
+  static __device__ __forceinline__ void store_neg(T* p, const float (&o)[8]) {
     uint4 u;
-    u.x = pack2(o[0], o[1]) ^ 0x80008000u; u.y = pack2(o[2], o[3]) ^ 0x80008000u;
-    u.z = pack2(o[4], o[5]) ^ 0x80008000u; u.w = pack2(o[6], o[7]) ^ 0x80008000u;
+    u.x = Cvt::pack2(o[0], o[1]) ^ 0x80008000u; u.y = Cvt::pack2(o[2], o[3]) ^ 0x80008000u;
+    u.z = Cvt::pack2(o[4], o[5]) ^ 0x80008000u; u.w = Cvt::pack2(o[6], o[7]) ^ 0x80008000u;
     *reinterpret_cast<uint4*>(p) = u;
   }
-  static __device__ __forceinline__ void store_neg_nt(bf16_t* p, const float (&o)[8]) {
-    const u32x4 u{pack2(o[0], o[1]) ^ 0x80008000u, pack2(o[2], o[3]) ^ 0x80008000u,
-                  pack2(o[4], o[5]) ^ 0x80008000u, pack2(o[6], o[7]) ^ 0x80008000u};
+  static __device__ __forceinline__ void store_neg_nt(T* p, const float (&o)[8]) {
+    const u32x4 u{Cvt::pack2(o[0], o[1]) ^ 0x80008000u, Cvt::pack2(o[2], o[3]) ^ 0x80008000u,
+                  Cvt::pack2(o[4], o[5]) ^ 0x80008000u, Cvt::pack2(o[6], o[7]) ^ 0x80008000u};
     __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(p));
   }
-  static __device__ __forceinline__ float round(float x) { return (float)(__bf16)x; }
+  static __device__ __forceinline__ float round(float x) { return Cvt::round(x); }
 };
+
+template <> struct IO<bf16_t> : IO16<bf16_t, Bf16Cvt> {};
+template <> struct IO<_Float16> : IO16<_Float16, F16Cvt> {};
 
 template <> struct IO<float> {
   struct Raw { float4 a, b; };
@@ -413,21 +446,23 @@ __global__ __launch_bounds__(WG) void k_rstd_bf16(const bf16_t* __restrict__ x, 
   }
 }
 
-// fp32 rows: the order of k_write_dots. Lane m of a row's 16 takes columns [c0 + 8m, c0 + 8m + 8) for c0 = 0, 128,
-// 256, ... (fused multiply-adds, chunks then elements in order); the 16 partials meet in the butterfly xor 8, 4, 2, 1.
-__global__ __launch_bounds__(WG) void k_rstd_f32(const float* __restrict__ x, float* __restrict__ r, int64_t n_tok,
-                                                 int d, float eps) {
+// fp32 and fp16 rows: the order of k_write_dots. Lane m of a row's 16 takes columns [c0 + 8m, c0 + 8m + 8) for
+// c0 = 0, 128, 256, ... (fused multiply-adds, chunks then elements in order); the 16 partials meet in the butterfly
+// xor 8, 4, 2, 1.
+template <typename T>
+__global__ __launch_bounds__(WG) void k_rstd_valu(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
+                                                  int d, float eps) {
   const int tid = (int)threadIdx.x, m = tid & 15;
   for (int64_t t0 = (int64_t)blockIdx.x * (WG / 16); t0 < n_tok; t0 += (int64_t)gridDim.x * (WG / 16)) {
     const int64_t tok = t0 + (tid >> 4);
-    const float* row = x + (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
+    const T* row = x + (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
     float ss = 0.f;
 #pragma unroll 4
     for (int c0 = 0; c0 < d; c0 += WR_KC) {
       const int col = c0 + 8 * m;
       if (col < d) {
         float e[8];
-        IO<float>::load(row + col, e);
+        IO<T>::load(row + col, e);
 #pragma unroll
         for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(e[k], e[k], ss);
       }
@@ -468,7 +503,7 @@ __device__ __forceinline__ float ld1(const float* p) { return *p; }
 __device__ __forceinline__ float ld1(const _Float16* p) { return (float)*p; }
 __device__ __forceinline__ void st1(bf16_t* p, float v) { *p = __builtin_bit_cast(bf16_t, (__bf16)v); }
 __device__ __forceinline__ void st1(float* p, float v) { *p = v; }
-__device__ __forceinline__ void st1(_Float16* p, float v) { *p = (_Float16)v; }
+__device__ __forceinline__ void st1(_Float16* p, float v) { *p = to_f16(v); }
 
 template <typename T>
 __global__ __launch_bounds__(WG) void k_rstd_fwd_any(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
@@ -534,7 +569,7 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
         for (int k = 0; k < 8; ++k) vv[k] = IO<T>::round(hv[k] - xv[k]);
         IO<T>::store(v + tok * (int64_t)d + col, vv);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) ss[e] = __builtin_fmaf(vv[k], vv[k], ss[e]);   // the scale's order: k_rstd_f32
+        for (int k = 0; k < 8; ++k) ss[e] = __builtin_fmaf(vv[k], vv[k], ss[e]);   // the scale's order: k_rstd_valu
       } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) vv[k] = 0.f;
@@ -2208,7 +2243,8 @@ int row_layout(int64_t d, int* vpt, int* tpr, int max_vpt = 4, bool wave_rows = 
 }
 
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-inline bool dtype_ok(int dt) { return dt == LDR_F32 || dt == LDR_BF16; }
+inline bool dtype_ok(int dt) { return dt == LDR_F32 || dt == LDR_BF16 || dt == LDR_F16; }
+inline int64_t elt_bytes(int dt) { return dt == LDR_F32 ? 4 : 2; }
 // a token-sized buffer: required, except that with no tokens it may be NULL (torch's empty tensors are)
 inline bool tok_ptr(const void* p, int64_t n_tok) { return p != nullptr || n_tok == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -2250,9 +2286,6 @@ int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n, int64_t
   }
 
 #define LDR_DTYPE_SWITCH(DT, ...)                                \
-  if ((DT) == LDR_BF16) { typedef bf16_t T; __VA_ARGS__; }       \
-  else { typedef float T; __VA_ARGS__; }
-#define LDR_DTYPE_SWITCH3(DT, ...)                               \
   if ((DT) == LDR_BF16) { typedef bf16_t T; __VA_ARGS__; }       \
   else if ((DT) == LDR_F16) { typedef _Float16 T; __VA_ARGS__; } \
   else { typedef float T; __VA_ARGS__; }
@@ -2322,7 +2355,7 @@ __global__ __launch_bounds__(WG) void k_zero(float* __restrict__ p, int64_t n) {
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 14; }
+int ldr_abi_version(void) { return 15; }
 
 const char* ldr_strerror(int code) {
   switch (code) {
@@ -2332,7 +2365,7 @@ const char* ldr_strerror(int code) {
       return "loopback_read: unsupported shape (d a multiple of 8 up to 8192 and 1 <= n <= 64; *_any: d >= 1, "
              "1 <= n <= 1024)";
     case LDR_E_ALIGN: return "loopback_read: a vector pointer is not 16-byte aligned (*_any: not element-aligned)";
-    case LDR_E_DTYPE: return "loopback_read: dtype must be LDR_F32 or LDR_BF16 (or LDR_F16 for the scale)";
+    case LDR_E_DTYPE: return "loopback_read: dtype must be LDR_F32, LDR_BF16 or LDR_F16";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "loopback_read: unknown error";
   }
 }
@@ -2349,14 +2382,14 @@ int64_t ldr_read_bwd1_parts(int64_t n_tok, int64_t d) {
 }
 
 int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, int dtype, void* stream) {
-  if (!dtype_ok(dtype) && dtype != LDR_F16) return LDR_E_DTYPE;
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (n_tok < 0 || d < 1 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok)) return LDR_E_ARG;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   int vpt, tpr;
-  if (dtype == LDR_F16 || !al16(x) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other row: scalar loads
+  if (!al16(x) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other row: scalar loads
     const unsigned grid = grid_of(cdiv(n_tok, WG / 64), 8192);
-    LDR_DTYPE_SWITCH3(dtype, hipLaunchKernelGGL((k_rstd_fwd_any<T>), dim3(grid), dim3(WG), 0, st,
+    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_rstd_fwd_any<T>), dim3(grid), dim3(WG), 0, st,
                                                 static_cast<const T*>(x), r, n_tok, d, eps))
     return launched();
   }
@@ -2364,22 +2397,26 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
   const unsigned grid = grid_of(cdiv(n_tok, WG / 16), 8192);
   if (dtype == LDR_BF16)
     hipLaunchKernelGGL(k_rstd_bf16, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(x), r, n_tok, (int)d, eps);
+  else if (dtype == LDR_F16)
+    hipLaunchKernelGGL(k_rstd_valu<_Float16>, dim3(grid), dim3(WG), 0, st, static_cast<const _Float16*>(x), r, n_tok,
+                       (int)d, eps);
   else
-    hipLaunchKernelGGL(k_rstd_f32, dim3(grid), dim3(WG), 0, st, static_cast<const float*>(x), r, n_tok, (int)d, eps);
+    hipLaunchKernelGGL(k_rstd_valu<float>, dim3(grid), dim3(WG), 0, st, static_cast<const float*>(x), r, n_tok,
+                       (int)d, eps);
   return launched();
 }
 
 int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64_t n_tok, int64_t d, int dtype,
                  void* stream) {
-  if (!dtype_ok(dtype) && dtype != LDR_F16) return LDR_E_DTYPE;
+  if (!dtype_ok(dtype)) return LDR_E_DTYPE;
   if (n_tok < 0 || d < 1 || !tok_ptr(x, n_tok) || !tok_ptr(r, n_tok) || !tok_ptr(gr, n_tok) || !tok_ptr(gx, n_tok))
     return LDR_E_ARG;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   int vpt, tpr;
-  if (dtype == LDR_F16 || !al16(x) || !al16(gx) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other row
+  if (!al16(x) || !al16(gx) || row_layout(d, &vpt, &tpr) != LDR_OK) {   // any other row
     const unsigned grid = grid_of(cdiv(n_tok, WG / 64), 8192);
-    LDR_DTYPE_SWITCH3(dtype, hipLaunchKernelGGL((k_rstd_bwd_any<T>), dim3(grid), dim3(WG), 0, st,
+    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_rstd_bwd_any<T>), dim3(grid), dim3(WG), 0, st,
                                                 static_cast<const T*>(x), r, gr, static_cast<T*>(gx), n_tok, d))
     return launched();
   }
@@ -2399,7 +2436,7 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
     return LDR_E_ARG;
   if (nq > LDR_MAX_QUERIES) return LDR_E_SHAPE;
   const bool scores = j_lo < nq;
-  const bool valu = dtype == LDR_F32 || LDR_WRITE_VALU;   // scores on the vector units, from the fp32 queries
+  const bool valu = dtype != LDR_BF16 || LDR_WRITE_VALU;   // scores on the vector units, from the fp32 queries
   if (scores && (!tok_ptr(dots, n_tok) || dots_jstride < n_tok)) return LDR_E_ARG;
   if (scores && ((valu && !q) || (!valu && !qb))) return LDR_E_ARG;
   if (!al16(h) || !al16(x) || !al16(v_out) || (scores && valu && !al16(q)) || (scores && !valu && !al16(qb)))
@@ -2425,7 +2462,7 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
       default: LDR_WM_LAUNCH(4); break;
     }
 #undef LDR_WM_LAUNCH
-  } else {   // vector-unit scores from the fp32 queries (fp32 updates; bf16 too in a build with LDR_WRITE_VALU)
+  } else {   // vector-unit scores from the fp32 queries (fp32, fp16 updates; bf16 in a build with LDR_WRITE_VALU)
     const unsigned grid = (unsigned)cdiv(n_tok, WR_TT);
     const float* qj = scores ? q + j_lo * d : nullptr;
     LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_write_dots<T>), dim3(grid), dim3(WG), 0, st,
@@ -2489,7 +2526,7 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
   if ((e = row_layout(d, &vpt, &tpr, LDR_RF_MAX_VPT, true, LDR_RF_VPT))) return e;
   if (n_tok == 0 && !next_prior) return LDR_OK;
   const Coef cf{cbar, (int)cbar_cols, c0, (int)c0_cols, lam};
-  const int64_t row_bytes = d * (int64_t)(dtype == LDR_BF16 ? 2 : 4);
+  const int64_t row_bytes = d * elt_bytes(dtype);
   // 512-lane workgroups with 32-token tiles whose output (at most 128 KiB) is written as one burst, one workgroup
   // per CU, whenever the tile's rows fit and the read has enough sources to repay the launch's higher fixed cost;
   // else 256-lane workgroups, 16-token tiles, 64 KiB bursts when they fit
@@ -2739,7 +2776,7 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
 // any-shape entry points: per-source addresses in device arrays, rows of any width at element alignment
 // ---------------------------------------------------------------------------------------------------------------
 static inline bool al_elt(const void* p, int dtype) {
-  return (reinterpret_cast<uintptr_t>(p) & (uintptr_t)(dtype == LDR_BF16 ? 1u : 3u)) == 0;
+  return (reinterpret_cast<uintptr_t>(p) & (uintptr_t)(elt_bytes(dtype) - 1)) == 0;
 }
 static inline unsigned any_row_grid(int64_t n_tok, int64_t cap) { return grid_of(cdiv(n_tok, ANY_WAVES), cap); }
 

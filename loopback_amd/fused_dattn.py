@@ -69,21 +69,16 @@ def _stream(dev: torch.device):
     return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
 
 
+_DTYPES = {torch.bfloat16: L.BF16, torch.float16: L.F16, torch.float32: L.F32}
+
+
 def _dtype_code(dtype: torch.dtype) -> int:
-    if dtype == torch.bfloat16:
-        return L.BF16
-    if dtype == torch.float32:
-        return L.F32
-    raise RuntimeError(f"delta_attnres HIP read: updates must be bfloat16 or float32, got {dtype}")
-
-
-def _scale_dtype_code(dtype: torch.dtype) -> int:
-    """The scale kernels also take fp16 rows, as the reference's rstd does; the read's kernels do not."""
-    if dtype == torch.float16:
-        return L.F16
-    if dtype in (torch.bfloat16, torch.float32):
-        return _dtype_code(dtype)
-    raise RuntimeError(f"delta_attnres HIP rstd: input must be bfloat16, float16 or float32, got {dtype}")
+    """The library's code of an update dtype: bf16, fp16 (the reference's kernels load any float dtype and round
+    back to it) or fp32."""
+    code = _DTYPES.get(dtype)
+    if code is None:
+        raise RuntimeError(f"delta_attnres HIP read: updates must be bfloat16, float16 or float32, got {dtype}")
+    return code
 
 
 def _require_gpu(t: torch.Tensor, what: str) -> None:
@@ -222,7 +217,7 @@ class _Rstd(torch.autograd.Function):
         d = xc.shape[-1]
         n_tok = xc.numel() // d
         r = torch.empty(xc.shape[:-1] + (1,), device=xc.device, dtype=torch.float32)
-        _run("rstd_fwd", _p(xc), _p(r), n_tok, d, float(eps), _scale_dtype_code(xc.dtype), _stream(xc.device))
+        _run("rstd_fwd", _p(xc), _p(r), n_tok, d, float(eps), _dtype_code(xc.dtype), _stream(xc.device))
         ctx.save_for_backward(xc, r)
         return r
 
@@ -233,7 +228,7 @@ class _Rstd(torch.autograd.Function):
         n_tok = xc.numel() // d
         gx = torch.empty_like(xc)
         grc = gr.float().contiguous()
-        _run("rstd_bwd", _p(xc), _p(r), _p(grc), _p(gx), n_tok, d, _scale_dtype_code(xc.dtype), _stream(xc.device))
+        _run("rstd_bwd", _p(xc), _p(r), _p(grc), _p(gx), n_tok, d, _dtype_code(xc.dtype), _stream(xc.device))
         return gx, None
 
 
@@ -250,10 +245,11 @@ def rstd(delta: torch.Tensor, eps: float) -> torch.Tensor:
 def fused_read_supported(base, values, rstds, cbar) -> bool:
     """The reference's gate (fused_dattn.py:379-395) -- GPU, contiguous, same-shape same-dtype bf16/fp32 sources and
     base, contiguous fp32 (b, t, 1) rstds, contiguous fp32 (b, t, n) cbar -- plus the kernels' source count (at most
-    ANY_MAX_SOURCES) and one device. Any width and alignment: rows the row-layout kernels do not take go to the
-    any-shape kernels."""
+    ANY_MAX_SOURCES) and one device; fp16 sources are taken too (the stacked layout's kernels, which the reference
+    runs on any float dtype). Any width and alignment: rows the row-layout kernels do not take go to the any-shape
+    kernels."""
     v0 = values[0]
-    if not v0.is_cuda or v0.dtype not in (torch.bfloat16, torch.float32):
+    if not v0.is_cuda or v0.dtype not in _DTYPES:
         return False
     shape = v0.shape
     if shape[-1] < 1 or len(values) > ANY_MAX_SOURCES or len(rstds) != len(values):
@@ -460,8 +456,8 @@ class DattnStack:
     def __init__(self, n_steps: int, shape, dtype, device, query=None, eps: float = 1e-6):
         b, t, d = shape
         n_steps = int(n_steps)
-        if dtype not in (torch.bfloat16, torch.float32):
-            raise RuntimeError(f"delta_attnres stacked read: dtype must be bfloat16 or float32, got {dtype}")
+        if dtype not in _DTYPES:
+            raise RuntimeError(f"delta_attnres stacked read: dtype must be bfloat16, float16 or float32, got {dtype}")
         if d < 1 or n_steps < 1 or n_steps > ANY_MAX_SOURCES:
             raise RuntimeError(f"delta_attnres stacked read: unsupported shape d={d} n_steps={n_steps} (d >= 1, "
                                f"1 to {ANY_MAX_SOURCES} steps)")

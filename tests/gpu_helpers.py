@@ -40,3 +40,30 @@ def err_norm(a, ref):
     """||a - ref|| / ||ref||: the stacked-layout test's relative error (tests/test_dattn_stack.py:64-65)."""
     ref = ref.double().cpu()
     return ((a.double().cpu() - ref).norm() / ref.norm().clamp_min(1e-30)).item()
+
+
+def lib_dtype(dtype):
+    """The C ABI's code of an update dtype."""
+    from loopback_amd import _lib as L
+    return {torch.float32: L.F32, torch.bfloat16: L.BF16, torch.float16: L.F16}[dtype]
+
+
+def lowp(bf16_bar, dtype):
+    """A bar stated for bf16 carried to fp16: fp16 rounds to 2^-11 relative where bf16 rounds to 2^-8, so the bar
+    is 8 times tighter."""
+    return bf16_bar if dtype == torch.bfloat16 else bf16_bar / 8
+
+
+def ulp_rel(dtype):
+    """The spacing of the dtype's values in [1, 2), relative: 2^-7 (bf16), 2^-10 (fp16) -- one rounding of an exact
+    value moves it by at most half of that."""
+    return {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[dtype]
+
+
+def within_ulps(a, ref, k=1, floor=2e-5):
+    """Elementwise |a - ref| <= k units in the last place of their 16-bit dtype at max(|a|, |ref|), plus floor x
+    RMS(ref): what k roundings of fp32 values that differ only in their last bits can leave between two results."""
+    u = ulp_rel(ref.dtype)
+    a, ref = a.double().cpu(), ref.double().cpu()
+    bound = torch.maximum(a.abs(), ref.abs()) * (k * u) + floor * rms(ref)
+    return bool(((a - ref).abs() <= bound).all())

@@ -2,18 +2,18 @@
 what torch's subtraction gives), R[s] the RMS scale of the rounded update, and the scores of the update against
 the queries of the reads still to come, DOTS[j, s, tok] = q_j . V[s, tok] for j >= s - 1 -- against an fp64 matmul
 of the rounded update (bf16: matrix cores from the queries' three bf16 parts -- k_write_rows for widths that are
-multiples of 256, here 768 and 2048, k_write_mfma for the others; fp32: vector units). Ragged token
+multiples of 256, here 768 and 2048, k_write_mfma for the others; fp32 and fp16: vector units). Ragged token
 counts, widths below one 64-column chunk and a width with a partial chunk included; every slice is checked
 again after the last write."""
 import pytest
 import torch
 
-from gpu_helpers import DEV, err_rms
+from gpu_helpers import DEV, err_rms, lib_dtype
 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("T,d", [(37, 64), (100, 768), (257, 1096), (64, 2048), (19, 40), (5, 8)])
 @pytest.mark.parametrize("N", [2, 9, 33, 64])   # 64: up to 63 queries, the 4-block score kernels
 def test_write_scores(dtype, T, d, N):
@@ -43,7 +43,7 @@ def test_write_scores(dtype, T, d, N):
             assert err_rms(got[j_lo:, s], ref[j_lo:, s]) <= 1e-5, s
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("m,T,d", [(1, 5, 64), (8, 77, 768), (3, 16, 8192)])
 @pytest.mark.parametrize("per_read", [0, 1])
 def test_blend_sum_bitwise(dtype, m, T, d, per_read):
@@ -54,8 +54,7 @@ def test_blend_sum_bitwise(dtype, m, T, d, per_read):
     gs = [torch.randn(T, d, generator=gen).to(dtype).to(DEV) for _ in range(m)]
     out = torch.empty(T, d, dtype=dtype, device=DEV)
     code = L.LIB.ldr_blend_sum(L.u64_array(g.data_ptr() for g in gs), m, 0.75, per_read, out.data_ptr(), T, d,
-                               L.BF16 if dtype == torch.bfloat16 else L.F32,
-                               torch.cuda.current_stream().cuda_stream)
+                               lib_dtype(dtype), torch.cuda.current_stream().cuda_stream)
     L.check(code, "blend_sum")
     torch.cuda.synchronize()
     if per_read:

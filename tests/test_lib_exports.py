@@ -79,9 +79,11 @@ def test_argument_checks_before_launch(lib):
     assert L.ldr_dots_online(lib.u64_array([4100]), 1, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, 1,
                              null) == -3
     assert L.ldr_rstd_fwd(ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 64, 1e-6, 7, null) == -4
-    # fp16 (code 2): the scale entry points take it, the read's do not
+    # fp16 (code 2) is an update dtype of every entry point (no tokens: nothing launched); code 3 is none
     assert L.ldr_rstd_fwd(null, null, 0, 64, 1e-6, lib.F16, null) == 0
-    assert L.ldr_dots_online(one_v, 1, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, lib.F16, null) == -4
+    assert L.ldr_dots_online(one_v, 1, ctypes.c_void_p(4096), null, 0, 0, 64, lib.F16, null) == 0
+    assert L.ldr_dots_online(one_v, 1, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, 3, null) == -4
+    assert L.ldr_write_dots(null, null, null, null, null, null, 4, 4, null, 0, 64, 0, 1e-6, lib.F16, null) == 0
     too_many = lib.u64_array([4096] * 65)
     assert L.ldr_dots_online(too_many, 65, ctypes.c_void_p(4096), ctypes.c_void_p(4096), 16, 16, 64, 1, null) == -1
     p4 = ctypes.c_void_p(4096)
