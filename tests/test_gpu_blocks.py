@@ -7,7 +7,8 @@ the same weights: norm-relative 1e-5 in fp32 and 1e-2 in bf16 (outputs and every
 <= 1e-5 x RMS against the exact (fp64) chain for the final state and the gradients of h0 and the query, and the
 blocks' weight gradients no further from it than those of the fp32 reference chain run on the same GPU (the weight
 gradients are torch's GPU products, whose own fp32 error dominates them); in bf16 no further from the fp64 oracle than the reference read in bf16
-is (<= 2 err_ref + 2e-3, tests/test_fused_dattn.py:104-109).
+is (<= 2 err_ref + 2e-3, tests/test_fused_dattn.py:104-109). And the reference's layout contract on this chain: with
+per-read rounding the stacked layout is the list layout bit for bit, state and every gradient, in bf16, fp16 and fp32.
 """
 import pytest
 import torch
@@ -102,3 +103,28 @@ def test_linear_block_chain_matches_oracle(monkeypatch, K, R, dtype, mode, glue)
         for a, b, c in zip(g, gr, g64):
             assert err_norm(a, c) <= 2 * err_norm(b, c) + 2e-3
 
+
+
+@pytest.mark.parametrize("K,R", [(2, 4), (3, 3)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("glue", ["0", "1"])
+def test_linear_block_chain_stack_is_list_bitwise(monkeypatch, K, R, dtype, glue):
+    """The reference's layout contract on its own chain (tests/test_dattn_stack.py:5-6, 96-107: stack vs list,
+    outputs bitwise, gradients bitwise in the training dtype): the stacked layout with online scores and
+    LOOP_DATTN_GRAD_ROUNDING=per_read against the list layout, the final state and the gradients of every W_s, h0
+    and the query bit for bit, in bf16, fp16 and fp32, with the caller's glue as torch ops or in the kernels. The
+    list chain run twice first gives the same bits (the blocks' products are deterministic here), so the comparison
+    is one of the read's layouts alone."""
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
+    print(f"case linear blocks per-read K{K} R{R} {dtype} glue={glue}", flush=True)
+    Ws, h0, q = make(K, R, 256, 2048, seed=5)
+    h0 = h0.to(dtype).float()
+    hl, gl = hip_chain(K, R, dtype, "list", Ws, h0, q)
+    hl2, gl2 = hip_chain(K, R, dtype, "list", Ws, h0, q)
+    assert torch.equal(hl, hl2) and all(torch.equal(a, b) for a, b in zip(gl, gl2))
+    monkeypatch.setenv("LOOP_DATTN_GRAD_ROUNDING", "per_read")
+    hs, gs = hip_chain(K, R, dtype, "stack", Ws, h0, q)
+    assert torch.equal(hs, hl)
+    names = [f"W{i}" for i in range(K * R)] + ["h0", "query"]
+    for name, a, b in zip(names, gs, gl):
+        assert torch.equal(a, b), name
