@@ -6,7 +6,9 @@ plain residual sum), and a loss near log(vocab) at init.
 GPU: the model with the HIP read against the same weights on the CPU with the oracle read in fp64 -- loss and every
 parameter gradient (fp32: norm-relative 1e-4; bf16: loss within 1e-2 relative) -- the model through every read
 path (stored / online scores, list layout, torch glue) agreeing, the model at init bitwise the same with the
-reference read run on the GPU, and a few training steps that lower the loss on a fixed batch. CPU also: the meta-device init path leaves the queries at zero.
+reference read run on the GPU, and a few training steps that lower the loss on a fixed batch; the reference's
+whole-model layout test (stacked == list bit for bit with per-read rounding: loss, logits, every gradient) with a
+deterministic attention. CPU also: the meta-device init path leaves the queries at zero.
 """
 import copy
 import math
@@ -280,3 +282,62 @@ def test_config5_lm_at_full_shape():
     opt.zero_grad(set_to_none=True)
     with torch.no_grad():
         assert torch.isfinite(hip(ids)).all()
+
+
+def _fp32_attention(q, k, v, is_causal=True):
+    """Causal attention by explicit fp32 products of contiguous operands, rounded back to the input dtype: the same
+    bits on every run (the library kernels may split their sums differently), as the reference's layout test runs
+    its model with a reference attention (tests/test_dattn_stack.py:34-47)."""
+    qf, kf, vf = q.float().contiguous(), k.float().contiguous(), v.float().contiguous()
+    s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * qf.shape[-1] ** -0.5
+    T = s.shape[-1]
+    s = s.masked_fill(torch.ones(T, T, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
+    return torch.matmul(torch.softmax(s, -1), vf).to(q.dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("glue", ["0", "1"])
+def test_lm_layout_contract(monkeypatch, dtype, glue):
+    """The reference's whole-model layout test (tests/test_dattn_stack.py:129-160) on this LM with a deterministic
+    attention: with LOOP_DATTN_GRAD_ROUNDING=per_read the stacked layout with online scores is the list layout bit
+    for bit -- loss, logits and every parameter gradient -- in bf16 (the reference's training dtype), fp16 and fp32;
+    with the default rounding, the stacked layout with stored scores within the reference's bar of the list layout
+    (norm-relative 1e-5 in fp32, 3e-2 in bf16, fp16 3.75e-3), logits and every gradient. The list run twice gives the
+    same bits first, so the comparisons are of the read's layouts alone."""
+    import torch.nn.functional as F
+    monkeypatch.setattr(F, "scaled_dot_product_attention", _fp32_attention)
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
+    torch.manual_seed(4)
+    cfg = LMConfig(**TINY)
+    model = LoopbackLM(cfg)
+    with torch.no_grad():
+        model.read.query.normal_(0, 0.3)
+    ids = ids_for(cfg, b=2, t=48, seed=1).cuda()
+    print(f"case LM layout contract {dtype} glue={glue}", flush=True)
+
+    def run(stack, dots, rounding):
+        monkeypatch.setenv("LOOP_DATTN_STACK", stack)
+        monkeypatch.setenv("LOOP_DATTN_DOTS", dots)
+        monkeypatch.setenv("LOOP_DATTN_GRAD_ROUNDING", rounding)
+        m = copy.deepcopy(model).to(device="cuda", dtype=dtype)
+        logits = m.head(m.hidden(ids))
+        labels = torch.cat((ids[:, 1:], torch.full_like(ids[:, :1], -100)), dim=1)
+        loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]).float(), labels.reshape(-1), ignore_index=-100)
+        loss.backward()
+        torch.cuda.synchronize()
+        return loss.item(), logits.detach().cpu(), {k: p.grad.detach().cpu() for k, p in m.named_parameters()
+                                                   if p.grad is not None}
+
+    ll, Ll, gl = run("0", "1", "once")
+    ll2, Ll2, gl2 = run("0", "1", "once")
+    assert ll == ll2 and torch.equal(Ll, Ll2) and all(torch.equal(gl[k], gl2[k]) for k in gl)
+    ls, Ls, gs = run("1", "0", "per_read")
+    assert ls == ll and torch.equal(Ls, Ll)
+    assert set(gs) == set(gl) and all(torch.equal(gs[k], gl[k]) for k in gl), \
+        [k for k in gl if not torch.equal(gs[k], gl[k])]
+    lw, Lw, gw = run("1", "1", "once")
+    tol = {torch.float32: 1e-5, torch.bfloat16: 3e-2, torch.float16: 3e-2 / 8}[dtype]
+    rel = lambda a, b: ((a.double() - b.double()).norm() / b.double().norm().clamp_min(1e-30)).item()
+    assert rel(Lw, Ll) <= tol
+    assert max(rel(gw[k], gl[k]) for k in gl) <= tol
