@@ -1,12 +1,14 @@
 """Benchmark of the Loopback depth-attention read on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--mode scores] [--no-cpu-baseline]
-                    [--no-extra-configs]
+                    [--no-extra-configs] [--dtype bf16|fp16|fp32]
 
 A step is one pass of the read path over one batch: the K x R chain of the benchmark configuration (default
 config 4: d=2048, K=4, R=8 -> N=32 updates, 31 reads, T = 8 x 2048 tokens, bf16 updates, fp32 scores), forward and
 backward -- N writes (with the read-query scores), N-1 reads, their backwards, the updates' gradients -- with the
-synthetic blocks x -> x + D_s and the caller's glue included. Inputs are resident in HBM before timing.
+synthetic blocks x -> x + D_s and the caller's glue included. Inputs are resident in HBM before timing. --dtype
+times the same configuration with other update dtypes (fp16: the trainer's fp16 mixed precision); the default run
+is the configuration's own dtype.
 
 Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / wall time), plus
   roofline      the dominant kernel (most time per pass): the reference dataflow's algorithmic bytes per launch for
@@ -28,6 +30,7 @@ from __future__ import annotations
 
 import argparse
 import contextlib
+import dataclasses
 import gc
 import hashlib
 import json
@@ -48,6 +51,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4"])
     ap.add_argument("--mode", default="scores", choices=["scores", "stack", "list"])
+    ap.add_argument("--dtype", default=None, choices=sorted(DTYPE_NAMES),
+                    help="the updates' dtype (default: the configuration's own)")
     ap.add_argument("--graph", action="store_true",
                     help="time replays of the pass captured in HIP graphs (no host work per kernel): the forward "
                          "as one graph, a training pass as a forward and a backward graph")
@@ -99,14 +104,22 @@ class KernelTimer:
         return {k: {"launches": v[0], "total_ms": v[1], "mean_us": 1e3 * v[1] / v[0]} for k, v in out.items()}
 
 
-def torch_bf16():
+DTYPE_NAMES = {"bf16": "bfloat16", "fp16": "float16", "fp32": "float32"}
+
+
+def dtype_name(dtype) -> str:
+    """The bench line's name of a torch dtype ("bf16", "fp16", "fp32")."""
+    return {v: k for k, v in DTYPE_NAMES.items()}[str(dtype).replace("torch.", "")]
+
+
+def elt_bytes(dtype) -> int:
     import torch
-    return torch.bfloat16
+    return torch.empty(0, dtype=dtype).element_size()
 
 
 def _shape(cfg, mode):
     from loopback_amd.cell import fuse_glue
-    e = 2 if cfg.dtype == torch_bf16() else 4
+    e = elt_bytes(cfg.dtype)
     N, T = cfg.N, cfg.n_tok
     S2 = N * (N + 1) // 2 - 1
     fused = mode != "list" and fuse_glue()
@@ -289,7 +302,7 @@ def cpu_baseline(cfg, tokens):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     med, runs = _cpu_time(cfg, tokens, 10, 30)
-    e = 2 if cfg.dtype == torch.bfloat16 else 4
+    e = elt_bytes(cfg.dtype)
     bpt = algorithmic_bytes_per_token(cfg.N, cfg.d, e, backward=cfg.backward)["total"]
     c1 = CONFIGS["c1"]
     med1, runs1 = _cpu_time(c1, c1.n_tok, 5, 15)
@@ -322,6 +335,10 @@ def main():
     from loopback_amd.chain import CONFIGS
 
     cfg = CONFIGS[args.config]
+    if args.dtype is not None and dtype_name(cfg.dtype) != args.dtype:
+        own = dtype_name(cfg.dtype)
+        cfg = dataclasses.replace(cfg, dtype=getattr(torch, DTYPE_NAMES[args.dtype]),
+                                  name=cfg.name.replace(own, args.dtype))
     dev = torch.device("cuda", 0)
     if args.graph:   # the pass replayed from HIP graphs: no Python or launch work per kernel
         elapsed = time_graphed(cfg, args.mode, args.steps, args.warmup)
@@ -330,7 +347,7 @@ def main():
                                     "HIP graph replay",
                           "value": cfg.n_tok * args.steps / elapsed, "unit": "read-tokens/s", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "ms_per_step": 1e3 * elapsed / args.steps,
-                          "higher_is_better": True, "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
+                          "higher_is_better": True, "dtype": dtype_name(cfg.dtype),
                           "formula_wall_gbs": ref_bytes * args.steps / elapsed / 1e9,
                           "config": {"workload": cfg.name, "mode": args.mode, "graph": True}}), flush=True)
         return
@@ -352,7 +369,9 @@ def main():
     alg = (sv[dom] if basis == "survey" else fam[dom]) / launches
     achieved = alg / mean_s / 1e9
     kernel_ms = sum(v["total_ms"] for v in ksum.values())
-    traffic, traffic_label = committed_traffic(args.config, args.mode, dom)
+    # the committed counter summary is of the configuration's own dtype
+    traffic, traffic_label = (committed_traffic(args.config, args.mode, dom) if cfg.dtype == CONFIGS[args.config].dtype
+                              else (None, None))
 
     line = {
         "metric": ("depth-read tokens/sec (fwd+bwd), d=2048, N=32 stack" if args.config == "c4" else
@@ -366,7 +385,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "fp32",
+        "dtype": dtype_name(cfg.dtype),
         "data": "synthetic (seeded N(0,1) updates and h0, N(0,0.02^2) queries; blocks x -> x + D_s)",
         "config": {"workload": cfg.name, "d": cfg.d, "K": cfg.K, "R": cfg.R, "N": cfg.N, "tokens": cfg.n_tok,
                    "mode": args.mode, "backward": cfg.backward, "parallelism": "single GPU"},

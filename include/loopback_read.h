@@ -74,9 +74,9 @@ int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64
 /* The write step of update s: v_out = round(h - x); r_out[tok] = rsqrt(mean(v_out^2) + eps) of the rounded update
  * (summed in ldr_rstd_fwd's order, so the same bits); and the scores of the update against the read queries
  * j_lo .. nq - 1 of the pass: dots[(j - j_lo) * dots_jstride + tok] = q[j, :] . v_out[tok, :] (dots points at query
- * j_lo's score slice for source s; j_lo == nq: no scores). bf16 updates take the scores on the matrix cores from
- * qb, the operand table ldr_split_queries made of the nq fp32 queries; fp32 and fp16 updates take them on the
- * vector units from q, the fp32 queries [nq, d]. Replaces _write_stk_kernel (fused_dattn.py:561-585, launched at 684-687; its
+ * j_lo's score slice for source s; j_lo == nq: no scores). bf16 and fp16 updates take the scores on the matrix cores
+ * from qb, the operand table ldr_split_queries made of the nq fp32 queries (an fp16 update as the exact sum of two
+ * bf16 values); fp32 updates take them on the vector units from q, the fp32 queries [nq, d]. Replaces _write_stk_kernel (fused_dattn.py:561-585, launched at 684-687; its
  * tensor-core product is tl.dot with tf32x3, 583). */
 int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, const void* qb,
                    int64_t nq, int64_t j_lo, float* dots, int64_t n_tok, int64_t d, int64_t dots_jstride, float eps,

@@ -69,7 +69,7 @@
 #define LDR_B1_WAVE_ROWS 1   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
 #ifndef LDR_WRITE_VALU
-#define LDR_WRITE_VALU 0     // write: bf16 scores on the vector units (k_write_dots) instead of the matrix cores; a
+#define LDR_WRITE_VALU 0     // write: 16-bit scores on the vector units (k_write_dots) instead of the matrix cores; a
 #endif                       // comparison build (its scale then follows the fp32 write's summation order)
 #ifndef LDR_WM_ROWS
 #define LDR_WM_ROWS 1        // write: rows streamed whole (d a multiple of 256), else in the matrix cores' layout
@@ -410,18 +410,20 @@ constexpr int WR_TT = 32, WR_KC = 128, WR_KP = WR_KC + 4, WR_MQ = 8;
 // (which store it beside the update) or by these kernels (the list layout's rstd, the stacked layout when the write
 // did not store it) -- so both layouts read with bitwise equal scales, and so bitwise equal outputs.
 //
-// bf16 rows: the order of k_write_mfma / k_write_rows. Columns go in 64-column chunks, chunk c to slot w = c mod 4;
+// 16-bit rows (bf16, fp16): the order of k_write_mfma / k_write_rows. Columns go in 64-column chunks, chunk c to slot
+// w = c mod 4;
 // inside a chunk, quad q takes columns [8q, 8q + 8) and [32 + 8q, 40 + 8q). Partial (w, q) is the fused
 // multiply-add sum over its chunks in order, its two column groups in order, and their elements in order. Then
 // W_w = (p_w0 + p_w1) + (p_w2 + p_w3), and sum = ((W_0 + W_1) + W_2) + W_3.
 // Here a row takes 16 lanes (lane 4 w + q holds partial (w, q)), 4 rows per wave.
-__global__ __launch_bounds__(WG) void k_rstd_bf16(const bf16_t* __restrict__ x, float* __restrict__ r, int64_t n_tok,
-                                                  int d, float eps) {
+template <typename T>
+__global__ __launch_bounds__(WG) void k_rstd_chunks(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
+                                                    int d, float eps) {
   const int tid = (int)threadIdx.x, lane = tid & 63, j = lane & 15, w = j >> 2, quad = j & 3;
   const int nchunks = (d + 63) >> 6;
   for (int64_t t0 = (int64_t)blockIdx.x * (WG / 16); t0 < n_tok; t0 += (int64_t)gridDim.x * (WG / 16)) {
     const int64_t tok = t0 + (tid >> 4);
-    const bf16_t* row = x + (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
+    const T* row = x + (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
     float ss = 0.f;
 #pragma unroll 4
     for (int c = w; c < nchunks; c += 4) {
@@ -430,7 +432,7 @@ __global__ __launch_bounds__(WG) void k_rstd_bf16(const bf16_t* __restrict__ x, 
         const int col = c * 64 + quad * 8 + 32 * hf;
         if (col < d) {   // d is a multiple of 8: a column group is whole or past the row
           float e[8];
-          IO<bf16_t>::load(row + col, e);
+          IO<T>::load(row + col, e);
 #pragma unroll
           for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(e[k], e[k], ss);
         }
@@ -446,7 +448,7 @@ __global__ __launch_bounds__(WG) void k_rstd_bf16(const bf16_t* __restrict__ x, 
   }
 }
 
-// fp32 and fp16 rows: the order of k_write_dots. Lane m of a row's 16 takes columns [c0 + 8m, c0 + 8m + 8) for
+// fp32 rows: the order of k_write_dots. Lane m of a row's 16 takes columns [c0 + 8m, c0 + 8m + 8) for
 // c0 = 0, 128, 256, ... (fused multiply-adds, chunks then elements in order); the 16 partials meet in the butterfly
 // xor 8, 4, 2, 1.
 template <typename T>
@@ -667,6 +669,28 @@ constexpr int WM_HS = 32;   // column step between a lane's two k-groups
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
+// The matrix cores' A operands of 8 stored update values (one 16-byte vector). A bf16 update is its own operand. An
+// fp16 value e is the exact sum of two bf16 values, hi = bf16(e) and lo = e - hi (e has 11 significant bits, hi takes
+// the top 8 and lo the rest; bf16 spans fp16's exponent range), so the products with hi and lo give e's share exactly
+// and the scores keep the bf16 updates' accuracy.
+template <typename T> struct MfmaA;
+template <> struct MfmaA<bf16_t> {
+  static constexpr int NP = 1;
+  static __device__ __forceinline__ void split(uint4 u, uint4 (&a)[1]) { a[0] = u; }
+};
+template <> struct MfmaA<_Float16> {
+  static constexpr int NP = 2;
+  static __device__ __forceinline__ void split(uint4 u, uint4 (&a)[2]) {
+    float e[8], hi[8];
+    IO<_Float16>::unpack(IO<_Float16>::Raw{u}, e);
+    a[0] = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
+    IO<bf16_t>::unpack(IO<bf16_t>::Raw{a[0]}, hi);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) e[k] -= hi[k];   // exact
+    a[1] = make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
+  }
+};
+
 // The bf16 parts of the read queries in the matrix cores' operand order (written once per stack by
 // k_split_queries): for chunk c of 64 columns, 16-query block b, part p (hi, mid, lo) and k-group half hf, the 64
 // lanes' 16-byte operands are consecutive -- qt[(((c nbq + b) 3 + p) 2 + hf) 64 + l], lane l holding query
@@ -681,11 +705,12 @@ struct QTile {
   int nq;     // queries in the table
 };
 
-template <int NB>   // NB 16-query blocks scored (from block qt.b0); NB = 0: no scores
-__global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h, const bf16_t* __restrict__ x,
-                                                   bf16_t* __restrict__ v, float* __restrict__ r, QTile qt,
+template <typename T, int NB>   // 16-bit updates; NB 16-query blocks scored (from block qt.b0); NB = 0: no scores
+__global__ __launch_bounds__(WG) void k_write_mfma(const T* __restrict__ h, const T* __restrict__ x,
+                                                   T* __restrict__ v, float* __restrict__ r, QTile qt,
                                                    float* __restrict__ dots, int64_t n_tok, int d,
                                                    int64_t dots_jstride, float eps) {
+  using AP = MfmaA<T>;
   constexpr int NBA = NB > 0 ? NB : 1;   // array extents
   __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
   __shared__ float s_ss[4][WM_MB][16];
@@ -748,24 +773,25 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) { hc[mb][hf] = hr[mb][hf]; xc[mb][hf] = xr[mb][hf]; }
     if (c + 4 < nchunks) load_hx(c + 4, hr, xr);   // uniform branch
-    uint4 va[WM_MB][2];
+    uint4 va[WM_MB][2][AP::NP];
 #pragma unroll
     for (int mb = 0; mb < WM_MB; ++mb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         float hv[8], xv[8], vv[8];
-        IO<bf16_t>::unpack(IO<bf16_t>::Raw{hc[mb][hf]}, hv);
-        IO<bf16_t>::unpack(IO<bf16_t>::Raw{xc[mb][hf]}, xv);
+        IO<T>::unpack(typename IO<T>::Raw{hc[mb][hf]}, hv);
+        IO<T>::unpack(typename IO<T>::Raw{xc[mb][hf]}, xv);
         const bool ok = tok_ok[mb] && col_ok[hf];
 #pragma unroll
         for (int k = 0; k < 8; ++k) vv[k] = ok ? hv[k] - xv[k] : 0.f;
-        uint4 u;
-        u.x = pack2(vv[0], vv[1]); u.y = pack2(vv[2], vv[3]); u.z = pack2(vv[4], vv[5]); u.w = pack2(vv[6], vv[7]);
-        va[mb][hf] = u;
+        T rounded[8];
+        IO<T>::store(rounded, vv);
+        const uint4 u = *reinterpret_cast<const uint4*>(rounded);
+        AP::split(u, va[mb][hf]);
         float rv[8];
-        IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);   // the stored (rounded) update
+        IO<T>::unpack(typename IO<T>::Raw{u}, rv);   // the stored (rounded) update
 #pragma unroll
-        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(rv[k], rv[k], ss[mb]);   // k_rstd_bf16's order
+        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(rv[k], rv[k], ss[mb]);   // k_rstd_chunks' order
         s_v[w][16 * mb + row][quad + 4 * hf] = u;
       }
     wave_lds_sync();
@@ -789,8 +815,10 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
         for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
           for (int mb = 0; mb < WM_MB; ++mb)   // (columns past d: zero operands on both sides)
-            acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qv[p][b][hf]),
-                                                                 acc[mb][b], 0, 0, 0);
+#pragma unroll
+            for (int a = 0; a < AP::NP; ++a)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf][a]), as_bf16x8(qv[p][b][hf]),
+                                                                   acc[mb][b], 0, 0, 0);
         }
   }
 #pragma unroll
@@ -827,12 +855,13 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const bf16_t* __restrict__ h,
 // 512-byte row segments (32 lanes per row), stores V row-major and puts it in an LDS tile; then each wave runs the
 // matrix-core product of its 64-column quarter (chunk 4 step + w, as k_write_mfma's chunks) on the tile. The chunk
 // order per wave, the operands and the order of every sum are k_write_mfma's: V, R and the scores are its bits.
-template <int NB>
-__global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h, const bf16_t* __restrict__ x,
-                                                   bf16_t* __restrict__ v, float* __restrict__ r, QTile qt,
+template <typename T, int NB>
+__global__ __launch_bounds__(WG) void k_write_rows(const T* __restrict__ h, const T* __restrict__ x,
+                                                   T* __restrict__ v, float* __restrict__ r, QTile qt,
                                                    float* __restrict__ dots, int64_t n_tok, int d,
                                                    int64_t dots_jstride, float eps) {
   static_assert(WM_MB == 4, "k_write_rows: its 4 waves x 16 rows are the workgroup's 64 tokens");
+  using AP = MfmaA<T>;
   constexpr int NBA = NB > 0 ? NB : 1;
   constexpr int KS = 4 * WM_KC;   // columns per step
   __shared__ f32x4_t s_part[4][WM_MB][NBA][64];
@@ -898,27 +927,30 @@ __global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h,
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float hv[8], xv[8], vv[8];
-      IO<bf16_t>::unpack(IO<bf16_t>::Raw{hc[i]}, hv);
-      IO<bf16_t>::unpack(IO<bf16_t>::Raw{xc[i]}, xv);
+      IO<T>::unpack(typename IO<T>::Raw{hc[i]}, hv);
+      IO<T>::unpack(typename IO<T>::Raw{xc[i]}, xv);
 #pragma unroll
       for (int k = 0; k < 8; ++k) vv[k] = rok[i] ? hv[k] - xv[k] : 0.f;
-      const u32x4 u{pack2(vv[0], vv[1]), pack2(vv[2], vv[3]), pack2(vv[4], vv[5]), pack2(vv[6], vv[7])};
+      T rounded[8];
+      IO<T>::store(rounded, vv);
+      const uint4 ru = *reinterpret_cast<const uint4*>(rounded);
+      const u32x4 u{ru.x, ru.y, ru.z, ru.w};
       // non-temporal: the read that follows streams V[s] with its other sources
       if (rok[i]) __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(v + rof[i] + st * KS + lr * 8));
       tile[16 * w + 2 * i + lh][lr] = make_uint4(u.x, u.y, u.z, u.w);
     }
     __syncthreads();
-    uint4 va[WM_MB][2];
+    uint4 va[WM_MB][2][AP::NP];
 #pragma unroll
     for (int mb = 0; mb < WM_MB; ++mb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const uint4 u = tile[16 * mb + row][w * (WM_KC / 8) + quad + 4 * hf];
-        va[mb][hf] = u;
+        AP::split(u, va[mb][hf]);
         float rv[8];
-        IO<bf16_t>::unpack(IO<bf16_t>::Raw{u}, rv);
+        IO<T>::unpack(typename IO<T>::Raw{u}, rv);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(rv[k], rv[k], ss[mb]);   // k_rstd_bf16's order
+        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(rv[k], rv[k], ss[mb]);   // k_rstd_chunks' order
       }
     if (!WM_DBUF) __syncthreads();   // the tile is read before the next step overwrites it
 #pragma unroll
@@ -929,8 +961,10 @@ __global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h,
         for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
           for (int mb = 0; mb < WM_MB; ++mb)
-            acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf]), as_bf16x8(qv[p][b][hf]),
-                                                                 acc[mb][b], 0, 0, 0);
+#pragma unroll
+            for (int a = 0; a < AP::NP; ++a)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf][a]), as_bf16x8(qv[p][b][hf]),
+                                                                   acc[mb][b], 0, 0, 0);
         }
     if (WM_QPF && NB > 0) {
 #pragma unroll
@@ -982,12 +1016,12 @@ __global__ __launch_bounds__(WG) void k_write_rows(const bf16_t* __restrict__ h,
 
 // the write kernel for bf16 updates: rows streamed whole when d is whole 256-column steps (and the build keeps
 // 64-token workgroups), else the matrix cores' layout; both give the same bits
-template <int NB>
+template <typename T, int NB>
 auto write_kernel(bool rows) {
   if constexpr (WM_ROWS) {
-    if (rows) return &k_write_rows<NB>;
+    if (rows) return &k_write_rows<T, NB>;
   }
-  return &k_write_mfma<NB>;
+  return &k_write_mfma<T, NB>;
 }
 
 // the three bf16 parts of fp32 query values, q = hi + mid + lo, into the operand table (QTile's layout)
@@ -2396,9 +2430,10 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
   // the write kernels' summation order (the same bits as the scale a stacked write stores)
   const unsigned grid = grid_of(cdiv(n_tok, WG / 16), 8192);
   if (dtype == LDR_BF16)
-    hipLaunchKernelGGL(k_rstd_bf16, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(x), r, n_tok, (int)d, eps);
+    hipLaunchKernelGGL(k_rstd_chunks<bf16_t>, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(x), r, n_tok,
+                       (int)d, eps);
   else if (dtype == LDR_F16)
-    hipLaunchKernelGGL(k_rstd_valu<_Float16>, dim3(grid), dim3(WG), 0, st, static_cast<const _Float16*>(x), r, n_tok,
+    hipLaunchKernelGGL(k_rstd_chunks<_Float16>, dim3(grid), dim3(WG), 0, st, static_cast<const _Float16*>(x), r, n_tok,
                        (int)d, eps);
   else
     hipLaunchKernelGGL(k_rstd_valu<float>, dim3(grid), dim3(WG), 0, st, static_cast<const float*>(x), r, n_tok,
@@ -2436,7 +2471,7 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
     return LDR_E_ARG;
   if (nq > LDR_MAX_QUERIES) return LDR_E_SHAPE;
   const bool scores = j_lo < nq;
-  const bool valu = dtype != LDR_BF16 || LDR_WRITE_VALU;   // scores on the vector units, from the fp32 queries
+  const bool valu = dtype == LDR_F32 || LDR_WRITE_VALU;   // scores on the vector units, from the fp32 queries
   if (scores && (!tok_ptr(dots, n_tok) || dots_jstride < n_tok)) return LDR_E_ARG;
   if (scores && ((valu && !q) || (!valu && !qb))) return LDR_E_ARG;
   if (!al16(h) || !al16(x) || !al16(v_out) || (scores && valu && !al16(q)) || (scores && !valu && !al16(qb)))
@@ -2444,16 +2479,21 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
   if (d <= 0 || (d & 7) || d > LDR_MAX_WIDTH) return LDR_E_SHAPE;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!valu) {   // matrix-core scores from the operand table of the nq queries
+  if (!valu) {   // matrix-core scores from the operand table of the nq queries (bf16 and fp16 updates)
     const unsigned grid = (unsigned)cdiv(n_tok, WM_TT);
     const int nbq = (int)query_blocks(nq), b0 = (int)(j_lo / 16);
     const QTile qtl{static_cast<const uint4*>(qb), nbq, b0, (int)j_lo, (int)nq};
     const int nb = scores ? nbq - b0 : 0;
     const bool rows = d % (4 * WM_KC) == 0;   // rows streamed whole when d is whole steps
 #define LDR_WM_LAUNCH(NBV)                                                                                        \
-  hipLaunchKernelGGL((write_kernel<NBV>(rows)), dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(h),      \
-                     static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), r_out, qtl, dots, n_tok, (int)d, \
-                     dots_jstride, eps)
+  if (dtype == LDR_BF16)                                                                                          \
+    hipLaunchKernelGGL((write_kernel<bf16_t, NBV>(rows)), dim3(grid), dim3(WG), 0, st,                            \
+                       static_cast<const bf16_t*>(h), static_cast<const bf16_t*>(x), static_cast<bf16_t*>(v_out), \
+                       r_out, qtl, dots, n_tok, (int)d, dots_jstride, eps);                                       \
+  else                                                                                                            \
+    hipLaunchKernelGGL((write_kernel<_Float16, NBV>(rows)), dim3(grid), dim3(WG), 0, st,                          \
+                       static_cast<const _Float16*>(h), static_cast<const _Float16*>(x),                          \
+                       static_cast<_Float16*>(v_out), r_out, qtl, dots, n_tok, (int)d, dots_jstride, eps)
     switch (nb) {
       case 0: LDR_WM_LAUNCH(0); break;
       case 1: LDR_WM_LAUNCH(1); break;
@@ -2462,7 +2502,7 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
       default: LDR_WM_LAUNCH(4); break;
     }
 #undef LDR_WM_LAUNCH
-  } else {   // vector-unit scores from the fp32 queries (fp32, fp16 updates; bf16 in a build with LDR_WRITE_VALU)
+  } else {   // vector-unit scores from the fp32 queries (fp32 updates; 16-bit ones in a build with LDR_WRITE_VALU)
     const unsigned grid = (unsigned)cdiv(n_tok, WR_TT);
     const float* qj = scores ? q + j_lo * d : nullptr;
     LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_write_dots<T>), dim3(grid), dim3(WG), 0, st,

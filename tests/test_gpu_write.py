@@ -1,8 +1,9 @@
 """The stacked write (DattnStack.write, fused_dattn.py:679-695): V[s] = h - x rounded to the stack dtype (bitwise
 what torch's subtraction gives), R[s] the RMS scale of the rounded update, and the scores of the update against
 the queries of the reads still to come, DOTS[j, s, tok] = q_j . V[s, tok] for j >= s - 1 -- against an fp64 matmul
-of the rounded update (bf16: matrix cores from the queries' three bf16 parts -- k_write_rows for widths that are
-multiples of 256, here 768 and 2048, k_write_mfma for the others; fp32 and fp16: vector units). Ragged token
+of the rounded update (bf16 and fp16: matrix cores from the queries' three bf16 parts, an fp16 update as the exact
+sum of two bf16 values -- k_write_rows for widths that are multiples of 256, here 768 and 2048, k_write_mfma for the
+others; fp32: vector units). Ragged token
 counts, widths below one 64-column chunk and a width with a partial chunk included; every slice is checked
 again after the last write."""
 import pytest
@@ -72,10 +73,12 @@ def test_blend_sum_bitwise(dtype, m, T, d, per_read):
 @pytest.mark.parametrize("d", [256, 2048, 8192])
 @pytest.mark.parametrize("nq", [0, 1, 16, 17, 32, 40, 63])
 @pytest.mark.parametrize("T", [1, 77, 333])
-def test_whole_row_write_is_the_matrix_core_write_bitwise(d, nq, T):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_whole_row_write_is_the_matrix_core_write_bitwise(d, nq, T, dtype):
     """k_write_rows (rows streamed whole, the write for widths that are multiples of 256) against k_write_mfma (the
-    matrix cores' layout) on the same inputs through the C ABI, scoring the last nq of 64 queries (so the first
-    16-query block scored starts inside the table at every nq not a multiple of 16): V, R and the scores bitwise
+    matrix cores' layout), bf16 and fp16 updates, on the same inputs through the C ABI, scoring the last nq of 64
+    queries (so the first 16-query block scored starts inside the table at every nq not a multiple of 16): V, R and
+    the scores bitwise
     equal (the same chunks per wave, operands and order of every sum), the scores within 1e-5 x RMS of an fp64
     product. k_write_mfma comes from the test fixture library built with the alternative kernel shapes
     (LDR_WM_ROWS=0; loopback_amd.build builds it beside the product library)."""
@@ -87,21 +90,21 @@ def test_whole_row_write_is_the_matrix_core_write_bitwise(d, nq, T):
     fns = [L.LIB.ldr_write_dots, other.ldr_write_dots]
     fns[1].restype, fns[1].argtypes = res, args
     gen = torch.Generator().manual_seed(d + 7 * nq + T)
-    h = torch.randn(T, d, generator=gen).to(torch.bfloat16).to(DEV)
-    x = torch.randn(T, d, generator=gen).to(torch.bfloat16).to(DEV)
+    h = torch.randn(T, d, generator=gen).to(dtype).to(DEV)
+    x = torch.randn(T, d, generator=gen).to(dtype).to(DEV)
     NQ = 64                                       # the pass's queries; this write scores the last nq of them
     q = (torch.randn(NQ, d, generator=gen) * 0.3).to(DEV)
     qb = torch.empty(int(L.LIB.ldr_query_parts_elems(NQ, d)), dtype=torch.bfloat16, device=DEV)
     st = torch.cuda.current_stream().cuda_stream
     L.check(L.LIB.ldr_split_queries(q.data_ptr(), NQ, d, qb.data_ptr(), st), "split_queries")
     outs = []
-    print(f"case write layouts d{d} nq{nq} T{T}", flush=True)
+    print(f"case write layouts d{d} nq{nq} T{T} {dtype}", flush=True)
     for fn in fns:
-        v = torch.empty(T, d, dtype=torch.bfloat16, device=DEV)
+        v = torch.empty(T, d, dtype=dtype, device=DEV)
         r = torch.empty(T, device=DEV)
         dots = torch.full((max(nq, 1), T), float("nan"), device=DEV)
         L.check(fn(h.data_ptr(), x.data_ptr(), v.data_ptr(), r.data_ptr(), q.data_ptr(), qb.data_ptr(), NQ,
-                   NQ - nq, dots.data_ptr(), T, d, T, 1e-6, L.BF16, st), "write_dots")
+                   NQ - nq, dots.data_ptr(), T, d, T, 1e-6, lib_dtype(dtype), st), "write_dots")
         torch.cuda.synchronize()
         outs.append((v.cpu(), r.cpu(), dots.cpu()))
     (v1, r1, s1), (v2, r2, s2) = outs
