@@ -1259,6 +1259,9 @@ __global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float
         for (int u = 0; u < NB; ++u)
 #pragma unroll
           for (int v = 0; v < VPT; ++v) raw[u][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i + u]) + roff + R.off(v));
+        // the loads stay ahead of the sums (the scheduler would otherwise interleave them with the fp16 kernels'
+        // mixed-precision multiply-adds, one register set reused, each load then waited for alone)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
           const float w = wrow[i + u];
