@@ -41,6 +41,9 @@
 #ifndef LDR_RF_BIG_GRID
 #define LDR_RF_BIG_GRID 256  // read forward, 512-lane workgroups: one per CU, each takes tiles in turn
 #endif
+#ifndef LDR_RF_HALF_TT
+#define LDR_RF_HALF_TT 1     // read forward: 8-token tiles for rows whose 16-token tile does not fit the staging space
+#endif
 #ifndef LDR_RF_STAGE_U
 #define LDR_RF_STAGE_U 6     // read forward with staged output: sources loaded per batch (the registers of 8 leave
 #endif                       // one wave per SIMD beside the staging code)
@@ -2575,7 +2578,12 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
   // else 256-lane workgroups, 16-token tiles, 64 KiB bursts when they fit
   const bool big = LDR_RF_BIG && (n + 2) * row_bytes >= LDR_RF_BIG_MIN_ROW_BYTES && RF_BIG_LANES / tpr <= RF_BIG_TT &&
                    RF_BIG_TT * row_bytes <= RF_BIG_STAGE;
-  const int tt = big ? RF_BIG_TT : rf_tile(tpr);
+  int tt = big ? RF_BIG_TT : rf_tile(tpr);
+  // rows too long for a tile's output to fit the staging space (fp32 rows of 2048, bf16 rows of 3072 and more): half
+  // the tokens per tile, while that still gives every row slot a row, so the output still goes out in bursts
+  if (LDR_RF_HALF_TT && !big && RF_STAGE_BYTES > 0 && tt * row_bytes > RF_STAGE_BYTES &&
+      (tt / 2) * row_bytes <= RF_STAGE_BYTES && tt / 2 >= WG / tpr)
+    tt /= 2;
   const unsigned grid = big ? grid_of(cdiv(n_tok, tt), LDR_RF_BIG_GRID)
                             : grid_of(cdiv(n_tok, tt), LDR_RF_GRID);   // no tokens: one workgroup writes next_prior
   hipStream_t st = static_cast<hipStream_t>(stream);
