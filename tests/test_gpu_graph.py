@@ -22,7 +22,7 @@ def _chain_forward(cell, h0, D, K, mode):
 
 
 @pytest.mark.parametrize("mode", ["scores", "stack", "list"])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_forward_chain_replays_in_a_graph(mode, dtype):
     from loopback_amd.cell import LoopDeltaAttnRes
     K, R, d, t = 2, 4, 256, 300
@@ -59,7 +59,7 @@ def test_forward_chain_replays_in_a_graph(mode, dtype):
 
 
 @pytest.mark.parametrize("mode", ["scores", "stack", "list"])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_training_chain_replays_in_graphs(mode, dtype):
     """The chain's forward and backward captured as HIP graphs (chain.capture_training): every replay -- with eager
     chains and synchronizations between them, and after the inputs' contents change -- gives the eager pass's final

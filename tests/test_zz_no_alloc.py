@@ -2,12 +2,12 @@
 against the entry points it varies (ldr_read_bwd1 with a caller workspace, then ldr_reduce_rows over the partials),
 through the C ABI on the same inputs: every output bitwise equal (dq, dcbar, the accumulated dr, the wz pairs, the
 blend gradients), on two calls in a row, the second with fewer tokens and a narrower row (the library's array then
-still holds the first call's partials), bf16 and fp32; an empty batch gives a zero query gradient; a repeated call
+still holds the first call's partials), bf16, fp16 and fp32; an empty batch gives a zero query gradient; a repeated call
 leaves the device's free memory unchanged."""
 import pytest
 import torch
 
-from gpu_helpers import DEV
+from gpu_helpers import DEV, lib_dtype
 
 pytestmark = pytest.mark.gpu
 
@@ -31,7 +31,7 @@ def _run(noalloc, n, T, d, dtype, args):
     """One call of either path on fresh output buffers; returns the outputs (on the CPU)."""
     from loopback_amd import _lib as L
     vals, rs, g, gt, p, dots, tc, cbar, c0, dr0 = args
-    dt = L.BF16 if dtype == torch.bfloat16 else L.F32
+    dt = lib_dtype(dtype)
     st = torch.cuda.current_stream().cuda_stream
     vp = L.u64_array([v.data_ptr() for v in vals])
     rp = L.u64_array([r.data_ptr() for r in rs])
@@ -59,7 +59,7 @@ def _run(noalloc, n, T, d, dtype, args):
     return [x.cpu() for x in (dq, dcbar, dr, wz, g_prop, g_h0)]
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_noalloc_backward_pass1_is_the_workspace_one(dtype):
     for call, (n, T, d) in enumerate([(9, 3000, 2048), (5, 333, 1024)]):
         print(f"case noalloc {dtype} call {call}: n{n} T{T} d{d}", flush=True)
