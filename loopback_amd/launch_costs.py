@@ -5,7 +5,8 @@ cost a kernel pays for the stores of the kernel before it (the caches write them
     python -m loopback_amd.launch_costs [--tokens 16384] [--widths 1024 2048] [--out FILE.md]
 
 Rows are update-shaped rows of T x d bf16 (the read forward: n sources, its base and its output; backward pass 1:
-n sources and g; the update gradient: n output gradients, the update, and its two outputs). Needs a GPU.
+n sources and g; the update gradient: n output gradients, the update, and its two outputs; the write: h and x in,
+the update out, scoring n queries). Needs a GPU.
 """
 from __future__ import annotations
 
@@ -59,6 +60,13 @@ class _Bufs:
         self.parts = L.bwd1_parts(T, d)
         self.dq = torch.empty(self.parts, d, device=dev)
         self.st = torch.cuda.current_stream().cuda_stream
+        # the write: a table of 32 read queries and their bf16 parts (the matrix cores' operand), its outputs
+        self.Qw = torch.randn(32, d, device=dev, generator=g) * 0.02
+        self.qb = torch.empty(int(L.LIB.ldr_query_parts_elems(32, d)), dtype=bf, device=dev)
+        L.check(L.LIB.ldr_split_queries(self.Qw.data_ptr(), 32, d, self.qb.data_ptr(), self.st), "split_queries")
+        self.W = torch.empty_like(self.base)
+        self.Rw = torch.empty(T, device=dev)
+        self.dw = torch.empty(32, T, device=dev)
 
     def launcher(self, kind: str, n: int):
         """(fn, rows) for one launch of `kind` over n sources."""
@@ -81,6 +89,10 @@ class _Bufs:
                 self.tc.data_ptr(), self.cbar.data_ptr(), n, self.c0.data_ptr(), n, 1.0, d ** -0.5,
                 self.dcbar.data_ptr(), n, drp, 1, self.WZ.data_ptr(), T, self.dq.data_ptr(), d, None, None, 0.0, T, d,
                 L.BF16, st))), n + 1
+        if kind == "write":   # n: the queries scored, the last n of the table's 32; h = V[0], x = V[1]
+            return (lambda: check(lib.ldr_write_dots(
+                self.V[0].data_ptr(), self.V[1].data_ptr(), self.W.data_ptr(), self.Rw.data_ptr(), self.Qw.data_ptr(),
+                self.qb.data_ptr(), 32, 32 - n, self.dw.data_ptr(), T, d, T, 1e-6, L.BF16, st))), 3
         if kind == "dv_assemble":
             gp = L.u64_array([self.G[i].data_ptr() for i in range(n)])
             wp = L.u64_array([self.WZ[i].data_ptr() for i in range(n)])
@@ -104,10 +116,10 @@ def fit(bufs: _Bufs, kind: str) -> dict:
             "marginal_tbs": row_bytes / (per_row * 1e-6) / 1e12, "times_us": ys, "rows": xs}
 
 
-def after_stores(bufs: _Bufs, n: int = 16, reps: int = 12) -> dict:
-    """One read forward over n sources timed alone (events just around it), after: an idle GPU, a read-only kernel
-    (a sum over 64 MiB), and a torch add writing 64 MiB with ordinary stores."""
-    fn, _ = bufs.launcher("read_fwd", n)
+def after_stores(bufs: _Bufs, kind: str = "read_fwd", n: int = 16, reps: int = 12) -> dict:
+    """One launch of `kind` (n sources; for the write, n queries scored) timed alone (events just around it), after:
+    an idle GPU, a read-only kernel (a sum over 64 MiB), and a torch add writing 64 MiB with ordinary stores."""
+    fn, _ = bufs.launcher(kind, n)
     a, b = bufs.G[n], bufs.G[n + 1] if n + 1 < bufs.G.shape[0] else bufs.G[0]
     c = torch.empty_like(a)
     res = {}
@@ -147,13 +159,19 @@ def main() -> None:
             lines.append(f"| {d} | {kind} | {r['fixed_us']:.1f} | {r['per_row_us']:.2f} | {r['marginal_tbs']:.2f} | "
                          + ", ".join(f"{t:.1f}" for t in r["times_us"]) + " |")
             print(lines[-1], flush=True)
+        wt = {nq: _time_us(bufs.launcher("write", nq)[0]) for nq in (0, 1, 16, 17, 32)}
+        lines.append(f"| {d} | write (3 rows; by queries scored 0, 1, 16, 17, 32) | - | - | "
+                     f"{3 * bufs.T * d * 2 / (wt[0] * 1e-6) / 1e12:.2f} (no scores) | "
+                     + ", ".join(f"{t:.1f}" for t in wt.values()) + " |")
+        print(lines[-1], flush=True)
         if d == max(args.widths):
-            stores = after_stores(bufs)
+            stores = {kind: after_stores(bufs, kind) for kind in ("read_fwd", "write")}
         del bufs
         torch.cuda.empty_cache()
-    lines += ["", f"Read forward (n = 16, d = {max(args.widths)}) timed alone after:", "", "| before | us |", "|---|---|"]
-    lines += [f"| {k} | {v:.1f} |" for k, v in stores.items()]
-    print("\n".join(lines[-5:]), flush=True)
+    lines += ["", f"One launch (d = {max(args.widths)}; the read forward over 16 sources, the write scoring 16 queries) "
+              "timed alone after:", "", "| before | read_fwd us | write us |", "|---|---|---|"]
+    lines += [f"| {k} | {stores['read_fwd'][k]:.1f} | {stores['write'][k]:.1f} |" for k in stores["read_fwd"]]
+    print("\n".join(lines[-6:]), flush=True)
     if args.out:
         with open(args.out, "w") as f:
             f.write("\n".join(lines) + "\n")
