@@ -675,7 +675,7 @@ class _RstdStk(torch.autograd.Function):
             if xc.numel() != stack.n_tok * stack.d or xc.dtype != stack.V.dtype:
                 raise RuntimeError("delta_attnres stacked read: the scale's input must be the stack's update")
             _run("rstd_fwd", _p(xc), _p(r), stack.n_tok, stack.d, float(eps), _dtype_code(xc.dtype),
-                                      _stream(xc.device))
+                 _stream(xc.device))
         ctx.stack, ctx.s, ctx.x = stack, s, x
         return r
 
