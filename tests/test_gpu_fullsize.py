@@ -8,6 +8,8 @@ and inside the kernels:
   * the query gradient is a sum over tokens: HIP(all) == HIP(first half) + HIP(second half) to fp32 round-off, and
     HIP(subset) == oracle(subset);
   * config 2 runs both score modes (stored at the write / computed at the read): equal to bf16 rounding;
+  * update tensors of more than 2^31 elements (4 GiB in bf16): per-token results at both ends of the range against
+    the oracle on those tokens;
   * one stacked read at the headline shape (d=2048, 32 sources): zero query gives out == base and tc == c0 bitwise,
     and a learned query keeps the mass sum_i tc_i == B_s.
 """
@@ -142,3 +144,39 @@ def test_headline_read_identity_and_mass(zero):
         mass = tc.double().sum(-1)
         assert (mass - prior.double().sum()).abs().max().item() <= 1e-5 * prior.sum().item()
         assert (tc - cbar).abs().max().item() > 1e-4         # the query moved the coefficients
+
+
+@pytest.mark.parametrize("mode,glue", [("scores", "1"), ("stack", "0"), ("list", "1")])
+def test_rows_past_2_31_elements(monkeypatch, mode, glue):
+    """Every update tensor of more than 2^31 elements (T = 2^20 + 8 tokens x d = 2048, 4 GiB in bf16): a K = 1, R = 3
+    chain, fwd+bwd (every read an iteration end), in the stacked and list layouts. Offsets past 2^31 elements must be
+    formed in 64 bits everywhere; the per-token results at both ends of the range -- the final state, dL/dh0 and
+    every dL/dD_s -- against the oracle chain on those tokens (the bars of test_fullsize_chain_on_token_subset), and
+    the query gradient finite."""
+    from loopback_amd.chain import ChainConfig, make_inputs, run_chain
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
+    T, d = (1 << 20) + 8, 2048
+    assert T * d > (1 << 31)
+    cfg = ChainConfig("rows-past-2^31", d, 1, 3, 1, T, torch.bfloat16, True, q_std=0.5)
+    print(f"case past 2^31 elements {mode} glue={glue}", flush=True)
+    h0, D, Q, G = make_inputs(cfg, DEV)
+    h, _, grads = run_chain(cfg, h0, D, Q, G, mode)
+    torch.cuda.synchronize()
+    idx = torch.cat([torch.arange(0, 24), torch.arange(T - 40, T)])
+    sub = lambda x: flat(x)[idx.to(x.device)].unsqueeze(0).cpu()
+    states, _, _, _, ref = oracle_chain(cfg.K, cfg.R, sub(h0), [sub(x) for x in D], Q.cpu(), sub(G), beta=cfg.beta,
+                                        eps=cfg.eps, grad=True)
+    st64, _, _, _, ref64 = oracle_chain(cfg.K, cfg.R, sub(h0).double(), [sub(x).double() for x in D],
+                                        Q.cpu().double(), sub(G).double(), beta=cfg.beta, eps=cfg.eps, grad=True)
+
+    def check(hip, r, r64):
+        assert err_norm(hip, r) <= 1e-2
+        assert err_norm(hip, r64) <= 2 * err_norm(r, r64) + 2e-3
+
+    check(sub(h), states[-1], st64[-1])
+    check(sub(grads["h0"]), ref["h0"], ref64["h0"])
+    for a, b, c in zip(grads["D"], ref["D"], ref64["D"]):
+        check(sub(a), b, c)
+    assert torch.isfinite(grads["query"]).all()
+    del h, grads, h0, D, G
+    torch.cuda.empty_cache()
