@@ -146,19 +146,20 @@ def test_headline_read_identity_and_mass(zero):
         assert (tc - cbar).abs().max().item() > 1e-4         # the query moved the coefficients
 
 
-@pytest.mark.parametrize("mode,glue", [("scores", "1"), ("stack", "0"), ("list", "1")])
-def test_rows_past_2_31_elements(monkeypatch, mode, glue):
+@pytest.mark.parametrize("mode,glue,d", [("scores", "1", 2048), ("stack", "0", 2048), ("list", "1", 2048),
+                                         ("scores", "1", 2050)])
+def test_rows_past_2_31_elements(monkeypatch, mode, glue, d):
     """Every update tensor of more than 2^31 elements (T = 2^20 + 8 tokens x d = 2048, 4 GiB in bf16): a K = 1, R = 3
-    chain, fwd+bwd (every read an iteration end), in the stacked and list layouts. Offsets past 2^31 elements must be
-    formed in 64 bits everywhere; the per-token results at both ends of the range -- the final state, dL/dh0 and
-    every dL/dD_s -- against the oracle chain on those tokens (the bars of test_fullsize_chain_on_token_subset), and
-    the query gradient finite."""
+    chain, fwd+bwd (every read an iteration end), in the stacked and list layouts, and at d = 2050 on the any-shape
+    kernels. Offsets past 2^31 elements must be formed in 64 bits everywhere; the per-token results at both ends of
+    the range -- the final state, dL/dh0 and every dL/dD_s -- against the oracle chain on those tokens (the bars of
+    test_fullsize_chain_on_token_subset), and the query gradient finite."""
     from loopback_amd.chain import ChainConfig, make_inputs, run_chain
     monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
-    T, d = (1 << 20) + 8, 2048
+    T = (1 << 20) + 8
     assert T * d > (1 << 31)
     cfg = ChainConfig("rows-past-2^31", d, 1, 3, 1, T, torch.bfloat16, True, q_std=0.5)
-    print(f"case past 2^31 elements {mode} glue={glue}", flush=True)
+    print(f"case past 2^31 elements {mode} glue={glue} d{d}", flush=True)
     h0, D, Q, G = make_inputs(cfg, DEV)
     h, _, grads = run_chain(cfg, h0, D, Q, G, mode)
     torch.cuda.synchronize()
