@@ -341,3 +341,28 @@ def test_lm_layout_contract(monkeypatch, dtype, glue):
     rel = lambda a, b: ((a.double() - b.double()).norm() / b.double().norm().clamp_min(1e-30)).item()
     assert rel(Lw, Ll) <= tol
     assert max(rel(gw[k], gl[k]) for k in gl) <= tol
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("stack,dots", [("1", "1"), ("1", "0"), ("0", "1")])
+def test_lm_training_memory_is_steady(monkeypatch, stack, dots):
+    """A training loop (loss, backward, optimizer step) through every read layout: once the optimizer's state exists
+    (after the first step), the allocated device memory between steps is the same after every step -- nothing of a
+    pass (its stack, the reads' kept output gradients, address tables, scale gradients) outlives it."""
+    monkeypatch.setenv("LOOP_DATTN_STACK", stack)
+    monkeypatch.setenv("LOOP_DATTN_DOTS", dots)
+    torch.manual_seed(5)
+    cfg = LMConfig(**TINY)
+    model = LoopbackLM(cfg).to(device="cuda", dtype=torch.bfloat16)
+    with torch.no_grad():
+        model.read.query.normal_(0, 0.3)
+    opt = make_optimizer(model)
+    ids = ids_for(cfg, b=2, t=256).cuda()
+    print(f"case LM memory stack={stack} dots={dots}", flush=True)
+    seen = []
+    for _ in range(6):
+        loss = train_step(model, opt, ids)
+        del loss
+        torch.cuda.synchronize()
+        seen.append(torch.cuda.memory_allocated())
+    assert len(set(seen[1:])) == 1, seen
