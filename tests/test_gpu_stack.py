@@ -16,7 +16,8 @@ against the oracle chain; mirrors tests/test_dattn_stack.py:68-199 of the refere
   2. eval (no grad) chains, also with more iterations than trained (remapped queries);
   3. memory: a loss kept after its backward holds no stack;
   4. misuse: the reference module's RuntimeError cases and this build's limits;
-  5. streams: a chain on a side stream, fwd+bwd, bitwise the default-stream chain.
+  5. streams: a chain on a side stream, fwd+bwd, bitwise the default-stream chain;
+  6. a NaN or inf in one token's input leaves every other token's result bitwise unchanged.
 """
 import pytest
 import torch
@@ -550,3 +551,25 @@ def test_per_read_rounding_is_the_list_layout_bitwise(monkeypatch, K, R, dtype, 
     assert torch.equal(hs, hl)
     for name, a, b in zip(["h0", "query"] + [f"D{i}" for i in range(cfg.N)], grad_list(gs), grad_list(gl)):
         assert torch.equal(a.cpu(), b.cpu()), name
+
+
+@pytest.mark.parametrize("mode", ["list", "stack", "scores"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_non_finite_input_stays_in_its_token(mode, dtype):
+    """A NaN in one update at one token and an inf in another at a second token (the reference's reads propagate
+    them through that token's scores and softmax): after the no-grad chain every other token's final state is
+    bitwise the clean run's -- no tile, staging burst or score table carries one token's values into another's."""
+    from loopback_amd.chain import ChainConfig, make_inputs, run_chain
+    cfg = ChainConfig("nonfinite-K2R3", 256, 2, 3, 1, 300, dtype, False, q_std=0.5)
+    h0, D, Q, G = make_inputs(cfg, "cpu")
+    print(f"case non-finite {mode} {dtype}", flush=True)
+    clean, _, _ = run_chain(cfg, h0.to(DEV), [x.to(DEV) for x in D], Q.to(DEV), G.to(DEV), mode, grad=False)
+    Db = [x.clone() for x in D]
+    Db[2][0, 17, 5] = float("nan")
+    Db[4][0, 250, 100] = float("inf")
+    dirty, _, _ = run_chain(cfg, h0.to(DEV), [x.to(DEV) for x in Db], Q.to(DEV), G.to(DEV), mode, grad=False)
+    torch.cuda.synchronize()
+    keep = torch.ones(cfg.n_tok, dtype=torch.bool)
+    keep[[17, 250]] = False
+    assert torch.equal(dirty[0, keep.to(DEV)], clean[0, keep.to(DEV)])
+    assert not torch.isfinite(dirty[0, 17]).all() and not torch.isfinite(dirty[0, 250]).all()
