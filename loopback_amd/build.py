@@ -27,6 +27,10 @@ LIB = os.path.join(HERE, "libloopback_read.so")
 # GPU tests can check that the shapes the product library picks give the same bits. Nothing else loads it.
 TEST_LIB_ALT = os.path.join(HERE, "libloopback_read_alt_shapes.so")
 ALT_DEFINES = ["LDR_WM_ROWS=0", "LDR_RF_BIG=0"]
+# A test program: the C ABI used from C alone (tests/c_abi/abi_smoke.c), linked against the product library.
+ABI_SMOKE_SRC = os.path.join(ROOT, "tests", "c_abi", "abi_smoke.c")
+ABI_SMOKE = os.path.join(ROOT, "tests", "c_abi", "abi_smoke")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code (plain fp32 VALU instead).
@@ -68,14 +72,33 @@ def _finish(job) -> None:
     os.replace(tmp, lib)
 
 
+def build_abi_smoke(verbose: bool = True) -> str:
+    """Compile the C test program against include/ and the built library (gcc, the HIP runtime's C API)."""
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no C compiler: the C ABI test program cannot be built")
+    tmp = ABI_SMOKE + ".tmp"
+    cmd = [cc, "-std=c11", "-O2", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
+           f"-I{INCLUDE}", ABI_SMOKE_SRC, f"-L{ROCM}/lib", "-lamdhip64", f"-L{HERE}", "-lloopback_read",
+           "-Wl,-rpath,$ORIGIN/../../loopback_amd", f"-Wl,-rpath,{ROCM}/lib", "-lm", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"the C ABI test program failed to build ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, ABI_SMOKE)
+    return ABI_SMOKE
+
+
 def build(verbose: bool = True, defines=None) -> str:
     """Compile the library (always; a stale build never survives a call) and, beside it, the test fixture
-    TEST_LIB_ALT (the two compiles run in parallel); returns the library's path.
+    TEST_LIB_ALT (the two compiles run in parallel), then the C ABI test program; returns the library's path.
     defines: NAME=VALUE launch settings (see the module docstring)."""
     jobs = [_start(SRC, LIB, verbose, defines),
             _start(SRC, TEST_LIB_ALT, verbose, list(defines or []) + ALT_DEFINES)]
     for job in jobs:
         _finish(job)
+    build_abi_smoke(verbose)
     return LIB
 
 
