@@ -12,7 +12,7 @@ is the configuration's own dtype.
 
 Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / wall time), plus
   roofline      the dominant kernel (most time per pass): the reference dataflow's algorithmic bytes per launch for
-                that kernel (the survey's per-kernel rows: a read moves n sources, its base and its output) / its mean
+                that kernel (per launch: a read moves n sources, its base and its output) / its mean
                 launch duration, from HIP events on the launch stream during the last timed step, against 8 TB/s;
                 the HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE for this source (the committed
                 profile, labelled with the kernel source it was measured on);
@@ -24,7 +24,7 @@ Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / 
                 (--no-extra-configs skips them);
   cpu_baseline  the CPU oracle (the restated reference read, torch on the host cores) on a bounded sample of the
                 same chain (T reduced), fwd+bwd, read-tokens/s and effective GB/s; beside it config 1 (the
-                reference's CPU case: d=768, N=8, 512 tokens, fp32, forward) as the survey plans it.
+                reference's CPU case: d=768, N=8, 512 tokens, fp32, forward).
 """
 from __future__ import annotations
 
@@ -152,9 +152,9 @@ def family_bytes(cfg, mode):
     return fam, ref_total
 
 
-def survey_bytes(cfg, mode):
-    """The reference dataflow's algorithmic bytes per pass of the work each kernel family does (the survey's rows
-    per token, without this build's extras): the write 3N, the reads sum_s (n + 2) (n sources, base, out), backward
+def reference_bytes(cfg, mode):
+    """The reference dataflow's algorithmic bytes per pass of the work each kernel family does (its rows per
+    token, without this build's extras): the write 3N, the reads sum_s (n + 2) (n sources, base, out), backward
     pass 1 sum_s (n + 1); the update gradient does the reference's backward pass 2 and scale-gradient
     accumulation, (N - 1) + N + 2 (S2 - N) + 3N. The fused blend's h0 rows (reads at an iteration end) are
     counted apart (`extra_rows_per_pass`). blend_sum has no counterpart in the reference's kernels."""
@@ -357,16 +357,16 @@ def main():
     ms_per_step = 1e3 * elapsed / args.steps
     ksum = timer.summary()
     fam, ref_bytes = family_bytes(cfg, args.mode)
-    sv, extra_rows = survey_bytes(cfg, args.mode)
+    sv, extra_rows = reference_bytes(cfg, args.mode)
     own_bytes = sum(fam.values())
     dom = max((k for k in fam if k in ksum), key=lambda k: ksum[k]["total_ms"])
     launches = ksum[dom]["launches"]
     mean_s = ksum[dom]["mean_us"] * 1e-6
-    # the survey's bytes per launch where the reference's dataflow is this kernel's (the write, the read, backward
+    # the reference dataflow's bytes per launch where the reference's dataflow is this kernel's (the write, the read, backward
     # pass 1); the update gradient replaces the reference's read-modify-written gradient stack, whose bytes it does
     # not move: its own compulsory bytes there
-    basis = "survey" if dom in sv and dom != "dv_assemble" else "build"
-    alg = (sv[dom] if basis == "survey" else fam[dom]) / launches
+    basis = "reference" if dom in sv and dom != "dv_assemble" else "build"
+    alg = (sv[dom] if basis == "reference" else fam[dom]) / launches
     achieved = alg / mean_s / 1e9
     kernel_ms = sum(v["total_ms"] for v in ksum.values())
     # the committed counter summary is of the configuration's own dtype
@@ -404,7 +404,7 @@ def main():
                   "formula_wall_gbs": ref_bytes / (ms_per_step * 1e-3) / 1e9,
                   "kernels": {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 4),
                                   "gbs": (fam[k] / (v["total_ms"] * 1e-3) / 1e9) if k in fam else None,
-                                  "survey_gbs": (sv[k] / (v["total_ms"] * 1e-3) / 1e9) if k in sv else None}
+                                  "reference_gbs": (sv[k] / (v["total_ms"] * 1e-3) / 1e9) if k in sv else None}
                               for k, v in sorted(ksum.items())},
                   # device memory, as the reference's --bench reports it: the inputs resident before the passes,
                   # and the peak during them (the pass's stacks, saved tensors and gradients on top of the inputs)

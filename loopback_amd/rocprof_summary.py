@@ -160,7 +160,7 @@ def main(argv=None):
     from loopback_amd.chain import CONFIGS
     cfg = CONFIGS[a.config]
     fam_bytes, _ = bench.family_bytes(cfg, a.mode)
-    sv_bytes, _ = bench.survey_bytes(cfg, a.mode)
+    sv_bytes, _ = bench.reference_bytes(cfg, a.mode)
 
     kt, span_ms = trace_pass(a.trace)
     fetch = counter_pass(a.fetch, "FETCH_SIZE")
@@ -175,13 +175,13 @@ def main(argv=None):
         lines += ["Commands:", "", *["    " + c for c in a.commands.split(";;")], ""]
     lines += [f"One pass (the last complete one of the trace): span {span_ms:.2f} ms between pass starts, "
               f"{busy:.2f} ms of kernel time.", "",
-              "Algorithmic GB: this build's compulsory rows (bench.py `family_bytes`); survey GB: the reference "
-              "dataflow's rows for the same work (bench.py `survey_bytes`), each over the family's kernel time. "
-              "The survey's figure for the update gradient counts the reference's read-modify-written gradient "
+              "Algorithmic GB: this build's compulsory rows (bench.py `family_bytes`); reference GB: the "
+              "reference dataflow's rows for the same work (bench.py `reference_bytes`), each over the family's "
+              "kernel time. The reference's figure for the update gradient counts the reference's read-modify-written gradient "
               "stack, bytes this kernel does not move; the last column is the bench line's roofline fraction: the "
-              "survey's bytes where its dataflow is the kernel's, the kernel's own for the update gradient, against "
+              "reference's bytes where its dataflow is the kernel's, the kernel's own for the update gradient, against "
               "8000 GB/s.", "",
-              "| kernel family | launches | total ms | mean us | algorithmic GB | GB/s | survey GB | GB/s (survey) "
+              "| kernel family | launches | total ms | mean us | algorithmic GB | GB/s | reference GB | GB/s (reference) "
               "| of peak (roofline bytes) |", "|---|---|---|---|---|---|---|---|---|"]
     for famname, (n, us) in sorted(kt.items(), key=lambda x: -x[1][1]):
         ab, sb = fam_bytes.get(famname), sv_bytes.get(famname)
