@@ -529,6 +529,51 @@ def test_chain_on_a_side_stream_is_bitwise_the_default_one(mode):
     assert all(torch.equal(a, b) for a, b in zip(g["D"], ref_g["D"]))
 
 
+@pytest.mark.parametrize("mode", ["list", "scores"])
+@pytest.mark.parametrize("d", [512, 100])
+def test_chains_from_two_threads_on_two_streams_at_once(mode, d):
+    """The library keeps no state between calls (its entry points take every address and the stream, ctypes drops
+    the GIL around each): two chains with different inputs, run fwd+bwd three times over from two host threads at
+    once, each on a stream of its own, give the bits each gives alone on the default stream -- at a width of the
+    row-layout kernels and one of the any-shape kernels (whose address tables are copied per call)."""
+    import threading
+    from loopback_amd.chain import ChainConfig, make_inputs, run_chain
+    cfg = ChainConfig(f"threads-{mode}", d, 2, 3, 1, 4096, torch.bfloat16, True, q_std=0.5)
+    h0, D, Q, G = make_inputs(cfg, "cpu")
+    sets = [(h0, D, Q, G), (-h0, D[::-1], Q.flip(0), 2 * G)]
+    sets = [(a.to(DEV), [x.to(DEV) for x in b], c.to(DEV), e.to(DEV)) for a, b, c, e in sets]
+    refs = [run_chain(cfg, *s, mode) for s in sets]
+    torch.cuda.synchronize()
+    outs, errors = [None, None], []
+    start = threading.Barrier(2)
+
+    def work(k):
+        try:
+            stream = torch.cuda.Stream()
+            stream.wait_stream(torch.cuda.default_stream())
+            start.wait()
+            with torch.cuda.stream(stream):
+                for _ in range(3):
+                    outs[k] = run_chain(cfg, *sets[k], mode)
+            stream.synchronize()
+        except Exception as exc:   # reported by the main thread
+            errors.append(exc)
+
+    print(f"case two threads {mode} d{d}", flush=True)
+    threads = [threading.Thread(target=work, args=(k,)) for k in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not any(t.is_alive() for t in threads), "a chain thread did not finish"
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for (h, loss, g), (rh, rloss, rg) in zip(outs, refs):
+        assert torch.equal(h, rh) and torch.equal(loss, rloss)
+        assert torch.equal(g["h0"], rg["h0"]) and torch.equal(g["query"], rg["query"])
+        assert all(torch.equal(a, b) for a, b in zip(g["D"], rg["D"]))
+
+
 @pytest.mark.parametrize("K,R", [(2, 4), (3, 3), (1, 4)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("d", [256, 100])
