@@ -47,7 +47,9 @@ extern "C" {
 #define LDR_E_ALIGN (-3)  /* a vector pointer is not 16-byte aligned (*_any: not element-aligned) */
 #define LDR_E_DTYPE (-4)  /* dtype is none of LDR_F32, LDR_BF16, LDR_F16 */
 
-/* Version of this ABI; bumped on any signature change or change of what an entry point accepts. */
+/* Version of this ABI; bumped on any signature change or change of what an entry point accepts. A caller compares
+ * ldr_abi_version() of the library it loaded with the LDR_ABI_VERSION of the header it was compiled with. */
+#define LDR_ABI_VERSION 15
 int ldr_abi_version(void);
 
 /* Human-readable text for a return code of any entry point (static storage). */

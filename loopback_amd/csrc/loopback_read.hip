@@ -2395,7 +2395,7 @@ __global__ __launch_bounds__(WG) void k_zero(float* __restrict__ p, int64_t n) {
 // ===============================================================================================================
 extern "C" {
 
-int ldr_abi_version(void) { return 15; }
+int ldr_abi_version(void) { return LDR_ABI_VERSION; }
 
 const char* ldr_strerror(int code) {
   switch (code) {

@@ -82,7 +82,7 @@ int main(void) {
   hipStream_t st;
   hip_ok(hipStreamCreate(&st), "hipStreamCreate");
 
-  check(ldr_abi_version() > 0, "ldr_abi_version");
+  check(ldr_abi_version() == LDR_ABI_VERSION, "ldr_abi_version == the header's LDR_ABI_VERSION");
   /* the scale of every source, against its closed form */
   for (int i = 0; i < N; ++i) check(ldr_rstd_fwd(dv[i], dr[i], T, D, eps, LDR_F32, st) == LDR_OK, "ldr_rstd_fwd");
   hip_ok(hipStreamSynchronize(st), "sync");

@@ -40,7 +40,9 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_messages(lib):
-    assert lib.LIB.ldr_abi_version() == lib.ABI_VERSION
+    with open(HEADER) as f:
+        header = int(re.search(r"#define LDR_ABI_VERSION (\d+)", f.read()).group(1))
+    assert lib.LIB.ldr_abi_version() == lib.ABI_VERSION == header
     for code in (0, -1, -2, -3, -4):
         assert lib.LIB.ldr_strerror(code).decode()
 
