@@ -112,6 +112,16 @@ def dtype_name(dtype) -> str:
     return {v: k for k, v in DTYPE_NAMES.items()}[str(dtype).replace("torch.", "")]
 
 
+def with_dtype(cfg, name: str | None):
+    """The configuration with its updates in dtype `name` ("bf16", "fp16", "fp32"; None or its own: unchanged),
+    its name saying so."""
+    import torch
+    own = dtype_name(cfg.dtype)
+    if name is None or name == own:
+        return cfg
+    return dataclasses.replace(cfg, dtype=getattr(torch, DTYPE_NAMES[name]), name=cfg.name.replace(own, name))
+
+
 def elt_bytes(dtype) -> int:
     import torch
     return torch.empty(0, dtype=dtype).element_size()
@@ -334,11 +344,7 @@ def main():
         return
     from loopback_amd.chain import CONFIGS
 
-    cfg = CONFIGS[args.config]
-    if args.dtype is not None and dtype_name(cfg.dtype) != args.dtype:
-        own = dtype_name(cfg.dtype)
-        cfg = dataclasses.replace(cfg, dtype=getattr(torch, DTYPE_NAMES[args.dtype]),
-                                  name=cfg.name.replace(own, args.dtype))
+    cfg = with_dtype(CONFIGS[args.config], args.dtype)
     dev = torch.device("cuda", 0)
     if args.graph:   # the pass replayed from HIP graphs: no Python or launch work per kernel
         elapsed = time_graphed(cfg, args.mode, args.steps, args.warmup)

@@ -138,6 +138,8 @@ def main(argv=None):
     ap.add_argument("--title", default="", help="heading of a --stats-only summary")
     ap.add_argument("--config", default="c4")
     ap.add_argument("--mode", default="scores")
+    ap.add_argument("--dtype", default=None, choices=["bf16", "fp16", "fp32"],
+                    help="the update dtype the run used (bench.py --dtype), when not the configuration's own")
     ap.add_argument("--out", default="profiles")
     ap.add_argument("--commands", default="", help="the commands that produced the inputs (quoted into the summaries)")
     ap.add_argument("--commit", default=None, help="the commit the profiled tree was taken from (recorded as given)")
@@ -158,7 +160,7 @@ def main(argv=None):
     sys.path.insert(0, root)
     import bench   # the byte model the bench line uses
     from loopback_amd.chain import CONFIGS
-    cfg = CONFIGS[a.config]
+    cfg = bench.with_dtype(CONFIGS[a.config], a.dtype)
     fam_bytes, _ = bench.family_bytes(cfg, a.mode)
     sv_bytes, _ = bench.reference_bytes(cfg, a.mode)
 
@@ -168,7 +170,9 @@ def main(argv=None):
     fs = calibration(a.calib_fetch, "FETCH_SIZE")
     ws = calibration(a.calib_write, "WRITE_SIZE")
 
-    tag = a.config if a.mode == "scores" else f"{a.config}_{a.mode}"   # the headline mode keeps the plain name
+    # the headline mode and the configuration's own dtype keep the plain name
+    tag = a.config + ("" if a.mode == "scores" else f"_{a.mode}") + \
+        ("" if cfg.dtype == CONFIGS[a.config].dtype else f"_{bench.dtype_name(cfg.dtype)}")
     busy = sum(v[1] for v in kt.values()) / 1e3
     lines = [f"# Kernel time per chain pass: config {a.config} ({cfg.name}), mode {a.mode}", ""]
     if a.commands:
@@ -218,7 +222,7 @@ def main(argv=None):
     with open(os.path.join(a.out, f"traffic_chain_{tag}.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     with open(os.path.join(a.out, f"traffic_chain_{tag}.txt"), "w") as f:
-        json.dump({"config": a.config, "mode": a.mode,
+        json.dump({"config": a.config, "mode": a.mode, "dtype": bench.dtype_name(cfg.dtype),
                    "source": f"profiles/traffic_chain_{tag}.md (commands and calibration there)",
                    # the kernel source the counters were read on (this tool runs in the same job as the profile)
                    "source_sha256": bench.source_sha256(), "commit": a.commit,
