@@ -131,3 +131,13 @@ def test_build_defines(monkeypatch):
     for bad in (["RF_GRID=1"], ["LDR_X=1; rm"], ["-O0"]):
         with pytest.raises(ValueError):
             _defines(bad)
+
+
+def test_missing_library_fails_at_import():
+    """No CPU fallback: without the built library the drop-in module does not import (the reference's callers then
+    take their own read, as for any import failure, looped_transformer.py:325-330)."""
+    env = dict(os.environ, LOOPBACK_READ_LIB=os.path.join(ROOT, "_no_such_dir", "libloopback_read.so"))
+    proc = subprocess.run([sys.executable, "-c", "import loopback_amd.fused_dattn"], cwd=ROOT, env=env,
+                          capture_output=True, text=True, timeout=300)
+    assert proc.returncode != 0
+    assert "ImportError" in proc.stderr and "no fallback" in proc.stderr, proc.stderr[-2000:]
