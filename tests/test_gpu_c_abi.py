@@ -1,7 +1,9 @@
 """The C ABI from C alone: tests/c_abi/abi_smoke (built by loopback_amd.build against include/loopback_read.h and the
-product library) allocates with hipMalloc and calls the entry points with no Python or torch in the process -- the
-scale against its closed form, the zero-query identity bitwise, the prior's mass kept by the installed coefficients,
-the output from the returned coefficients, and argument errors as negative codes. It runs as a child process."""
+product library) allocates with hipMalloc and calls the entry points with no Python or torch in the process: the
+scale and its gradient, the online and stored-score reads and the any-shape read, backward pass 1 with and without
+a workspace, the list layout's pass 2 and the stacked assembly, the fp32 and bf16 writes, the blends' sum and the
+argument errors, each checked against a closed form, an identity, another entry point or a dot product (the
+program's header lists them). It runs as a child process."""
 import os
 import subprocess
 
