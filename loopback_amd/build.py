@@ -2,6 +2,7 @@
 
     python -m loopback_amd.build                          # compile, print the commands
     python -m loopback_amd.build -D LDR_RF_GRID=768 ...   # with launch settings other than the measured defaults
+    python -m loopback_amd.build -D LDR_WRITE_VALU=1 --out /path/lib.so   # a comparison build of the library alone
 
 The launch settings (the LDR_* constants at the top of csrc/loopback_read.hip: sources per batch, workgroups,
 tile sizes, staging space) are compile-time constants of the kernels; -D NAME=VALUE (or LOOPBACK_READ_DEFINES,
@@ -107,5 +108,11 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser(description="build the loopback_read library for gfx950")
     ap.add_argument("-D", dest="defines", action="append", default=[], metavar="LDR_NAME=VALUE",
                     help="a launch setting of the read kernels (repeatable)")
-    build(defines=ap.parse_args().defines)
+    ap.add_argument("--out", default=None, metavar="PATH",
+                    help="build only the library, to PATH (a comparison build, loaded with LOOPBACK_READ_LIB=PATH)")
+    args = ap.parse_args()
+    if args.out:
+        _finish(_start(SRC, os.path.abspath(args.out), True, args.defines))
+    else:
+        build(defines=args.defines)
     sys.exit(0)

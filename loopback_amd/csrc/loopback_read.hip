@@ -559,6 +559,34 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
 #pragma unroll
   for (int m = 0; m < WR_MQ; ++m) acc[m] = 0.f;
   float ss[2] = {0.f, 0.f};
+  // A chunk's update rows (two vectors of h and x per lane) and query values (up to QV float4 per lane) arrive in
+  // registers; once they are in LDS the next chunk's are requested, before the current chunk is summed, so a
+  // chunk's loads wait behind the previous chunk's products instead of after them.
+  using Raw = typename IO<T>::Raw;
+  constexpr int QV = LDR_MAX_QUERIES * (WR_KC / 4) / WG;
+  static_assert(QV * WG == LDR_MAX_QUERIES * (WR_KC / 4), "write: whole query chunks per lane");
+  Raw hn[2], xn[2];
+  float4 qn[QV];
+  auto fetch = [&](int c0) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int u = tid + WG * e, row = u >> 4, col = c0 + (u & 15) * 8;
+      const int64_t tok = t0 + row;
+      hn[e] = IO<T>::zero();
+      xn[e] = IO<T>::zero();
+      if (tok < n_tok && col < d) {
+        hn[e] = IO<T>::raw(h + tok * (int64_t)d + col);
+        xn[e] = IO<T>::raw(x + tok * (int64_t)d + col);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < QV; ++m) {
+      const int idx = tid + WG * m, jj = idx >> 5, col = c0 + (idx & 31) * 4;
+      qn[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (idx < nq * (WR_KC / 4) && col < d) qn[m] = *reinterpret_cast<const float4*>(q + (int64_t)jj * d + col);
+    }
+  };
+  fetch(0);
   for (int c0 = 0; c0 < d; c0 += WR_KC) {
     // the update chunk: 32 rows x 16 vectors, two vectors per lane
 #pragma unroll
@@ -568,11 +596,12 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
       float vv[8];
       if (tok < n_tok && col < d) {
         float hv[8], xv[8];
-        IO<T>::load(h + tok * (int64_t)d + col, hv);
-        IO<T>::load(x + tok * (int64_t)d + col, xv);
+        IO<T>::unpack(hn[e], hv);
+        IO<T>::unpack(xn[e], xv);
 #pragma unroll
         for (int k = 0; k < 8; ++k) vv[k] = IO<T>::round(hv[k] - xv[k]);
-        IO<T>::store(v + tok * (int64_t)d + col, vv);
+        // non-temporal: the read that follows streams V[s] with its other sources
+        IO<T>::store_nt(v + tok * (int64_t)d + col, vv);
 #pragma unroll
         for (int k = 0; k < 8; ++k) ss[e] = __builtin_fmaf(vv[k], vv[k], ss[e]);   // the scale's order: k_rstd_valu
       } else {
@@ -584,12 +613,12 @@ __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, cons
       dst[1] = make_float4(vv[4], vv[5], vv[6], vv[7]);
     }
     // the query chunk: nq rows x 32 float4
-    for (int idx = tid; idx < nq * (WR_KC / 4); idx += WG) {
-      const int jj = idx >> 5, col = c0 + (idx & 31) * 4;
-      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (col < d) val = *reinterpret_cast<const float4*>(q + (int64_t)jj * d + col);
-      *reinterpret_cast<float4*>(&sq[jj * WR_KP + (idx & 31) * 4]) = val;
+#pragma unroll
+    for (int m = 0; m < QV; ++m) {
+      const int idx = tid + WG * m;
+      if (idx < nq * (WR_KC / 4)) *reinterpret_cast<float4*>(&sq[(idx >> 5) * WR_KP + (idx & 31) * 4]) = qn[m];
     }
+    if (c0 + WR_KC < d) fetch(c0 + WR_KC);   // uniform branch
     __syncthreads();
     if (nq > 0) {
       const int kend = (d - c0) < WR_KC ? (d - c0) : WR_KC;
