@@ -49,7 +49,7 @@ extern "C" {
 
 /* Version of this ABI; bumped on any signature change or change of what an entry point accepts. A caller compares
  * ldr_abi_version() of the library it loaded with the LDR_ABI_VERSION of the header it was compiled with. */
-#define LDR_ABI_VERSION 15
+#define LDR_ABI_VERSION 16
 int ldr_abi_version(void);
 
 /* Human-readable text for a return code of any entry point (static storage). */
@@ -76,10 +76,12 @@ int ldr_rstd_bwd(const void* x, const float* r, const float* gr, void* gx, int64
 /* The write step of update s: v_out = round(h - x); r_out[tok] = rsqrt(mean(v_out^2) + eps) of the rounded update
  * (summed in ldr_rstd_fwd's order, so the same bits); and the scores of the update against the read queries
  * j_lo .. nq - 1 of the pass: dots[(j - j_lo) * dots_jstride + tok] = q[j, :] . v_out[tok, :] (dots points at query
- * j_lo's score slice for source s; j_lo == nq: no scores). bf16 and fp16 updates take the scores on the matrix cores
- * from qb, the operand table ldr_split_queries made of the nq fp32 queries (an fp16 update as the exact sum of two
- * bf16 values); fp32 updates take them on the vector units from q, the fp32 queries [nq, d]. Replaces _write_stk_kernel (fused_dattn.py:561-585, launched at 684-687; its
- * tensor-core product is tl.dot with tf32x3, 583). */
+ * j_lo's score slice for source s; j_lo == nq: no scores). The scores are formed on the matrix cores from qb, the
+ * operand table ldr_split_queries made of the nq fp32 queries, for every dtype: a bf16 update is its own operand, an
+ * fp16 one the exact sum of two bf16 values, an fp32 one the sum of three (the six products of parts whose orders
+ * sum to at most two). q, the fp32 queries [nq, d], is read only by a build with LDR_WRITE_VALU=1 (the scores on
+ * the vector units, a comparison build); it may be NULL otherwise. Replaces _write_stk_kernel (fused_dattn.py:561-585,
+ * launched at 684-687; its tensor-core product is tl.dot with tf32x3, 583). */
 int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, const float* q, const void* qb,
                    int64_t nq, int64_t j_lo, float* dots, int64_t n_tok, int64_t d, int64_t dots_jstride, float eps,
                    int dtype, void* stream);

@@ -12,7 +12,7 @@ import torch  # noqa: F401  -- first: the library must bind to the HIP runtime t
 
 from . import build as _build
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 F32, BF16, F16 = 0, 1, 2
 MAX_SOURCES = 64
 MAX_WIDTH = 8192

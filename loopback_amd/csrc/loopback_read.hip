@@ -1046,6 +1046,159 @@ __global__ __launch_bounds__(WG) void k_write_rows(const T* __restrict__ h, cons
   }
 }
 
+// The write of fp32 updates on the matrix cores. Each stored value v is split into three bf16 parts,
+// v = a0 + a1 + a2 with a0 = bf16(v), a1 = bf16(v - a0), a2 = bf16(v - a0 - a1) (both differences exact in fp32), as
+// the queries are in the operand table; of the nine products a_i q_j the six with i + j <= 2 are accumulated, the
+// others being below 2^-24 of the score's terms. The layout is k_write_mfma's (lane quad g holds columns 8g.. and
+// 32 + 8g.. of its row in each 64-column chunk; the scale sums in k_rstd_chunks' order) with 32-token workgroups
+// (fp32 rows take twice the registers); a chunk's values go to LDS and into their parts before the next chunk's rows
+// are requested into the same registers, and the V tile is stored by 16 lanes per row, non-temporally.
+constexpr int W32_MB = 2, W32_TT = 16 * W32_MB;
+
+__device__ __forceinline__ void split3(const float (&e)[8], uint4 (&a)[3]) {
+  float rem[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) rem[k] = e[k];
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    a[p] = make_uint4(pack2(rem[0], rem[1]), pack2(rem[2], rem[3]), pack2(rem[4], rem[5]), pack2(rem[6], rem[7]));
+    if (p < 2) {
+      float part[8];
+      IO<bf16_t>::unpack(IO<bf16_t>::Raw{a[p]}, part);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) rem[k] -= part[k];   // exact
+    }
+  }
+}
+
+template <int NB>   // NB 16-query blocks scored (from block qt.b0); NB = 0: no scores
+__global__ __launch_bounds__(WG) void k_write_mfma32(const float* __restrict__ h, const float* __restrict__ x,
+                                                     float* __restrict__ v, float* __restrict__ r, QTile qt,
+                                                     float* __restrict__ dots, int64_t n_tok, int d,
+                                                     int64_t dots_jstride, float eps) {
+  constexpr int NBA = NB > 0 ? NB : 1;
+  __shared__ f32x4_t s_part[4][W32_MB][NBA][64];
+  __shared__ float s_ss[4][W32_MB][16];
+  __shared__ float4 s_v[4][W32_TT][WM_KC / 4 + 1];   // each wave's V tile of a chunk (a 16-byte pad per row)
+  const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * W32_TT;
+  f32x4_t acc[W32_MB][NBA];
+#pragma unroll
+  for (int mb = 0; mb < W32_MB; ++mb)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[W32_MB];
+#pragma unroll
+  for (int mb = 0; mb < W32_MB; ++mb) ss[mb] = 0.f;
+  int64_t roff[W32_MB];
+  bool tok_ok[W32_MB];
+#pragma unroll
+  for (int mb = 0; mb < W32_MB; ++mb) {
+    const int64_t tok = t0 + 16 * mb + row;
+    tok_ok[mb] = tok < n_tok;
+    roff[mb] = (tok_ok[mb] ? tok : n_tok - 1) * (int64_t)d;
+  }
+  const int nchunks = (d + WM_KC - 1) / WM_KC;
+  using Raw = IO<float>::Raw;
+  Raw hr[W32_MB][2], xr[W32_MB][2];
+  auto load_hx = [&](int c) {   // a chunk's h and x rows: every 16-token block, the lane's two k-groups
+    const int col = c * WM_KC + quad * WM_QS;
+#pragma unroll
+    for (int mb = 0; mb < W32_MB; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int cc = col + WM_HS * hf < d ? col + WM_HS * hf : 0;
+        hr[mb][hf] = IO<float>::raw(h + roff[mb] + cc);
+        xr[mb][hf] = IO<float>::raw(x + roff[mb] + cc);
+      }
+  };
+  if (w < nchunks) load_hx(w);
+  for (int c = w; c < nchunks; c += 4) {   // wave-uniform trip count
+    const int col = c * WM_KC + quad * WM_QS;
+    uint4 qv[3][NBA][2];   // the chunk's query parts (cache-resident)
+#pragma unroll
+    for (int p = 0; p < 3 * (NB > 0); ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          qv[p][b][hf] = qt.qt[((((int64_t)c * qt.nbq + qt.b0 + b) * 3 + p) * 2 + hf) * 64 + l];
+    uint4 va[W32_MB][2][3];
+#pragma unroll
+    for (int mb = 0; mb < W32_MB; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        float hv[8], xv[8], vv[8];
+        IO<float>::unpack(hr[mb][hf], hv);
+        IO<float>::unpack(xr[mb][hf], xv);
+        const bool ok = tok_ok[mb] && col + WM_HS * hf < d;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) vv[k] = ok ? hv[k] - xv[k] : 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(vv[k], vv[k], ss[mb]);   // k_rstd_chunks' order
+        split3(vv, va[mb][hf]);
+        const int u4 = 2 * (quad + 4 * hf);
+        s_v[w][16 * mb + row][u4] = make_float4(vv[0], vv[1], vv[2], vv[3]);
+        s_v[w][16 * mb + row][u4 + 1] = make_float4(vv[4], vv[5], vv[6], vv[7]);
+      }
+    if (c + 4 < nchunks) load_hx(c + 4);   // uniform branch; the registers are free again
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < W32_TT * (WM_KC / 4) / 64; ++k) {   // 16 lanes per token row
+      const int e = l + 64 * k, t = e >> 4, u = e & 15;
+      const int64_t tok = t0 + t;
+      const int col4 = c * WM_KC + 4 * u;
+      const float4 f = s_v[w][t][u];
+      // non-temporal: the read that follows streams V[s] with its other sources
+      if (tok < n_tok && col4 < d)
+        __builtin_nontemporal_store(u32x4{__float_as_uint(f.x), __float_as_uint(f.y), __float_as_uint(f.z),
+                                          __float_as_uint(f.w)},
+                                    reinterpret_cast<u32x4*>(v + tok * (int64_t)d + col4));
+    }
+    wave_lds_sync();   // the tile is read before the next chunk overwrites it
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int mb = 0; mb < W32_MB; ++mb)   // a_i q_j, i + j <= 2 (columns past d: zero operands on both sides)
+#pragma unroll
+          for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j + i < 3; ++j)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf][i]), as_bf16x8(qv[j][b][hf]),
+                                                                   acc[mb][b], 0, 0, 0);
+  }
+#pragma unroll
+  for (int mb = 0; mb < W32_MB; ++mb) {
+    ss[mb] += __shfl_xor(ss[mb], 16, 64);
+    ss[mb] += __shfl_xor(ss[mb], 32, 64);
+    if (quad == 0) s_ss[w][mb][row] = ss[mb];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) s_part[w][mb][b][l] = acc[mb][b];
+  }
+  __syncthreads();
+  if (tid < 16 * W32_MB) {
+    const int mb = tid >> 4, rr = tid & 15;
+    const float tot = ((s_ss[0][mb][rr] + s_ss[1][mb][rr]) + s_ss[2][mb][rr]) + s_ss[3][mb][rr];
+    const int64_t tok = t0 + tid;
+    if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
+  }
+  if constexpr (NB > 0) {   // the scores (NB = 0 writes none)
+    for (int e = tid; e < W32_MB * NB * 64; e += WG) {
+      const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
+      const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
+      const int jj = 16 * (qt.b0 + b) + (ll & 15);   // the query; dots points at query j_lo's slice
+      if (jj < qt.j_lo || jj >= qt.nq) continue;
+      const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
+      float* dst = dots + (int64_t)(jj - qt.j_lo) * dots_jstride + tok;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (tok + i < n_tok) dst[i] = sum[i];
+    }
+  }
+}
+
 // the write kernel for bf16 updates: rows streamed whole when d is whole 256-column steps (and the build keeps
 // 64-token workgroups), else the matrix cores' layout; both give the same bits
 template <typename T, int NB>
@@ -2470,8 +2623,11 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
   else if (dtype == LDR_F16)
     hipLaunchKernelGGL(k_rstd_chunks<_Float16>, dim3(grid), dim3(WG), 0, st, static_cast<const _Float16*>(x), r, n_tok,
                        (int)d, eps);
-  else
+  else if (LDR_WRITE_VALU)
     hipLaunchKernelGGL(k_rstd_valu<float>, dim3(grid), dim3(WG), 0, st, static_cast<const float*>(x), r, n_tok,
+                       (int)d, eps);
+  else
+    hipLaunchKernelGGL(k_rstd_chunks<float>, dim3(grid), dim3(WG), 0, st, static_cast<const float*>(x), r, n_tok,
                        (int)d, eps);
   return launched();
 }
@@ -2506,7 +2662,7 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
     return LDR_E_ARG;
   if (nq > LDR_MAX_QUERIES) return LDR_E_SHAPE;
   const bool scores = j_lo < nq;
-  const bool valu = dtype == LDR_F32 || LDR_WRITE_VALU;   // scores on the vector units, from the fp32 queries
+  const bool valu = LDR_WRITE_VALU;   // scores on the vector units, from the fp32 queries (a comparison build)
   if (scores && (!tok_ptr(dots, n_tok) || dots_jstride < n_tok)) return LDR_E_ARG;
   if (scores && ((valu && !q) || (!valu && !qb))) return LDR_E_ARG;
   if (!al16(h) || !al16(x) || !al16(v_out) || (scores && valu && !al16(q)) || (scores && !valu && !al16(qb)))
@@ -2514,7 +2670,27 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
   if (d <= 0 || (d & 7) || d > LDR_MAX_WIDTH) return LDR_E_SHAPE;
   if (n_tok == 0) return LDR_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!valu) {   // matrix-core scores from the operand table of the nq queries (bf16 and fp16 updates)
+  if (!valu && dtype == LDR_F32) {   // fp32 updates: split into three bf16 parts on the matrix cores
+    const int nbq = (int)query_blocks(nq), b0 = (int)(j_lo / 16);
+    const QTile qtl{static_cast<const uint4*>(qb), nbq, b0, (int)j_lo, (int)nq};
+    const int nb = scores ? nbq - b0 : 0;
+    const unsigned grid = (unsigned)cdiv(n_tok, W32_TT);
+    const float* hf = static_cast<const float*>(h);
+    const float* xf = static_cast<const float*>(x);
+    float* vf = static_cast<float*>(v_out);
+    switch (nb) {
+      case 0: hipLaunchKernelGGL(k_write_mfma32<0>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
+                                 (int)d, dots_jstride, eps); break;
+      case 1: hipLaunchKernelGGL(k_write_mfma32<1>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
+                                 (int)d, dots_jstride, eps); break;
+      case 2: hipLaunchKernelGGL(k_write_mfma32<2>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
+                                 (int)d, dots_jstride, eps); break;
+      case 3: hipLaunchKernelGGL(k_write_mfma32<3>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
+                                 (int)d, dots_jstride, eps); break;
+      default: hipLaunchKernelGGL(k_write_mfma32<4>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
+                                  (int)d, dots_jstride, eps); break;
+    }
+  } else if (!valu) {   // matrix-core scores from the operand table of the nq queries (bf16 and fp16 updates)
     const unsigned grid = (unsigned)cdiv(n_tok, WM_TT);
     const int nbq = (int)query_blocks(nq), b0 = (int)(j_lo / 16);
     const QTile qtl{static_cast<const uint4*>(qb), nbq, b0, (int)j_lo, (int)nq};

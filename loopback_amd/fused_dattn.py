@@ -503,7 +503,7 @@ class DattnStack:
         # form their scores as they read (the same read, as with LOOP_DATTN_DOTS=0)
         if query is not None and self.fast_d and nq <= L.MAX_QUERIES:
             self.DOTS = torch.empty((max(1, nq), n_steps, b * t), dtype=torch.float32, device=device)
-            if dtype != torch.float32 and nq > 0:   # the queries' bf16 parts: the 16-bit write's matrix-core operand
+            if nq > 0:   # the queries' bf16 parts: the write's matrix-core operand (every update dtype)
                 self.QB = torch.empty(int(L.LIB.ldr_query_parts_elems(nq, d)), dtype=torch.bfloat16, device=device)
                 _run("split_queries", _p(self.Q), nq, d, _p(self.QB), _stream(self.Q.device))
 

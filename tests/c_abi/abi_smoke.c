@@ -12,7 +12,7 @@
  *     dcbar == -g . v_i per token and source (a dot product);
  *   - ldr_read_bwd2_list: dv_i == w_i g + dzr_i q from the returned pairs; ldr_dv_assemble of one read, per-read
  *     rounding: the same bits, and dv_neg == -dv bitwise;
- *   - ldr_write_dots, fp32 (vector units) and bf16 (matrix cores, operand table from ldr_split_queries): the
+ *   - ldr_write_dots, fp32 and bf16 (matrix cores, the operand table from ldr_split_queries): the
  *     update bitwise h - x rounded as torch rounds it, its scale against the closed form, the scores against a
  *     double-precision dot product to 1e-5 x RMS;
  *   - ldr_blend_sum: the sum of beta g_j, to fp32 rounding;
@@ -337,16 +337,16 @@ int main(void) {
     float* dsc = (float*)dev_copy(NULL, sizeof(sc));
     for (int pass = 0; pass < 2; ++pass) {   /* 0: fp32, 1: bf16 */
       const int dt = pass ? LDR_BF16 : LDR_F32;
-      void* qb = NULL;
       if (pass) {
         for (int k = 0; k < T * D; ++k) { h16[k] = to_bf16(h[k]); x16[k] = to_bf16(x[k]); }
         hip_ok(hipMemcpy(dh, h16, sizeof(h16), hipMemcpyHostToDevice), "hipMemcpy h");
         hip_ok(hipMemcpy(dx, x16, sizeof(x16), hipMemcpyHostToDevice), "hipMemcpy x");
-        const int64_t elems = ldr_query_parts_elems(NQ, D);
-        check(elems > 0, "ldr_query_parts_elems");
-        qb = dev_copy(NULL, sizeof(uint16_t) * (size_t)(elems > 0 ? elems : 1));
-        check(ldr_split_queries(dqw, NQ, D, qb, st) == LDR_OK, "ldr_split_queries");
       }
+      /* the queries' bf16 parts: the matrix cores' operand for every update dtype */
+      const int64_t elems = ldr_query_parts_elems(NQ, D);
+      check(elems > 0, "ldr_query_parts_elems");
+      void* qb = dev_copy(NULL, sizeof(uint16_t) * (size_t)(elems > 0 ? elems : 1));
+      check(ldr_split_queries(dqw, NQ, D, qb, st) == LDR_OK, "ldr_split_queries");
       check(ldr_write_dots(dh, dx, dvo, dro, dqw, qb, NQ, 0, dsc, T, D, T, eps, dt, st) == LDR_OK, "ldr_write_dots");
       hip_ok(hipStreamSynchronize(st), "sync");
       to_host(ro, dro, sizeof(ro));
@@ -383,7 +383,7 @@ int main(void) {
           ref[j * T + t] = s;
         }
       check(err_rms(sc, ref, NQ * T) <= 1e-5, pass ? "bf16 write: scores (matrix cores)" : "fp32 write: scores");
-      if (qb) hipFree(qb);
+      hipFree(qb);
     }
     hipFree(dh); hipFree(dx); hipFree(dvo); hipFree(dro); hipFree(dqw); hipFree(dsc);
   }

@@ -1,9 +1,9 @@
 """The stacked write (DattnStack.write, fused_dattn.py:679-695): V[s] = h - x rounded to the stack dtype (bitwise
 what torch's subtraction gives), R[s] the RMS scale of the rounded update, and the scores of the update against
 the queries of the reads still to come, DOTS[j, s, tok] = q_j . V[s, tok] for j >= s - 1 -- against an fp64 matmul
-of the rounded update (bf16 and fp16: matrix cores from the queries' three bf16 parts, an fp16 update as the exact
-sum of two bf16 values -- k_write_rows for widths that are multiples of 256, here 768 and 2048, k_write_mfma for the
-others; fp32: vector units). Ragged token
+of the rounded update (matrix cores from the queries' three bf16 parts; an fp16 update as the exact sum of two bf16
+values, an fp32 one as the sum of three -- for 16-bit updates k_write_rows at widths that are multiples of 256, here
+768 and 2048, k_write_mfma for the others; k_write_mfma32 for fp32). Ragged token
 counts, widths below one 64-column chunk and a width with a partial chunk included; every slice is checked
 again after the last write."""
 import pytest

@@ -92,9 +92,9 @@ def test_argument_checks_before_launch(lib):
     # more queries than a stack holds; a first scored query past the last
     assert L.ldr_write_dots(p4, p4, p4, p4, p4, p4, 65, 0, p4, 16, 64, 16, 1e-6, 1, null) == -2
     assert L.ldr_write_dots(p4, p4, p4, p4, p4, p4, 4, 5, p4, 16, 64, 16, 1e-6, 1, null) == -1
-    # bf16 scores need the queries' operand table, fp32 scores the fp32 queries
+    # scores of every dtype need the queries' operand table (the fp32 queries alone do not do)
     assert L.ldr_write_dots(p4, p4, p4, p4, p4, null, 4, 0, p4, 16, 64, 16, 1e-6, 1, null) == -1
-    assert L.ldr_write_dots(p4, p4, p4, p4, null, p4, 4, 0, p4, 16, 64, 16, 1e-6, 0, null) == -1
+    assert L.ldr_write_dots(p4, p4, p4, p4, p4, null, 4, 0, p4, 16, 64, 16, 1e-6, 0, null) == -1
     # no scores (j_lo == nq): neither is needed
     assert L.ldr_write_dots(null, null, null, null, null, null, 4, 4, null, 0, 64, 0, 1e-6, 1, null) == 0
     assert L.ldr_split_queries(null, 8, 64, p4, null) == -1
