@@ -72,8 +72,8 @@
 #define LDR_B1_WAVE_ROWS 1   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
 #ifndef LDR_WRITE_VALU
-#define LDR_WRITE_VALU 0     // write: 16-bit scores on the vector units (k_write_dots) instead of the matrix cores; a
-#endif                       // comparison build (its scale then follows the fp32 write's summation order)
+#define LDR_WRITE_VALU 0     // write: the scores on the vector units (k_write_dots) instead of the matrix cores, every
+#endif                       // dtype; a comparison build (the scale kernels then follow k_write_dots' summation order)
 #ifndef LDR_WM_ROWS
 #define LDR_WM_ROWS 1        // write: rows streamed whole (d a multiple of 256), else in the matrix cores' layout
 #endif
@@ -413,9 +413,8 @@ constexpr int WR_TT = 32, WR_KC = 128, WR_KP = WR_KC + 4, WR_MQ = 8;
 // (which store it beside the update) or by these kernels (the list layout's rstd, the stacked layout when the write
 // did not store it) -- so both layouts read with bitwise equal scales, and so bitwise equal outputs.
 //
-// 16-bit rows (bf16, fp16): the order of k_write_mfma / k_write_rows. Columns go in 64-column chunks, chunk c to slot
-// w = c mod 4;
-// inside a chunk, quad q takes columns [8q, 8q + 8) and [32 + 8q, 40 + 8q). Partial (w, q) is the fused
+// Every dtype: the order of the matrix-core writes (k_write_mfma, k_write_rows, k_write_mfma32). Columns go in
+// 64-column chunks, chunk c to slot w = c mod 4; inside a chunk, quad q takes columns [8q, 8q + 8) and [32 + 8q, 40 + 8q). Partial (w, q) is the fused
 // multiply-add sum over its chunks in order, its two column groups in order, and their elements in order. Then
 // W_w = (p_w0 + p_w1) + (p_w2 + p_w3), and sum = ((W_0 + W_1) + W_2) + W_3.
 // Here a row takes 16 lanes (lane 4 w + q holds partial (w, q)), 4 rows per wave.
@@ -451,8 +450,8 @@ __global__ __launch_bounds__(WG) void k_rstd_chunks(const T* __restrict__ x, flo
   }
 }
 
-// fp32 rows: the order of k_write_dots. Lane m of a row's 16 takes columns [c0 + 8m, c0 + 8m + 8) for
-// c0 = 0, 128, 256, ... (fused multiply-adds, chunks then elements in order); the 16 partials meet in the butterfly
+// The order of k_write_dots (the vector-unit write of a LDR_WRITE_VALU build). Lane m of a row's 16 takes columns
+// [c0 + 8m, c0 + 8m + 8) for c0 = 0, 128, 256, ... (fused multiply-adds, chunks then elements in order); the 16 partials meet in the butterfly
 // xor 8, 4, 2, 1.
 template <typename T>
 __global__ __launch_bounds__(WG) void k_rstd_valu(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
@@ -2615,20 +2614,16 @@ int ldr_rstd_fwd(const void* x, float* r, int64_t n_tok, int64_t d, float eps, i
                                                 static_cast<const T*>(x), r, n_tok, d, eps))
     return launched();
   }
-  // the write kernels' summation order (the same bits as the scale a stacked write stores)
+  // the write kernels' summation order (the same bits as the scale a stacked write stores): the matrix-core writes'
+  // chunks, or the vector-unit write's in a build that forms the scores there
   const unsigned grid = grid_of(cdiv(n_tok, WG / 16), 8192);
-  if (dtype == LDR_BF16)
-    hipLaunchKernelGGL(k_rstd_chunks<bf16_t>, dim3(grid), dim3(WG), 0, st, static_cast<const bf16_t*>(x), r, n_tok,
-                       (int)d, eps);
-  else if (dtype == LDR_F16)
-    hipLaunchKernelGGL(k_rstd_chunks<_Float16>, dim3(grid), dim3(WG), 0, st, static_cast<const _Float16*>(x), r, n_tok,
-                       (int)d, eps);
-  else if (LDR_WRITE_VALU)
-    hipLaunchKernelGGL(k_rstd_valu<float>, dim3(grid), dim3(WG), 0, st, static_cast<const float*>(x), r, n_tok,
-                       (int)d, eps);
-  else
-    hipLaunchKernelGGL(k_rstd_chunks<float>, dim3(grid), dim3(WG), 0, st, static_cast<const float*>(x), r, n_tok,
-                       (int)d, eps);
+  if (LDR_WRITE_VALU) {
+    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL(k_rstd_valu<T>, dim3(grid), dim3(WG), 0, st,
+                                                static_cast<const T*>(x), r, n_tok, (int)d, eps))
+  } else {
+    LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL(k_rstd_chunks<T>, dim3(grid), dim3(WG), 0, st,
+                                                static_cast<const T*>(x), r, n_tok, (int)d, eps))
+  }
   return launched();
 }
 
@@ -2713,7 +2708,7 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
       default: LDR_WM_LAUNCH(4); break;
     }
 #undef LDR_WM_LAUNCH
-  } else {   // vector-unit scores from the fp32 queries (fp32 updates; 16-bit ones in a build with LDR_WRITE_VALU)
+  } else {   // vector-unit scores from the fp32 queries (a build with LDR_WRITE_VALU)
     const unsigned grid = (unsigned)cdiv(n_tok, WR_TT);
     const float* qj = scores ? q + j_lo * d : nullptr;
     LDR_DTYPE_SWITCH(dtype, hipLaunchKernelGGL((k_write_dots<T>), dim3(grid), dim3(WG), 0, st,
