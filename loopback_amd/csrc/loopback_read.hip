@@ -414,9 +414,10 @@ constexpr int WR_TT = 32, WR_KC = 128, WR_KP = WR_KC + 4, WR_MQ = 8;
 // did not store it) -- so both layouts read with bitwise equal scales, and so bitwise equal outputs.
 //
 // Every dtype: the order of the matrix-core writes (k_write_mfma, k_write_rows, k_write_mfma32). Columns go in
-// 64-column chunks, chunk c to slot w = c mod 4; inside a chunk, quad q takes columns [8q, 8q + 8) and [32 + 8q, 40 + 8q). Partial (w, q) is the fused
-// multiply-add sum over its chunks in order, its two column groups in order, and their elements in order. Then
-// W_w = (p_w0 + p_w1) + (p_w2 + p_w3), and sum = ((W_0 + W_1) + W_2) + W_3.
+// 64-column chunks, chunk c to slot w = c mod 4; inside a chunk, quad q takes columns [8q, 8q + 8) and
+// [32 + 8q, 40 + 8q). Partial (w, q) is the fused multiply-add sum over its chunks in order, its two column groups
+// in order, and their elements in order. Then W_w = (p_w0 + p_w1) + (p_w2 + p_w3), and
+// sum = ((W_0 + W_1) + W_2) + W_3.
 // Here a row takes 16 lanes (lane 4 w + q holds partial (w, q)), 4 rows per wave.
 template <typename T>
 __global__ __launch_bounds__(WG) void k_rstd_chunks(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
