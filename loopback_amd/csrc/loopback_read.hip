@@ -452,8 +452,8 @@ __global__ __launch_bounds__(WG) void k_rstd_chunks(const T* __restrict__ x, flo
 }
 
 // The order of k_write_dots (the vector-unit write of a LDR_WRITE_VALU build). Lane m of a row's 16 takes columns
-// [c0 + 8m, c0 + 8m + 8) for c0 = 0, 128, 256, ... (fused multiply-adds, chunks then elements in order); the 16 partials meet in the butterfly
-// xor 8, 4, 2, 1.
+// [c0 + 8m, c0 + 8m + 8) for c0 = 0, 128, 256, ... (fused multiply-adds, chunks then elements in order); the 16
+// partials meet in the butterfly xor 8, 4, 2, 1.
 template <typename T>
 __global__ __launch_bounds__(WG) void k_rstd_valu(const T* __restrict__ x, float* __restrict__ r, int64_t n_tok,
                                                   int d, float eps) {
