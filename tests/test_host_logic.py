@@ -84,6 +84,22 @@ def test_traffic_formula_of_the_reference_dataflow():
     assert C.algorithmic_bytes_per_token(8, 768, 2, backward=False)["total"] == (3 * 8 + 35 + 14) * 768 * 2
 
 
+def test_per_kernel_bytes_add_up_to_the_formula():
+    """The bench's per-family byte models: the reference dataflow's rows per family sum to the whole-pass formula,
+    and this build's own rows differ from them only by its documented extras (the fused blend's h0 rows, the
+    update gradient's own rows in place of the read-modify-written gradient stack)."""
+    sys.path.insert(0, ROOT)
+    import bench
+    for name in ("c2", "c3", "c4"):
+        cfg = C.CONFIGS[name]
+        ref, extra = bench.reference_bytes(cfg, "scores")
+        fam, ref_total = bench.family_bytes(cfg, "scores")
+        assert sum(ref.values()) == ref_total, name
+        row = cfg.d * torch.empty(0, dtype=cfg.dtype).element_size() * cfg.n_tok
+        assert fam["read_fwd"] - ref["read_fwd"] == extra["read_fwd"] * row, name   # h0 at each iteration end
+        assert fam["write_dots"] == ref["write_dots"] and fam.get("read_bwd1") == ref.get("read_bwd1"), name
+
+
 def test_configs():
     c4 = C.CONFIGS["c4"]
     assert (c4.d, c4.N, c4.n_tok, c4.dtype, c4.backward) == (2048, 32, 16384, torch.bfloat16, True)
