@@ -204,7 +204,8 @@ def _run(name: str, *args) -> None:
 # ---------------------------------------------------------------------------------------------------------------
 def rstd_ref(delta: torch.Tensor, eps: float) -> torch.Tensor:
     """The RMSNorm scale of a source as a torch expression, (b, t, 1) fp32 (fused_dattn.py:197-199). Part of the
-    module's interface for callers; the HIP path below does not use it."""
+    module's interface for callers, and what rstd returns for a tensor that is not on the GPU; the HIP path does not
+    use it."""
     return torch.rsqrt(delta.float().pow(2).mean(-1, keepdim=True) + eps)
 
 
@@ -233,10 +234,14 @@ class _Rstd(torch.autograd.Function):
 
 
 def rstd(delta: torch.Tensor, eps: float) -> torch.Tensor:
-    """The RMSNorm scale of a source, (b, t, 1) fp32, differentiable, computed by the HIP kernels
-    (fused_dattn.py:257-261). GPU tensors only: there is no CPU path in this module."""
-    _require_gpu(delta, "rstd input")
-    return _Rstd.apply(delta, float(eps))
+    """The RMSNorm scale of a source, (b, t, 1) fp32, differentiable (fused_dattn.py:257-261): the HIP kernels for a
+    GPU tensor; for any other tensor rstd_ref, as the reference module returns there. That keeps the reference's
+    callers working on CPU tensors: `combine` takes the scales from rstd before asking fused_read_supported, which is
+    False off the GPU, and then runs its own read (looped_transformer.py:395-404). No read of this module runs on the
+    CPU."""
+    if delta.is_cuda:
+        return _Rstd.apply(delta, float(eps))
+    return rstd_ref(delta, eps)
 
 
 # ---------------------------------------------------------------------------------------------------------------

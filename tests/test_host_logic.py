@@ -28,9 +28,81 @@ def test_supported_is_false_on_cpu():
     assert FD.fused_read_supported(v[0].clone(), v, r, torch.ones(1, 4, 3)) is False
 
 
-def test_rstd_refuses_cpu_tensors():
-    with pytest.raises(RuntimeError, match="GPU"):
-        FD.rstd(torch.randn(2, 3, 64), 1e-6)
+def test_rstd_on_cpu_tensors_is_rstd_ref():
+    """Off the GPU, rstd returns rstd_ref, as the reference module does (fused_dattn.py:257-261): the same tensor
+    bitwise; r x equals torch's own rms_norm (the library routine), and the gradient is the closed form
+    gr (-r^3) x / d (fused_dattn.py:232-254), for every update dtype."""
+    g = torch.Generator().manual_seed(5)
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
+        x = (torch.randn(2, 3, 64, generator=g) * 1.7).to(dtype).requires_grad_()
+        r = FD.rstd(x, 1e-6)
+        assert r.dtype == torch.float32 and r.shape == (2, 3, 1)
+        assert torch.equal(r, FD.rstd_ref(x, 1e-6))
+        xf = x.detach().double()
+        rn = torch.nn.functional.rms_norm(xf, (64,), eps=1e-6)
+        assert torch.allclose(r.double() * xf, rn, rtol=1e-6, atol=1e-6)
+        gr = torch.randn(2, 3, 1, generator=g)
+        r.backward(gr)
+        r64 = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+        want = gr.double() * (-r64 ** 3) * xf / 64
+        tol = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 2e-3}[dtype]
+        assert (x.grad.double() - want).abs().max().item() <= tol * want.abs().max().item()
+
+
+def test_reference_combine_on_cpu_falls_back_to_its_read():
+    """The reference cell with LOOP_DATTN_FUSED=1 on CPU tensors (looped_transformer.py:392-404): it caches
+    `fused.rstd` of each update, asks `fused.fused_read_supported`, gets False and runs its own read. With this
+    module as `fused` that sequence completes (rstd takes CPU tensors), the gate refuses every read, and the chain's
+    final state and gradients are bitwise those of the reference read alone (the oracle's restatement of it; the
+    fallback is the caller's read, never this module's)."""
+    from oracle.reference_read import OracleCell
+    K, R, d, T, eps, beta = 2, 2, 64, 6, 1e-6, 0.75
+    g = torch.Generator().manual_seed(11)
+    h0 = torch.randn(1, T, d, generator=g)
+    D = [torch.randn(1, T, d, generator=g) for _ in range(K * R)]
+    Q = torch.randn(K * R - 1, d, generator=g) * 0.5
+    G = torch.randn(1, T, d, generator=g)
+    refused = []
+
+    def combine(cell, proposal, h0_, deltas, coeffs, prior, l, blk, keys):
+        # the fused branch of the reference cell, with this module as `fused`
+        step = l * K + blk
+        at_end = blk == K - 1
+        base = proposal + beta * (h0_ - proposal) if at_end else proposal
+        one = torch.ones(*proposal.shape[:-1], 1)
+        base_coeffs = one if coeffs is None else torch.cat((coeffs, one), -1)
+        if at_end:
+            base_coeffs = (1 - beta) * base_coeffs
+        if len(keys) < len(deltas):
+            keys.append(FD.rstd(deltas[-1], eps))
+        if len(deltas) > 1:
+            ok = FD.fused_read_supported(base, deltas, keys, base_coeffs)
+            refused.append(not ok)
+            assert step >= 1
+        return cell.combine(proposal, h0_, deltas, coeffs, prior, l, blk, keys=None)
+
+    def run(via_module):
+        q = Q.clone().requires_grad_()
+        h0_ = h0.clone().requires_grad_()
+        Dl = [x.clone().requires_grad_() for x in D]
+        cell = OracleCell(d, R, K, beta, eps, q)
+        h, deltas, keys, coeffs, prior = h0_, [], [], None, None
+        for s in range(K * R):
+            l, blk = divmod(s, K)
+            x = h
+            hs = x + Dl[s]
+            deltas.append(hs - x)
+            if via_module:
+                h, coeffs, prior = combine(cell, hs, h0_, deltas, coeffs, prior, l, blk, keys)
+            else:
+                h, coeffs, prior = cell.combine(hs, h0_, deltas, coeffs, prior, l, blk)
+        (h * G).sum().backward()
+        return [h.detach(), h0_.grad, q.grad] + [x.grad for x in Dl]
+
+    got = run(True)
+    assert refused == [True] * (K * R - 1)
+    for a, b in zip(got, run(False)):
+        assert torch.equal(a, b)
 
 
 def test_stack_refuses_cpu_and_bad_shapes():
