@@ -65,12 +65,20 @@ def _start(src: str, lib: str, verbose: bool, defines) -> tuple:
     return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True), tmp, lib
 
 
-def _finish(job) -> None:
+def _wait(job) -> str | None:
+    """Wait for one compile; install its output, or return its error message."""
     proc, tmp, lib = job
     out, err = proc.communicate()
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}) for {os.path.basename(lib)}:\n{out}\n{err}")
+        return f"hipcc failed ({proc.returncode}) for {os.path.basename(lib)}:\n{out}\n{err}"
     os.replace(tmp, lib)
+    return None
+
+
+def _finish(job) -> None:
+    msg = _wait(job)
+    if msg is not None:
+        raise RuntimeError(msg)
 
 
 def build_abi_smoke(verbose: bool = True) -> str:
@@ -91,15 +99,26 @@ def build_abi_smoke(verbose: bool = True) -> str:
     return ABI_SMOKE
 
 
-def build(verbose: bool = True, defines=None) -> str:
-    """Compile the library (always; a stale build never survives a call) and, beside it, the test fixture
-    TEST_LIB_ALT (the two compiles run in parallel), then the C ABI test program; returns the library's path.
-    defines: NAME=VALUE launch settings (see the module docstring)."""
-    jobs = [_start(SRC, LIB, verbose, defines),
-            _start(SRC, TEST_LIB_ALT, verbose, list(defines or []) + ALT_DEFINES)]
-    for job in jobs:
-        _finish(job)
-    build_abi_smoke(verbose)
+def build(verbose: bool = True, defines=None, fixtures: bool = True) -> str:
+    """Compile the library (always; a stale build never survives a call) and, with `fixtures`, beside it the test
+    fixture TEST_LIB_ALT (the two compiles run in parallel) and then the C ABI test program; returns the library's
+    path. Every compile started is waited for before any error is raised. The library's failure raises; a test
+    fixture's is reported on stderr and does not fail the library's build (the GPU tests that load the fixture then
+    fail on its absence). defines: NAME=VALUE launch settings (see the module docstring)."""
+    jobs = [_start(SRC, LIB, verbose, defines)]
+    if fixtures:
+        jobs.append(_start(SRC, TEST_LIB_ALT, verbose, list(defines or []) + ALT_DEFINES))
+    errors = [_wait(job) for job in jobs]
+    if errors[0] is not None:
+        raise RuntimeError(errors[0])
+    fixture_errors = [e for e in errors[1:] if e is not None]
+    if fixtures and not fixture_errors:
+        try:
+            build_abi_smoke(verbose)
+        except RuntimeError as e:
+            fixture_errors.append(str(e))
+    for e in fixture_errors:
+        print(f"loopback_read build: a test fixture was not built (the library was): {e}", file=sys.stderr)
     return LIB
 
 
