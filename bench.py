@@ -1,14 +1,16 @@
 """Benchmark of the Loopback depth-attention read on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--mode scores] [--no-cpu-baseline]
-                    [--no-extra-configs] [--dtype bf16|fp16|fp32]
+                    [--no-extra-configs] [--dtype bf16|fp16|fp32] [--glue 0|1]
 
 A step is one pass of the read path over one batch: the K x R chain of the benchmark configuration (default
 config 4: d=2048, K=4, R=8 -> N=32 updates, 31 reads, T = 8 x 2048 tokens, bf16 updates, fp32 scores), forward and
 backward -- N writes (with the read-query scores), N-1 reads, their backwards, the updates' gradients -- with the
 synthetic blocks x -> x + D_s and the caller's glue included. Inputs are resident in HBM before timing. --dtype
 times the same configuration with other update dtypes (fp16: the trainer's fp16 mixed precision); the default run
-is the configuration's own dtype.
+is the configuration's own dtype. --glue 0 runs the stacked read as the reference trainer calls it after the import
+swap (FusedDattnReadStk with the caller's glue as torch ops, LOOP_DATTN_FUSE_GLUE=0); the default, 1, is the read
+cell's own path, with that glue inside the read's kernels (FusedCombineStk).
 
 Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / wall time), plus
   roofline      the dominant kernel (most time per pass): the reference dataflow's algorithmic bytes per launch for
@@ -18,8 +20,12 @@ Prints ONE JSON line (rank 0): the headline metric (read tokens/s = T * steps / 
                 profile, labelled with the kernel source it was measured on);
   chain         every library kernel of the pass: this build's compulsory bytes / summed kernel time, and the
                 reference dataflow's bytes (its backward read-modify-writes a gradient stack) over the same time and
-                over the wall time;
+                over the wall time; counter_gbs: the HBM bytes the FETCH_SIZE / WRITE_SIZE counters measured per
+                launch of each family (the committed profile, labelled with the kernel source it was measured on)
+                times this pass's launches, over the same families' kernel time;
   configs       configs 2 and 3 timed the same way (wall time per pass), eager and replayed from HIP graphs;
+                configs 4 and 3 through the drop-in path the reference trainer runs (FusedDattnReadStk with the
+                caller's torch glue: c4_torch_glue, c3_torch_glue);
                 config 5, the LM training step with the read, and the same model as Plain Loop (the read's cost)
                 (--no-extra-configs skips them);
   cpu_baseline  the CPU oracle (the restated reference read, torch on the host cores) on a bounded sample of the
@@ -53,6 +59,10 @@ def parse():
     ap.add_argument("--mode", default="scores", choices=["scores", "stack", "list"])
     ap.add_argument("--dtype", default=None, choices=sorted(DTYPE_NAMES),
                     help="the updates' dtype (default: the configuration's own)")
+    ap.add_argument("--glue", default=None, choices=["0", "1"],
+                    help="LOOP_DATTN_FUSE_GLUE for the timed chain: 0 the caller's glue as torch ops around "
+                         "FusedDattnReadStk (the reference trainer's calls), 1 the glue in the read's kernels "
+                         "(default: the environment's setting, else 1)")
     ap.add_argument("--graph", action="store_true",
                     help="time replays of the pass captured in HIP graphs (no host work per kernel): the forward "
                          "as one graph, a training pass as a forward and a backward graph")
@@ -182,22 +192,56 @@ def source_sha256() -> str:
         return hashlib.sha256(f.read()).hexdigest()
 
 
-def committed_traffic(config, mode, dom):
-    """HBM bytes per launch of `dom` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this
-    configuration (profiles/traffic_chain_<config>.txt, copy-calibrated), labelled with the kernel source it was
-    measured on and whether that is this build's source."""
+@contextlib.contextmanager
+def env_set(name: str, value: str):
+    """os.environ[name] = value inside the block (the read's mode switches are read at every call)."""
+    old = os.environ.get(name)
+    os.environ[name] = value
+    try:
+        yield
+    finally:
+        if old is None:
+            os.environ.pop(name, None)
+        else:
+            os.environ[name] = old
+
+
+def committed_traffic_table(config, mode):
+    """The committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this configuration and read mode with the glue in
+    the kernels (profiles/traffic_chain_<config>.txt, copy-calibrated): HBM bytes per launch of each kernel family,
+    and a label naming the kernel source it was measured on and whether that is this build's source."""
     path = os.path.join(ROOT, "profiles", f"traffic_chain_{config}.txt")
     if not os.path.exists(path):
         return None, None
     with open(path) as f:
         tr = json.load(f)
-    if tr.get("mode") != mode or dom not in tr.get("hbm_bytes_per_launch", {}):
+    if tr.get("mode") != mode or str(tr.get("glue", "1")) != "1":
         return None, None
     measured_on = tr.get("source_sha256")
     label = {"file": os.path.relpath(path, ROOT), "measured_on_source_sha256": measured_on,
              "measured_at_commit": tr.get("commit"), "this_source_sha256": source_sha256(),
              "current": measured_on == source_sha256()}
-    return tr["hbm_bytes_per_launch"][dom], label
+    return tr.get("hbm_bytes_per_launch", {}), label
+
+
+def committed_traffic(config, mode, dom):
+    """HBM bytes per launch of `dom` from committed_traffic_table, with its label."""
+    table, label = committed_traffic_table(config, mode)
+    if table is None or dom not in table:
+        return None, None
+    return table[dom], label
+
+
+def counter_chain(table, ksum):
+    """The chain's HBM GB/s from the counters: per family, the measured bytes per launch times this pass's launches,
+    summed over the families the table holds, over those families' kernel time in this pass."""
+    fams = [k for k in table if k in ksum]
+    if not fams:
+        return None
+    measured = sum(table[k] * ksum[k]["launches"] for k in fams)
+    ms = sum(ksum[k]["total_ms"] for k in fams)
+    return {"counter_gbs": measured / (ms * 1e-3) / 1e9, "counter_bytes_per_pass": measured,
+            "counter_kernel_ms": ms, "families": sorted(fams)}
 
 
 def time_chain(cfg, mode, steps, warmup, timer=None):
@@ -331,6 +375,8 @@ def cpu_baseline(cfg, tokens):
 
 def main():
     args = parse()
+    if args.glue is not None:     # before the read's modules look at it
+        os.environ["LOOP_DATTN_FUSE_GLUE"] = args.glue
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the read shards by tokens "
               "across GPUs (only the query gradient is summed over them), but no multi-GPU figure is produced", file=sys.stderr)
@@ -342,6 +388,7 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
+    from loopback_amd.cell import fuse_glue
     from loopback_amd.chain import CONFIGS
 
     cfg = with_dtype(CONFIGS[args.config], args.dtype)
@@ -375,9 +422,12 @@ def main():
     alg = (sv[dom] if basis == "reference" else fam[dom]) / launches
     achieved = alg / mean_s / 1e9
     kernel_ms = sum(v["total_ms"] for v in ksum.values())
-    # the committed counter summary is of the configuration's own dtype
-    traffic, traffic_label = (committed_traffic(args.config, args.mode, dom) if cfg.dtype == CONFIGS[args.config].dtype
-                              else (None, None))
+    # the committed counter summary is of the configuration's own dtype, with the glue in the kernels
+    own = cfg.dtype == CONFIGS[args.config].dtype and fuse_glue()
+    table, table_label = committed_traffic_table(args.config, args.mode) if own else (None, None)
+    traffic = table.get(dom) if table is not None else None
+    traffic_label = table_label if traffic is not None else None
+    counters = counter_chain(table, ksum) if table is not None else None
 
     line = {
         "metric": ("depth-read tokens/sec (fwd+bwd), d=2048, N=32 stack" if args.config == "c4" else
@@ -394,7 +444,10 @@ def main():
         "dtype": dtype_name(cfg.dtype),
         "data": "synthetic (seeded N(0,1) updates and h0, N(0,0.02^2) queries; blocks x -> x + D_s)",
         "config": {"workload": cfg.name, "d": cfg.d, "K": cfg.K, "R": cfg.R, "N": cfg.N, "tokens": cfg.n_tok,
-                   "mode": args.mode, "backward": cfg.backward, "parallelism": "single GPU"},
+                   "mode": args.mode, "backward": cfg.backward, "parallelism": "single GPU",
+                   "glue": ("caller's glue in the read's kernels (FusedCombineStk)" if fuse_glue() else
+                            "caller's glue as torch ops around FusedDattnReadStk (the reference trainer's calls)")
+                   if args.mode != "list" else "caller's glue as torch ops around FusedDattnRead"},
         "roofline": {"bound": "hbm", "kernel": dom, "bytes_basis": basis, "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_label,
@@ -408,6 +461,11 @@ def main():
                   "reference_formula_bytes_per_token": ref_bytes / cfg.n_tok,
                   "formula_gbs": ref_bytes / (kernel_ms * 1e-3) / 1e9,
                   "formula_wall_gbs": ref_bytes / (ms_per_step * 1e-3) / 1e9,
+                  # measured HBM bytes (FETCH_SIZE + WRITE_SIZE, copy-calibrated) over kernel time
+                  **({"counter_gbs": counters["counter_gbs"], "counter_frac": counters["counter_gbs"] / HBM_PEAK_GBS,
+                      "counter_bytes_per_pass": counters["counter_bytes_per_pass"],
+                      "counter_kernel_ms": counters["counter_kernel_ms"], "counter_families": counters["families"],
+                      "counter_source": table_label} if counters else {}),
                   "kernels": {k: {"launches": v["launches"], "total_ms": round(v["total_ms"], 4),
                                   "gbs": (fam[k] / (v["total_ms"] * 1e-3) / 1e9) if k in fam else None,
                                   "reference_gbs": (sv[k] / (v["total_ms"] * 1e-3) / 1e9) if k in sv else None}
@@ -429,6 +487,25 @@ def main():
                                          "unit": "read-tokens/s", "backward": c.backward,
                                          "formula_wall_gbs": rb / (ms * 1e-3) / 1e9,
                                          "formula_wall_frac": rb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        # the drop-in path the reference trainer runs after the import swap: FusedDattnReadStk with the caller's
+        # glue as torch ops (LOOP_DATTN_FUSE_GLUE=0), stacked with stored scores
+        for key, n_steps, n_warm in (("c4", args.steps, args.warmup), ("c3", 20, 5)):
+            c = CONFIGS[key]
+            with env_set("LOOP_DATTN_FUSE_GLUE", "0"):
+                tg = KernelTimer()
+                el = time_chain(c, "scores", n_steps, n_warm, tg)[0]
+                _, rb = family_bytes(c, "scores")
+            ms = 1e3 * el / n_steps
+            ks = tg.summary()
+            lib_ms = sum(v["total_ms"] for v in ks.values())
+            extra[f"{key}_torch_glue"] = {
+                "workload": c.name, "path": "FusedDattnReadStk with the caller's glue as torch ops "
+                                            "(LOOP_DATTN_FUSE_GLUE=0, stored scores)",
+                "ms_per_step": ms, "value": c.n_tok * n_steps / el, "unit": "read-tokens/s", "backward": c.backward,
+                "steps": n_steps, "warmup": n_warm,
+                "formula_wall_gbs": rb / (ms * 1e-3) / 1e9, "formula_wall_frac": rb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "library_kernel_ms": lib_ms, "other_ms": ms - lib_ms,
+                "kernels_ms": {k: round(v["total_ms"], 4) for k, v in sorted(ks.items())}}
         # config 2 runs both score modes: the table stored at the write (above) and the reads forming the scores
         # as they stream (LOOP_DATTN_DOTS=0, the stack without a score table)
         c = CONFIGS["c2"]

@@ -140,6 +140,9 @@ def main(argv=None):
     ap.add_argument("--mode", default="scores")
     ap.add_argument("--dtype", default=None, choices=["bf16", "fp16", "fp32"],
                     help="the update dtype the run used (bench.py --dtype), when not the configuration's own")
+    ap.add_argument("--glue", default="1", choices=["0", "1"],
+                    help="LOOP_DATTN_FUSE_GLUE of the profiled run (bench.py --glue): 0 names the summaries "
+                         "*_torchglue and counts the bytes of the torch-glue path")
     ap.add_argument("--out", default="profiles")
     ap.add_argument("--commands", default="", help="the commands that produced the inputs (quoted into the summaries)")
     ap.add_argument("--commit", default=None, help="the commit the profiled tree was taken from (recorded as given)")
@@ -161,8 +164,9 @@ def main(argv=None):
     import bench   # the byte model the bench line uses
     from loopback_amd.chain import CONFIGS
     cfg = bench.with_dtype(CONFIGS[a.config], a.dtype)
-    fam_bytes, _ = bench.family_bytes(cfg, a.mode)
-    sv_bytes, _ = bench.reference_bytes(cfg, a.mode)
+    with bench.env_set("LOOP_DATTN_FUSE_GLUE", a.glue):   # the byte model of the profiled run's glue setting
+        fam_bytes, _ = bench.family_bytes(cfg, a.mode)
+        sv_bytes, _ = bench.reference_bytes(cfg, a.mode)
 
     kt, span_ms = trace_pass(a.trace)
     fetch = counter_pass(a.fetch, "FETCH_SIZE")
@@ -172,9 +176,12 @@ def main(argv=None):
 
     # the headline mode and the configuration's own dtype keep the plain name
     tag = a.config + ("" if a.mode == "scores" else f"_{a.mode}") + \
-        ("" if cfg.dtype == CONFIGS[a.config].dtype else f"_{bench.dtype_name(cfg.dtype)}")
+        ("" if cfg.dtype == CONFIGS[a.config].dtype else f"_{bench.dtype_name(cfg.dtype)}") + \
+        ("" if a.glue == "1" or a.mode == "list" else "_torchglue")
     busy = sum(v[1] for v in kt.values()) / 1e3
-    lines = [f"# Kernel time per chain pass: config {a.config} ({cfg.name}), mode {a.mode}", ""]
+    glue = "" if a.mode == "list" else (", the caller's glue as torch ops (LOOP_DATTN_FUSE_GLUE=0)" if a.glue == "0"
+                                        else ", the caller's glue in the read's kernels")
+    lines = [f"# Kernel time per chain pass: config {a.config} ({cfg.name}), mode {a.mode}{glue}", ""]
     if a.commands:
         lines += ["Commands:", "", *["    " + c for c in a.commands.split(";;")], ""]
     lines += [f"One pass (the last complete one of the trace): span {span_ms:.2f} ms between pass starts, "
@@ -200,7 +207,7 @@ def main(argv=None):
         f.write("\n".join(lines) + "\n")
 
     per_launch = {}
-    lines = [f"# HBM traffic per kernel: config {a.config} ({cfg.name}), mode {a.mode}, one pass", ""]
+    lines = [f"# HBM traffic per kernel: config {a.config} ({cfg.name}), mode {a.mode}{glue}, one pass", ""]
     if a.commands:
         lines += ["Commands:", "", *["    " + c for c in a.commands.split(";;")], ""]
     lines += [f"Calibration: a 1 GiB device-to-device copy reads FETCH_SIZE = {(COPY_BYTES / 1024) / fs:.0f} KiB and "
@@ -222,7 +229,7 @@ def main(argv=None):
     with open(os.path.join(a.out, f"traffic_chain_{tag}.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
     with open(os.path.join(a.out, f"traffic_chain_{tag}.txt"), "w") as f:
-        json.dump({"config": a.config, "mode": a.mode, "dtype": bench.dtype_name(cfg.dtype),
+        json.dump({"config": a.config, "mode": a.mode, "glue": a.glue, "dtype": bench.dtype_name(cfg.dtype),
                    "source": f"profiles/traffic_chain_{tag}.md (commands and calibration there)",
                    # the kernel source the counters were read on (this tool runs in the same job as the profile)
                    "source_sha256": bench.source_sha256(), "commit": a.commit,

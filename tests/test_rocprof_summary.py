@@ -91,3 +91,45 @@ def test_traffic_file_per_launch_bytes(tmp_path):
     assert tr["hbm_bytes_per_launch"]["read_fwd"] == pytest.approx((500_000 * 2 + 100_000) * 1024)
     assert tr["commit"] == "abc1234" and tr["dtype"] == "bf16"
     assert os.path.exists(out / "kernels_chain_c4.md") and os.path.exists(out / "traffic_chain_c4.md")
+    assert tr["glue"] == "1"
+
+
+def test_torch_glue_summaries_are_named_apart(tmp_path):
+    """--glue 0 (a profile of bench.py --glue 0) writes *_torchglue summaries, counted with the torch-glue path's
+    bytes (no iteration-end h0 rows, no blend sum), and leaves the process's environment as it was."""
+    kt, pf, pw, cf, cw = (tmp_path / f"{n}.csv" for n in ("kt", "pf", "pw", "cf", "cw"))
+    _trace(kt)
+    _counter(pf, "FETCH_SIZE", lambda name: 10.0)
+    _counter(pw, "WRITE_SIZE", lambda name: 10.0)
+    for path, counter, kib in ((cf, "FETCH_SIZE", 524288.0), (cw, "WRITE_SIZE", 1048576.0)):
+        _write_csv(path, ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"],
+                   [{"Dispatch_Id": 1, "Kernel_Name": "__amd_rocclr_copyBuffer", "Counter_Name": counter,
+                     "Counter_Value": kib}])
+    out = tmp_path / "profiles"
+    out.mkdir()
+    before = os.environ.get("LOOP_DATTN_FUSE_GLUE")
+    RS.main(["--trace", str(kt), "--fetch", str(pf), "--write", str(pw), "--calib-fetch", str(cf),
+             "--calib-write", str(cw), "--config", "c4", "--mode", "scores", "--glue", "0", "--out", str(out)])
+    assert os.environ.get("LOOP_DATTN_FUSE_GLUE") == before
+    assert json.loads((out / "traffic_chain_c4_torchglue.txt").read_text())["glue"] == "0"
+    text = (out / "kernels_chain_c4_torchglue.md").read_text()
+    assert "torch ops" in text
+    # the read forward's bytes without the blend's h0 rows: sum_s (n + 2) rows of 64 MiB
+    N, row = 32, 2 * 2048 * 16384
+    reads = (N * (N + 1) // 2 - 1 + 2 * (N - 1)) * row
+    assert f"| {reads / 1e9:.2f} |" in text
+
+
+def test_bench_counter_chain_arithmetic():
+    """bench.counter_chain: measured bytes per launch x this pass's launches, over the same families' kernel time;
+    families the table lacks (or the pass lacks) are left out of both sums."""
+    import bench
+    table = {"read_fwd": 2e9, "read_bwd1": 1e9, "blend_sum": 5e8}
+    ksum = {"read_fwd": {"launches": 3, "total_ms": 1.0}, "read_bwd1": {"launches": 2, "total_ms": 0.5},
+            "reduce_rows": {"launches": 1, "total_ms": 0.25}}
+    c = bench.counter_chain(table, ksum)
+    assert c["families"] == ["read_bwd1", "read_fwd"]
+    assert c["counter_bytes_per_pass"] == pytest.approx(3 * 2e9 + 2 * 1e9)
+    assert c["counter_kernel_ms"] == pytest.approx(1.5)
+    assert c["counter_gbs"] == pytest.approx(8e9 / 1.5e-3 / 1e9)
+    assert bench.counter_chain({"x": 1.0}, ksum) is None
