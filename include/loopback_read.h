@@ -163,7 +163,8 @@ int ldr_read_bwd1(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const
  * No counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops, harnesses that forbid allocation). The partials go to a device array the library holds on
  * each GPU it runs on (LDR_B1_GRID x LDR_MAX_WIDTH fp32: 512 x 8192 x 4 B = 16 MiB with the default launch settings,
- * kept until the process ends; its address is looked up once per device on the first call there). Calls that
+ * kept until the process ends; its address is looked up once per device on the first call there, so under HIP graph
+ * capture make one call on that device first, outside capture -- an empty batch, n_tok = 0, suffices). Calls that
  * overlap on one GPU (on two streams, or from two threads) share that array and race: serialize them. Returns
  * LDR_E_SHAPE for a width or batch whose partials would not fit the array (none with d <= LDR_MAX_WIDTH at the
  * default launch settings). */

@@ -320,6 +320,44 @@ def test_proposal_gradient_through_update_kernel(K, R, dtype):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("case", ["other_eps", "copy"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode,glue", [("scores", "1"), ("scores", "0"), ("stack", "1"), ("stack", "0")])
+def test_separate_scale_node_chain_matches_oracle(monkeypatch, case, dtype, mode, glue):
+    """Scales the stack cannot take from the write go through the separate scale node (_RstdStk, the reference's
+    DattnStack.rstd node, fused_dattn.py:698-722): "other_eps" asks stack.rstd for an eps other than the stack's
+    (0.05 against 1e-6: the node recomputes R[s], and the reads' scores follow it), "copy" for the scale of a copy of
+    the update (the node keeps the write's R[s]). Its backward assembles the update's gradient and hands (dv, -dv)
+    and any proposal gradient a fused combine gave it to the write's backward (stack.neg). The chain, both glue
+    settings (with glue in the kernels the proposal's gradient goes through that hand-off), both score modes,
+    against the oracle chain whose keys use the scales' eps: the chain bars of test_chain_matches_oracle for the
+    final state and every gradient (h0, every D_s, the query), and nothing handed over is left behind."""
+    from loopback_amd import fused_dattn as FD
+    from loopback_amd.chain import ChainConfig, make_cell, make_inputs
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
+    key_eps = 0.05 if case == "other_eps" else 1e-6
+    cfg = ChainConfig(f"rstdstk-{case}", 256, 2, 3, 1, 384, dtype, True, eps=key_eps, q_std=0.5)
+    print(f"case separate scale node {case} {dtype} {mode} glue={glue}", flush=True)
+    h0c, Dc, Qc, Gc = make_inputs(cfg, "cpu")
+    h0 = h0c.to(DEV).requires_grad_()
+    D = [x.to(DEV).requires_grad_() for x in Dc]
+    cell = make_cell(cfg, Qc.to(DEV))
+    stack = FD.DattnStack(cfg.N, h0.shape, dtype, DEV, query=cell.query if mode == "scores" else None, eps=1e-6)
+    h, deltas, keys, coeffs, prior = h0, [], [], None, None
+    for s in range(cfg.N):
+        l, blk = divmod(s, cfg.K)
+        x = h
+        hs = x + D[s]
+        deltas.append(stack.write(s, hs, x))
+        keys.append(stack.rstd(s, deltas[-1].clone() if case == "copy" else deltas[-1], key_eps))
+        assert type(keys[-1].grad_fn).__name__ == "_RstdStkBackward"
+        h, coeffs, prior = cell.combine(hs, h0, deltas, coeffs, prior, l, blk, keys=keys, stack=stack)
+    (h.float() * Gc.to(DEV)).sum().backward()
+    torch.cuda.synchronize()
+    assert not stack.gadd and not stack.neg
+    check_chain(h.detach().cpu(), {"h0": h0.grad, "D": [x.grad for x in D], "query": cell.query.grad}, cfg)
+
+
 def test_stack_and_list_read_bitwise_on_shared_scales():
     """One read, both layouts, the same sources and the same scale tensors: the same kernels give the same bits."""
     from loopback_amd import fused_dattn as FD
