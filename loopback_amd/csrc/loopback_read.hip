@@ -71,6 +71,9 @@
 #ifndef LDR_B1_WAVE_ROWS
 #define LDR_B1_WAVE_ROWS 1   // backward pass 1: prefer rows inside one wave (no LDS in the row reductions)
 #endif
+#ifndef LDR_B1_GD64
+#define LDR_B1_GD64 1        // backward pass 1 with fp32 updates: g . v_i and the scalars formed from it in fp64
+#endif
 #ifndef LDR_WRITE_VALU
 #define LDR_WRITE_VALU 0     // write: the scores on the vector units (k_write_dots) instead of the matrix cores, every
 #endif                       // dtype; a comparison build (the scale kernels then follow k_write_dots' summation order)
@@ -131,6 +134,7 @@ static_assert(LDR_RF_VPT >= 0 && LDR_RF_VPT <= 4 && LDR_AS_VPT >= 0 && LDR_AS_VP
 static_assert(LDR_AS_STORES >= 0 && LDR_AS_STORES <= 3, "update gradient: LDR_AS_STORES is 0..3");
 static_assert(LDR_AS_RB >= 1 && LDR_AS_JB >= 1, "update gradient: at least one row per lane and one read per batch");
 static_assert(LDR_B1_C >= 0 && LDR_B1_C <= 8, "backward pass 1: 0 (by vectors per lane) or 1..8 sources per chunk");
+static_assert(LDR_B1_GD64 == 0 || LDR_B1_GD64 == 1, "backward pass 1: LDR_B1_GD64 is 0 or 1");
 static_assert(LDR_ON_PD >= 1 && LDR_ON_WAVES >= 1, "online read: at least one source in flight, one wave per SIMD");
 static_assert(LDR_AS_GRID >= 1 && LDR_RF_GRID >= 1 && LDR_ON_GRID >= 1 && LDR_B1_GRID >= 1 && LDR_RF_BIG_GRID >= 1,
               "grids: >= 1 workgroup");
@@ -318,6 +322,40 @@ __device__ __forceinline__ float lanes_reduce(float x, int g, Op op) {
 struct AddOp { __device__ __forceinline__ float operator()(float a, float b) const { return a + b; } };
 struct MaxOp { __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); } };
 
+// The same lane-group sum for fp64 values: each level moves the two 32-bit halves with the same DPP or row swap
+// (the halves of one value travel together), and adds in fp64.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double x) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double join_d(unsigned lo, unsigned hi) {
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | (uint64_t)lo);
+}
+__device__ __forceinline__ double lanes_sum_d(double x, int g) {
+  if (g >= 2) x += dpp_d<0xB1>(x);
+  if (g >= 4) x += dpp_d<0x4E>(x);
+  if (g >= 8) x += dpp_d<0x141>(x);
+  if (g >= 16) x += dpp_d<0x140>(x);
+  if (g >= 32) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
+    const auto sl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto sh = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    x = join_d((unsigned)sl[0], (unsigned)sh[0]) + join_d((unsigned)sl[1], (unsigned)sh[1]);
+  }
+  if (g >= 64) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
+    const auto sl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto sh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    x = join_d((unsigned)sl[0], (unsigned)sh[0]) + join_d((unsigned)sl[1], (unsigned)sh[1]);
+  }
+  return x;
+}
+
 // Sum NV values over the tpr lanes of a row (tpr a power of two); every lane of the row ends with the totals,
 // bitwise equal on all of them. tpr <= 64: the row is an aligned lane group of one wave. tpr > 64: the row spans
 // tpr/64 waves and the wave totals meet in `red` (4 * NV floats of LDS); the whole workgroup must then call
@@ -339,6 +377,30 @@ __device__ __forceinline__ void row_sum(float (&x)[NV], int tpr, float* red) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       float s = 0.f;
+      for (int k = 0; k < nw; ++k) s += red[(first + k) * NV + j];
+      x[j] = s;
+    }
+  }
+}
+
+// row_sum in fp64 (the wave totals meet in `red`, 4 * NV doubles of LDS, when the row spans several waves)
+template <int NV>
+__device__ __forceinline__ void row_sum_d(double (&x)[NV], int tpr, double* red) {
+  const int w = tpr < 64 ? tpr : 64;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) x[j] = lanes_sum_d(x[j], w);
+  if (tpr > 64) {
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) red[wave * NV + j] = x[j];
+    }
+    __syncthreads();
+    const int nw = tpr >> 6, first = (wave / nw) * nw;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      double s = 0.0;
       for (int k = 0; k < nw; ++k) s += red[(first + k) * NV + j];
       x[j] = s;
     }
@@ -1692,8 +1754,16 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
                                              int d, int tpr, int tt) {
   // LDS: six [TT_MAX][SP] scalar planes (probability, scale, upstream tc gradient, g.v, raw score then dr, and
   // tc - cbar) during the tiles; the first d floats are reused for the workgroup's dq sum at the end.
+  // fp32 updates: g . v_i summed in fp64 (each product rounded to fp32, the d-term sum and the lane reduction in
+  // fp64; the products exact would take the registers of a second wave) and gp, Sacc formed from it in fp64. The
+  // query gradient of a chain's last reads sums p (gp_i - Sacc) r v over every token, and the fp32 sum of g . v was
+  // the largest error left in it at the headline shape in fp32 (1.05e-5 of its RMS; 6.2e-6 with this, 3.6e-6 with
+  // the row-local sums below).
+  constexpr bool GD64 = LDR_B1_GD64 && std::is_same<T, float>::value;
+  typedef typename std::conditional<GD64, double, float>::type Acc;
   __shared__ float lds[6 * TT_MAX * SP];
-  __shared__ float s_sacc[TT_MAX], s_c0[MAXS], s_lc[MAXS], s_M, red[4 * C];
+  __shared__ float s_sacc[TT_MAX], s_c0[MAXS], s_lc[MAXS], s_M;
+  __shared__ Acc red[4 * C];
   float* s_p = lds;
   float* s_r = lds + 1 * TT_MAX * SP;
   float* s_gt = lds + 2 * TT_MAX * SP;
@@ -1761,35 +1831,38 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
           if (g_prop) IO<T>::store(g_prop + roff + R.c8(v) * 8, gpv);
         }
       }
-      // dq of the row is sum_i p_i r_i (gp_i - Sacc) v_i: the gp part goes straight into the running dq, the
-      // Sacc part (Sacc known only after the last source) through b = sum_i p_i r_i v_i
-      float b[VPT][8];
+      // dq of the row is sum_i p_i r_i (gp_i - Sacc) v_i, with Sacc known only after the last source: the row's
+      // a = sum_i p_i r_i gp_i v_i and b = sum_i p_i r_i v_i, then a - Sacc b joins the running dq. The two terms
+      // largely cancel, so they meet in the row's own registers before the (much longer) running sum takes the
+      // difference: adding a to the running dq directly and subtracting Sacc b there was measured to leave twice
+      // the fp32 error in the headline chain's query gradient.
+      float a[VPT][8], b[VPT][8];
 #pragma unroll
       for (int v = 0; v < VPT; ++v)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) b[v][k] = 0.f;
-      float sacc = 0.f;
+        for (int k = 0; k < 8; ++k) a[v][k] = b[v][k] = 0.f;
+      Acc sacc = 0;
       // one source's share once its g.v is known: the scalars, the two accumulators, g.v to LDS
-      auto take = [&](int i, float gd, const typename IO<T>::Raw (&rw)[VPT]) {
+      auto take = [&](int i, Acc gd, const typename IO<T>::Raw (&rw)[VPT]) {
         const float p = s_p[rr * SP + i];
         const float pr = p * s_r[rr * SP + i];
-        const float gp = M * (gd + s_gt[rr * SP + i]);
-        sacc += p * gp;
-        const float alpha = pr * gp;
+        const Acc gp = (Acc)M * (gd + (Acc)s_gt[rr * SP + i]);
+        sacc += (Acc)p * gp;
+        const float alpha = (float)((Acc)pr * gp);
 #pragma unroll
         for (int v = 0; v < VPT; ++v) {
           float e[8];
           IO<T>::unpack(rw[v], e);
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
-            dqa[v][k] += alpha * e[k];
+            a[v][k] += alpha * e[k];
             b[v][k] += pr * e[k];
           }
         }
-        if (R.lr == 0) s_gd[rr * SP + i] = gd;
+        if (R.lr == 0) s_gd[rr * SP + i] = (float)gd;
       };
       auto dotc = [&](const typename IO<T>::Raw (&rw)[VPT]) {
-        float acc = 0.f;
+        Acc acc = 0;
 #pragma unroll
         for (int v = 0; v < VPT; ++v) {
           float e[8];
@@ -1797,9 +1870,15 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
           float gvv[8];
           IO<T>::unpack(gq[v], gvv);
 #pragma unroll
-          for (int k = 0; k < 8; ++k) acc += gvv[k] * e[k];
+          for (int k = 0; k < 8; ++k) acc += (Acc)(gvv[k] * e[k]);
         }
         return acc;
+      };
+      auto rsum = [&](auto& pd) {
+        if constexpr (GD64)
+          row_sum_d(pd, tpr, red);
+        else
+          row_sum(pd, tpr, red);
       };
       auto load_chunk = [&](int i0, typename IO<T>::Raw (&rw)[C][VPT]) {
 #pragma unroll
@@ -1814,10 +1893,10 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
       for (; i0 < nfull; i0 += C) {   // the next chunk's loads in flight while this one is reduced
         typename IO<T>::Raw nxt[C][VPT];
         if (i0 + C < nfull) load_chunk(i0 + C, nxt);
-        float pd[C];
+        Acc pd[C];
 #pragma unroll
         for (int c = 0; c < C; ++c) pd[c] = dotc(cur[c]);
-        row_sum<C>(pd, tpr, red);
+        rsum(pd);
         if (valid) {
 #pragma unroll
           for (int c = 0; c < C; ++c) take(i0 + c, pd[c], cur[c]);
@@ -1831,16 +1910,17 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
         typename IO<T>::Raw raw[1][VPT];
 #pragma unroll
         for (int v = 0; v < VPT; ++v) raw[0][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0]) + roff + R.off(v));
-        float pd[1] = {dotc(raw[0])};
-        row_sum<1>(pd, tpr, red);
+        Acc pd[1] = {dotc(raw[0])};
+        rsum(pd);
         if (valid) take(i0, pd[0], raw[0]);
       }
       if (valid) {
+        const float sf = (float)sacc;
 #pragma unroll
         for (int v = 0; v < VPT; ++v)
 #pragma unroll
-          for (int k = 0; k < 8; ++k) dqa[v][k] -= sacc * b[v][k];
-        if (R.lr == 0) s_sacc[rr] = sacc;
+          for (int k = 0; k < 8; ++k) dqa[v][k] += a[v][k] - sf * b[v][k];
+        if (R.lr == 0) s_sacc[rr] = sf;
       }
     }
     __syncthreads();

@@ -155,9 +155,11 @@ def main(argv=None):
         with open(os.path.join(a.out, f"{a.stats_only}.md"), "w") as f:
             f.write("\n".join(lines) + "\n")
         return
-    for need in ("trace", "fetch", "write", "calib_fetch", "calib_write"):
-        if getattr(a, need) is None:
-            ap.error(f"--{need.replace('_', '-')} is required")
+    if a.trace is None:
+        ap.error("--trace is required")
+    counters = [a.fetch, a.write, a.calib_fetch, a.calib_write]
+    if any(c is not None for c in counters) and not all(c is not None for c in counters):
+        ap.error("--fetch, --write, --calib-fetch and --calib-write go together (or none: the kernel table alone)")
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     sys.path.insert(0, root)
@@ -169,10 +171,6 @@ def main(argv=None):
         sv_bytes, _ = bench.reference_bytes(cfg, a.mode)
 
     kt, span_ms = trace_pass(a.trace)
-    fetch = counter_pass(a.fetch, "FETCH_SIZE")
-    write = counter_pass(a.write, "WRITE_SIZE")
-    fs = calibration(a.calib_fetch, "FETCH_SIZE")
-    ws = calibration(a.calib_write, "WRITE_SIZE")
 
     # the headline mode and the configuration's own dtype keep the plain name
     tag = a.config + ("" if a.mode == "scores" else f"_{a.mode}") + \
@@ -205,6 +203,12 @@ def main(argv=None):
         lines += [""] + stats_table(a.stats, 12)
     with open(os.path.join(a.out, f"kernels_chain_{tag}.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
+    if a.fetch is None:
+        return
+    fetch = counter_pass(a.fetch, "FETCH_SIZE")
+    write = counter_pass(a.write, "WRITE_SIZE")
+    fs = calibration(a.calib_fetch, "FETCH_SIZE")
+    ws = calibration(a.calib_write, "WRITE_SIZE")
 
     per_launch = {}
     lines = [f"# HBM traffic per kernel: config {a.config} ({cfg.name}), mode {a.mode}{glue}, one pass", ""]

@@ -51,7 +51,8 @@ def headline_fp32():
     del states, ref32
     torch.cuda.empty_cache()
     worst = max(range(len(e32)), key=lambda i: e32[i])
-    print(f"fp32 oracle chain vs exact: worst {e32[worst]:.3e} x RMS ({_names(cfg.N)[worst]})", flush=True)
+    print(f"fp32 oracle chain vs exact: worst {e32[worst]:.3e} x RMS ({_names(cfg.N)[worst]}); h {e32[0]:.2e} "
+          f"h0 {e32[1]:.2e} query {e32[2]:.2e} D max {max(e32[3:]):.2e}", flush=True)
     yield cfg, (h0, D, Q, G), exact
     del exact, h0, D, Q, G
     torch.cuda.empty_cache()
@@ -68,6 +69,7 @@ def test_headline_fp32_chain_against_exact(monkeypatch, headline_fp32, mode, glu
     errs = [_err(a, b) for a, b in zip(_flat(h, grads), exact)]
     names = _names(cfg.N)
     worst = max(range(len(errs)), key=lambda i: errs[i])
-    print(f"HIP chain {mode} glue={glue} vs exact: worst {errs[worst]:.3e} x RMS ({names[worst]})", flush=True)
+    print(f"HIP chain {mode} glue={glue} vs exact: worst {errs[worst]:.3e} x RMS ({names[worst]}); h {errs[0]:.2e} "
+          f"h0 {errs[1]:.2e} query {errs[2]:.2e} D max {max(errs[3:]):.2e}", flush=True)
     assert all(torch.isfinite(x).all() for x in _flat(h, grads))
     assert errs[worst] <= 1e-5, {n: e for n, e in zip(names, errs) if e > 1e-5}
