@@ -64,8 +64,8 @@ def parse():
                          "FusedDattnReadStk (the reference trainer's calls), 1 the glue in the read's kernels "
                          "(default: the environment's setting, else 1)")
     ap.add_argument("--graph", action="store_true",
-                    help="time replays of the pass captured in HIP graphs (no host work per kernel): the forward "
-                         "as one graph, a training pass as a forward and a backward graph")
+                    help="time replays of the pass captured in a HIP graph (no host work per kernel): the forward, "
+                         "or a training pass's forward and backward, as one graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra-configs", action="store_true", help="skip the c2 / c3 timings of the default run")
     ap.add_argument("--cpu-tokens", type=int, default=1024, help="tokens of the CPU baseline sample")
@@ -279,16 +279,15 @@ def time_chain(cfg, mode, steps, warmup, timer=None):
 
 
 def time_graphed(cfg, mode, steps, warmup):
-    """The pass replayed from HIP graphs (forward-only configs: chain.capture_forward; with a backward:
-    chain.capture_training, the loss and its backward eager around the graphs), `steps` passes timed after
-    `warmup`; returns elapsed s."""
+    """The pass replayed from a HIP graph (forward-only configs: chain.capture_forward; with a backward:
+    chain.capture_training, forward and backward in one graph, the loss summed eagerly after each replay), `steps`
+    passes timed after `warmup`; returns elapsed s."""
     import torch
     from loopback_amd.chain import capture_forward, capture_training, make_inputs
     dev = torch.device("cuda", 0)
     h0, D, Q, G = make_inputs(cfg, dev)
     if cfg.backward:
-        step = capture_training(cfg, h0, D, Q, mode)
-        run = lambda: step(G)
+        run = capture_training(cfg, h0, D, Q, G, mode)
     else:
         graph, _ = capture_forward(cfg, h0, D, Q, mode)
         run = graph.replay

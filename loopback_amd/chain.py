@@ -118,39 +118,46 @@ def capture_forward(cfg: ChainConfig, h0, D, Q, mode: str):
     return graph, out
 
 
-class ChainModule(torch.nn.Module):
-    """The chain's layer loop as a module of its read cell: forward(h0, *D) -> the final state."""
-
-    def __init__(self, cell: LoopDeltaAttnRes, K: int, mode: str):
-        super().__init__()
-        self.cell, self.K, self.mode = cell, int(K), mode
-
-    def forward(self, h0, *D):
-        return chain_forward(self.cell, h0, list(D), self.K, self.mode)
-
-
-def capture_training(cfg: ChainConfig, h0, D, Q, mode: str):
-    """The chain's forward and backward captured as two HIP graphs (torch.cuda.make_graphed_callables): every
-    library launch takes its addresses and sizes by value and allocates nothing, torch's allocations come from the
-    graphs' pool, so a training pass replays with no host work per kernel. Returns step(G) -> (h, loss, grads): one
-    pass on the static inputs h0, D (their contents may change between passes, not their storage) with the loss
-    sum(h.float() * G) and its backward (eager, outside the graphs); grads = {'h0', 'D', 'query'} alias the graphs'
-    output buffers until the next step (clone them to keep them)."""
+def capture_training(cfg: ChainConfig, h0, D, Q, G, mode: str):
+    """The whole training pass -- the chain's forward and its backward from the loss sum(h.float() * G) -- captured
+    as ONE HIP graph: every library launch takes its addresses and sizes by value and allocates nothing, and torch's
+    allocations (the stack, the saved tensors, the gradients) come from the graph's private pool, so a pass replays
+    with one graph launch and no host work per kernel. The backward is seeded with that loss's gradient, G in the
+    updates' dtype (what (h.float() * G).sum().backward() passes to h). Returns step() -> (h, loss, grads): one pass
+    on the static inputs h0, D, G (their contents may change between passes, not their storage), the loss summed
+    eagerly after the replay; grads = {'h0', 'D', 'query'} alias the graph's buffers until the next step (clone
+    them to keep them)."""
     cell = make_cell(cfg, Q)
-    mod = ChainModule(cell, cfg.K, mode)
     h0s = h0.detach().requires_grad_()
     Ds = [x.detach().requires_grad_() for x in D]
-    graphed = torch.cuda.make_graphed_callables(mod, (h0s, *Ds))
 
-    def step(G):
+    def body():
+        h = chain_forward(cell, h0s, Ds, cfg.K, mode)
+        h.backward(G.to(cfg.dtype))
+        return h
+
+    def clear():
         for t in (h0s, *Ds, cell.query):
             t.grad = None
-        h = graphed(h0s, *Ds)
-        loss = (h.float() * G).sum()
-        loss.backward()
-        return h.detach(), loss.detach(), {"h0": h0s.grad, "D": [x.grad for x in Ds], "query": cell.query.grad}
 
-    step.cell = cell
+    side = torch.cuda.Stream()   # warm-up on a side stream, as torch's capture expects
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            clear()
+            body()
+    torch.cuda.current_stream().wait_stream(side)
+    clear()                      # the captured backward then writes fresh gradient buffers of the graph's pool
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        h = body()
+    grads = {"h0": h0s.grad, "D": [x.grad for x in Ds], "query": cell.query.grad}
+
+    def step():
+        graph.replay()
+        return h.detach(), (h.float() * G).sum(), grads
+
+    step.graph, step.cell = graph, cell
     return step
 
 

@@ -45,9 +45,10 @@ FWD_KERNELS = ("k_split_queries", "k_write_mfma", "k_write_rows", "k_write_dots"
 BWD_KERNELS = ("k_bwd1", "k_dv_assemble", "k_reduce_rows", "k_blend_sum", "k_bwd2_list", "k_rstd_bwd")
 
 
-def _passes(rows, key="Start_Timestamp"):
+def _passes(rows, key="Start_Timestamp", n_steps=None):
     """The rows of each chain pass, in launch order. With stored scores a pass starts at its k_split_queries launch
-    (the stack's queries); otherwise at the first forward kernel of the library after a backward one."""
+    (the stack's queries); otherwise at the first forward kernel of the library after a backward one; a forward-only
+    chain without stored scores (no backward kernels) at every n_steps-th write (a pass writes n_steps updates)."""
     rows = sorted(rows, key=lambda r: int(r[key]))
     starts = [i for i, r in enumerate(rows) if "k_split_queries" in r["Kernel_Name"]]
     if not starts:
@@ -58,12 +59,14 @@ def _passes(rows, key="Start_Timestamp"):
             if kind == "f" and prev != "f":
                 starts.append(i)
             prev = kind or prev
+        if len(starts) < 2 and n_steps:
+            starts = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]) == "write_dots"][::n_steps]
     return [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
 
 
-def trace_pass(path):
+def trace_pass(path, n_steps=None):
     """Per-family launches and GPU time of the last complete pass of a kernel trace; also the pass's span."""
-    passes = _passes(_rows(path))
+    passes = _passes(_rows(path), n_steps=n_steps)
     if len(passes) < 2:
         raise SystemExit("kernel trace: need at least two chain passes")
     p = passes[-2]   # the last complete pass (the final one runs into the end of the program)
@@ -78,11 +81,11 @@ def trace_pass(path):
     return out, span_ms
 
 
-def counter_pass(path, counter):
+def counter_pass(path, counter, n_steps=None):
     """Per-family launches and counter total (KiB) of the last pass of a counter run."""
     rows = [r for r in _rows(path) if r["Counter_Name"] == counter]
     # one row per dispatch per counter
-    p = _passes(rows, key="Dispatch_Id")[-1]
+    p = _passes(rows, key="Dispatch_Id", n_steps=n_steps)[-1]
     out = {}
     for r in p:
         t = out.setdefault(family(r["Kernel_Name"]), [0, 0.0])
@@ -170,7 +173,7 @@ def main(argv=None):
         fam_bytes, _ = bench.family_bytes(cfg, a.mode)
         sv_bytes, _ = bench.reference_bytes(cfg, a.mode)
 
-    kt, span_ms = trace_pass(a.trace)
+    kt, span_ms = trace_pass(a.trace, cfg.N)
 
     # the headline mode and the configuration's own dtype keep the plain name
     tag = a.config + ("" if a.mode == "scores" else f"_{a.mode}") + \
@@ -205,8 +208,8 @@ def main(argv=None):
         f.write("\n".join(lines) + "\n")
     if a.fetch is None:
         return
-    fetch = counter_pass(a.fetch, "FETCH_SIZE")
-    write = counter_pass(a.write, "WRITE_SIZE")
+    fetch = counter_pass(a.fetch, "FETCH_SIZE", cfg.N)
+    write = counter_pass(a.write, "WRITE_SIZE", cfg.N)
     fs = calibration(a.calib_fetch, "FETCH_SIZE")
     ws = calibration(a.calib_write, "WRITE_SIZE")
 

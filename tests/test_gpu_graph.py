@@ -61,7 +61,7 @@ def test_forward_chain_replays_in_a_graph(mode, dtype):
 @pytest.mark.parametrize("mode", ["scores", "stack", "list"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_training_chain_replays_in_graphs(mode, dtype):
-    """The chain's forward and backward captured as HIP graphs (chain.capture_training): every replay -- with eager
+    """The chain's forward and backward captured as one HIP graph (chain.capture_training): every replay -- with eager
     chains and synchronizations between them, and after the inputs' contents change -- gives the eager pass's final
     state, loss and every gradient (h0, each update, the query) bitwise."""
     from loopback_amd.chain import ChainConfig, capture_training, make_inputs, run_chain
@@ -75,9 +75,9 @@ def test_training_chain_replays_in_graphs(mode, dtype):
         return h.clone(), loss.clone(), [g["h0"].clone(), g["query"].clone()] + [x.clone() for x in g["D"]]
 
     ref = eager()
-    step = capture_training(cfg, h0, D, Q, mode)
+    step = capture_training(cfg, h0, D, Q, G, mode)
     for k in range(4):
-        h, loss, g = step(G)
+        h, loss, g = step()
         torch.cuda.synchronize()
         got = [g["h0"].clone(), g["query"].clone()] + [x.clone() for x in g["D"]]
         assert torch.equal(h, ref[0]) and torch.equal(loss, ref[1]), k
@@ -88,8 +88,32 @@ def test_training_chain_replays_in_graphs(mode, dtype):
         D[5].mul_(-0.5)
         h0.add_(0.25)
     ref2 = eager()
-    h, loss, g = step(G)
+    h, loss, g = step()
     torch.cuda.synchronize()
     assert torch.equal(h, ref2[0]) and torch.equal(loss, ref2[1]) and not torch.equal(ref2[0], ref[0])
     got = [g["h0"].clone(), g["query"].clone()] + [x.clone() for x in g["D"]]
     assert all(torch.equal(a, b) for a, b in zip(got, ref2[2]))
+
+
+def test_training_pass_replays_at_config3():
+    """Config 3 whole (d=1024, K=3, R=4, 16384 tokens, bf16, fwd+bwd), the pass as one graph: three replays with an
+    eager pass between each give the eager pass's final state, loss and every gradient bitwise."""
+    from loopback_amd.chain import CONFIGS, capture_training, make_cell, make_inputs, run_chain
+    cfg = CONFIGS["c3"]
+    h0, D, Q, G = make_inputs(cfg, DEV)
+    cell = make_cell(cfg, Q)
+    print("case graph training config 3", flush=True)
+
+    def eager():
+        h, loss, g = run_chain(cfg, h0, D, Q, G, "scores", cell=cell)
+        torch.cuda.synchronize()
+        return [h.clone(), loss.clone(), g["h0"].clone(), g["query"].clone()] + [x.clone() for x in g["D"]]
+
+    ref = eager()
+    step = capture_training(cfg, h0, D, Q, G, "scores")
+    for k in range(3):
+        h, loss, g = step()
+        torch.cuda.synchronize()
+        got = [h, loss, g["h0"], g["query"]] + list(g["D"])
+        assert all(torch.equal(a, b) for a, b in zip(got, ref)), k
+        assert torch.equal(eager()[0], ref[0])
