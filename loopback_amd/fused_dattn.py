@@ -699,7 +699,10 @@ class _RstdStk(torch.autograd.Function):
 class FusedDattnReadStk(torch.autograd.Function):
     """(out, tc) = apply(stack, step, q, base, cbar, c0, *updates, *scales) (fused_dattn.py:725-793): the updates and
     scales are the stack's slices 0..step (inputs only for autograd's bookkeeping; the kernels read the stack).
-    Backward returns (None, None, dq, g, dcbar, None, None x n, dR alias for the scales whose last read this is)."""
+    Backward returns (None, None, dq, g, dcbar, None, None x n, dR alias for the scales whose last read this is) --
+    except that when the base is the write's h of this step (the caller's proposal, as the trainer passes it at every
+    read that is not an iteration end) the base's gradient g is added by the update's gradient kernel instead, which
+    then returns h's whole gradient, the same bits (its None here)."""
 
     @staticmethod
     def forward(ctx, stack: DattnStack, step: int, q, base, cbar, c0, *srcs):
@@ -730,6 +733,13 @@ class FusedDattnReadStk(torch.autograd.Function):
         if grad:
             ctx.save_for_backward(qc, cbar_c, c0c, prob, dots, tc)
         ctx.stack, ctx.step, ctx.n, ctx.q_dtype, ctx.base_shape = stack, int(step), n, q.dtype, base.shape
+        # the base is the write's h of this step (the caller's proposal, no blend) and the newest scale comes from
+        # that update's scale node, whose backward runs after this one: the base's gradient then goes to the update's
+        # gradient kernel, which adds it as autograd would (round(round(dv) + g)), instead of autograd's own add
+        wr = stack.wh.get(int(step))
+        scale = srcs[-1]
+        ctx.linked = (step >= 1 and base.requires_grad and wr is not None and wr() is base and scale.grad_fn is not None
+                      and type(scale.grad_fn).__name__ in ("_WriteDeltaBackward", "_RstdStkBackward"))
         return out, tc.view(*base.shape[:-1], n)
 
     @staticmethod
@@ -745,7 +755,11 @@ class FusedDattnReadStk(torch.autograd.Function):
         # for the updates' gradients, formed once per update (the tensors, and their addresses for the kernel tables)
         stack.bwd[step] = (g, qc, g.data_ptr(), qc.data_ptr())
         final = [i == step or (step == 1 and i == 0) for i in range(n)]   # the last read of scale i, in backward order
-        grads = (None, None, dq.to(ctx.q_dtype), g, dcbar.view(*ctx.base_shape[:-1], n), None,
+        gbase = g
+        if ctx.linked and ctx.needs_input_grad[3]:
+            stack.gadd[step] = (g, 0.0)
+            gbase = None
+        grads = (None, None, dq.to(ctx.q_dtype), gbase, dcbar.view(*ctx.base_shape[:-1], n), None,
                  *[None] * n, *[_alias(stack.dR, i) if final[i] else None for i in range(n)])
         # Release the stack from this node: ctx attributes live as long as the graph node, and a training loop that
         # keeps each micro-batch's loss until the optimizer step would otherwise keep each micro-batch's stack.

@@ -289,12 +289,16 @@ def test_fused_glue_matches_torch_glue(monkeypatch, K, R, dtype, mode):
 
 @pytest.mark.parametrize("K,R", [(3, 3), (1, 4)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_proposal_gradient_through_update_kernel(K, R, dtype):
-    """A fused combine whose proposal is the write's h hands the proposal's gradient to the update-gradient kernel,
-    which adds it as autograd would (round(round(dv) + g)); with the proposal a copy of h the same sum is formed by
-    autograd. Every gradient agrees bitwise, and no handed-over gradient is left behind."""
+@pytest.mark.parametrize("glue", ["1", "0"])
+def test_proposal_gradient_through_update_kernel(monkeypatch, K, R, dtype, glue):
+    """A read whose proposal (glue "1", FusedCombineStk) or base (glue "0", FusedDattnReadStk with the caller's torch
+    glue; the base is the proposal at every read that is not an iteration end) is the write's h hands that gradient
+    to the update-gradient kernel, which adds it as autograd would (round(round(dv) + g)); with the proposal a copy
+    of h the same sum is formed by autograd. Every gradient agrees bitwise, and no handed-over gradient is left
+    behind."""
     from loopback_amd.cell import LoopDeltaAttnRes
     from loopback_amd.chain import make_inputs
+    monkeypatch.setenv("LOOP_DATTN_FUSE_GLUE", glue)
     cfg = chain_cfg(K, R, dtype)
     h0c, Dc, Q, G = make_inputs(cfg, "cpu")
     outs = []
