@@ -62,6 +62,12 @@
 #ifndef LDR_AS_MAX_VPT
 #define LDR_AS_MAX_VPT 3
 #endif
+#ifndef LDR_AS_MAX_VPT_F32
+#define LDR_AS_MAX_VPT_F32 4   // update gradient, fp32 updates: one wave per row of 2048 (bf16 and fp16: two)
+#endif
+#ifndef LDR_AS_JB_F32
+#define LDR_AS_JB_F32 2        // update gradient, fp32 updates: reads whose rows are loaded together
+#endif
 #ifndef LDR_B1_MAX_VPT
 #define LDR_B1_MAX_VPT 4     // backward pass 1 (holds g and two accumulators per element)
 #endif
@@ -135,7 +141,9 @@ static_assert(LDR_RF_MAX_VPT >= 1 && LDR_RF_MAX_VPT <= 4 && LDR_AS_MAX_VPT >= 1 
 static_assert(LDR_RF_VPT >= 0 && LDR_RF_VPT <= 4 && LDR_AS_VPT >= 0 && LDR_AS_VPT <= 4 && LDR_B1_VPT >= 0 &&
               LDR_B1_VPT <= 4, "fixed vectors per lane: 0 (chosen from d) or 1..4");
 static_assert(LDR_AS_STORES >= 0 && LDR_AS_STORES <= 3, "update gradient: LDR_AS_STORES is 0..3");
-static_assert(LDR_AS_RB >= 1 && LDR_AS_JB >= 1, "update gradient: at least one row per lane and one read per batch");
+static_assert(LDR_AS_RB >= 1 && LDR_AS_JB >= 1 && LDR_AS_JB_F32 >= 1,
+              "update gradient: at least one row per lane and one read per batch");
+static_assert(LDR_AS_MAX_VPT_F32 >= 1 && LDR_AS_MAX_VPT_F32 <= 4, "vectors per lane: 1..4");
 static_assert(LDR_B1_C >= 0 && LDR_B1_C <= 8, "backward pass 1: 0 (by vectors per lane) or 1..8 sources per chunk");
 static_assert(LDR_B1_GD64 == 0 || LDR_B1_GD64 == 1, "backward pass 1: LDR_B1_GD64 is 0 or 1");
 static_assert(LDR_B1_KEEP_LAST == 0 || LDR_B1_KEEP_LAST == 1, "backward pass 1: LDR_B1_KEEP_LAST is 0 or 1");
@@ -2098,7 +2106,9 @@ __global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, c
 // ---------------------------------------------------------------------------------------------------------------
 // token rows per lane, sharing each query load (fewer when the lane holds 3+ vectors of a row: registers)
 constexpr int as_rb(int vpt) { return vpt >= 3 ? 2 : LDR_AS_RB; }
-constexpr int AS_JB = LDR_AS_JB;   // reads per batch of loads
+// reads per batch of loads: fp32 rows two (c4 fp32: the update gradients 16.0 -> 14.8 ms per pass, with one wave per
+// row; either setting takes bf16's from 6.4 to 7.0-7.8 ms)
+template <typename T> constexpr int as_jb() { return std::is_same<T, float>::value ? LDR_AS_JB_F32 : LDR_AS_JB; }
 
 // ADD_LAST: add is the output gradient of the last read in tab. PER_READ: each read's share rounded to T and added
 // to the running gradient in T, in table order, then the scale's term rounded and added -- the roundings of the list
@@ -2175,7 +2185,8 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
     };
     const int mm = ADD_LAST ? m - 1 : m;
     int j = 0;
-    for (; j + AS_JB <= mm; j += AS_JB) batch(j, std::integral_constant<int, AS_JB>());
+    constexpr int JB = as_jb<T>();
+    for (; j + JB <= mm; j += JB) batch(j, std::integral_constant<int, JB>());
     for (; j < mm; ++j) batch(j, std::integral_constant<int, 1>());
     typename IO<T>::Raw last[AS_RB][VPT];   // ADD_LAST: the last read's rows, kept for the added gradient
     if (ADD_LAST) {
@@ -3088,7 +3099,8 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
     if (j < m && (!tok_ptr(t.g[j], n_tok) || !tok_ptr(t.wz[j], n_tok) || !t.q[j])) return LDR_E_ARG;
     if (j < m && (!al16(t.g[j]) || !al16(t.q[j]) || (reinterpret_cast<uintptr_t>(t.wz[j]) & 7u))) return LDR_E_ALIGN;
   }
-  int vpt, tpr, e = row_layout(d, &vpt, &tpr, LDR_AS_MAX_VPT, false, LDR_AS_VPT, true);
+  const int max_vpt = dtype == LDR_F32 ? LDR_AS_MAX_VPT_F32 : LDR_AS_MAX_VPT;
+  int vpt, tpr, e = row_layout(d, &vpt, &tpr, max_vpt, false, LDR_AS_VPT, true);
   if (e == LDR_E_SHAPE && !LDR_AS_VPT) e = row_layout(d, &vpt, &tpr, 4, false, 0, true);   // rows past 3 x 256 x 8
   if (e) return e;
   if (n_tok == 0) return LDR_OK;
