@@ -81,6 +81,23 @@ def trace_pass(path, n_steps=None):
     return out, span_ms
 
 
+def pass_timeline(path, n_steps=None):
+    """The last complete pass of a kernel trace as a timeline: kernels, kernel time (us), the span from its first
+    kernel's start to its last kernel's end, the idle time between its kernels, and the idle time from its last kernel
+    to the next pass's first (all in us)."""
+    passes = _passes(_rows(path), n_steps=n_steps)
+    if len(passes) < 2:
+        raise SystemExit("kernel trace: need at least two chain passes")
+    p, nxt = passes[-2], passes[-1][0]
+    ts = lambda r, k: int(r[k])
+    busy = sum(ts(r, "End_Timestamp") - ts(r, "Start_Timestamp") for r in p) / 1e3
+    span = (ts(p[-1], "End_Timestamp") - ts(p[0], "Start_Timestamp")) / 1e3
+    gaps = sum(max(0, ts(b, "Start_Timestamp") - ts(a, "End_Timestamp")) for a, b in zip(p, p[1:])) / 1e3
+    tail = (ts(nxt, "Start_Timestamp") - ts(p[-1], "End_Timestamp")) / 1e3
+    return {"kernels": len(p), "busy_us": busy, "span_us": span, "gaps_us": gaps, "to_next_us": tail,
+            "period_us": (ts(nxt, "Start_Timestamp") - ts(p[0], "Start_Timestamp")) / 1e3}
+
+
 def counter_pass(path, counter, n_steps=None):
     """Per-family launches and counter total (KiB) of the last pass of a counter run."""
     rows = [r for r in _rows(path) if r["Counter_Name"] == counter]
@@ -139,6 +156,10 @@ def main(argv=None):
     ap.add_argument("--stats-only", default=None, metavar="NAME",
                     help="write only the --stats table, as profiles/NAME.md (any program, e.g. the LM step)")
     ap.add_argument("--title", default="", help="heading of a --stats-only summary")
+    ap.add_argument("--compare", nargs=2, default=None, metavar=("EAGER", "REPLAY"),
+                    help="two kernel traces of the same configuration (eager, replayed from a HIP graph): writes "
+                         "profiles/NAME.md (--name) with each one's pass timeline")
+    ap.add_argument("--name", default=None, help="file name of a --compare summary")
     ap.add_argument("--config", default="c4")
     ap.add_argument("--mode", default="scores")
     ap.add_argument("--dtype", default=None, choices=["bf16", "fp16", "fp32"],
@@ -150,6 +171,27 @@ def main(argv=None):
     ap.add_argument("--commands", default="", help="the commands that produced the inputs (quoted into the summaries)")
     ap.add_argument("--commit", default=None, help="the commit the profiled tree was taken from (recorded as given)")
     a = ap.parse_args(argv)
+    if a.compare:
+        root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+        sys.path.insert(0, root)
+        from loopback_amd.chain import CONFIGS
+        cfg = CONFIGS[a.config]
+        lines = [f"# {a.title or 'Eager against HIP-graph replay'}: config {a.config} ({cfg.name})", ""]
+        if a.commands:
+            lines += ["Commands:", "", *["    " + c for c in a.commands.split(";;")], ""]
+        lines += ["The last complete pass of each trace (us): kernel time, the span from its first kernel's start to its "
+                  "last kernel's end, the idle time between its kernels, the idle time before the next pass's first "
+                  "kernel, and the period between pass starts. The eager trace's idle time is the profiler's slow-down "
+                  "of the host's launches.", "",
+                  "| run | kernels | kernel time | span | idle between kernels | idle before the next pass | period |",
+                  "|---|---|---|---|---|---|---|"]
+        for label, path in zip(("eager", "graph replay"), a.compare):
+            t = pass_timeline(path, cfg.N)
+            lines.append(f"| {label} | {t['kernels']} | {t['busy_us']:.1f} | {t['span_us']:.1f} | {t['gaps_us']:.1f} | "
+                         f"{t['to_next_us']:.1f} | {t['period_us']:.1f} |")
+        with open(os.path.join(a.out, f"{a.name or 'graph_replay_' + a.config}.md"), "w") as f:
+            f.write("\n".join(lines) + "\n")
+        return
     if a.stats_only:
         lines = [f"# {a.title or a.stats_only}", ""]
         if a.commands:

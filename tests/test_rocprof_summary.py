@@ -133,3 +133,23 @@ def test_bench_counter_chain_arithmetic():
     assert c["counter_kernel_ms"] == pytest.approx(1.5)
     assert c["counter_gbs"] == pytest.approx(8e9 / 1.5e-3 / 1e9)
     assert bench.counter_chain({"x": 1.0}, ksum) is None
+
+
+def test_compare_pass_timelines(tmp_path):
+    """--compare: the last complete pass of each trace -- its kernel time, span, idle time between its kernels and
+    before the next pass -- from synthetic traces whose timings are known."""
+    kt1, kt2 = tmp_path / "e.csv", tmp_path / "g.csv"
+    _trace(kt1)                    # 1 us between kernels
+    _trace(kt2, scale=2)
+    t = RS.pass_timeline(str(kt1))
+    ns = sum(ns for _, ns in PASS)
+    assert t["kernels"] == len(PASS)
+    assert t["busy_us"] == pytest.approx(2 * ns / 1e3)        # the second of three passes runs at twice the time
+    assert t["gaps_us"] == pytest.approx((len(PASS) - 1) * 1.0)
+    assert t["to_next_us"] == pytest.approx(1.0)
+    assert t["span_us"] == pytest.approx(t["busy_us"] + t["gaps_us"])
+    out = tmp_path / "profiles"
+    out.mkdir()
+    RS.main(["--config", "c3", "--compare", str(kt1), str(kt2), "--name", "cmp", "--out", str(out)])
+    text = (out / "cmp.md").read_text()
+    assert "| eager | 8 |" in text and "| graph replay | 8 |" in text
