@@ -47,6 +47,9 @@
 #ifndef LDR_RF_STAGE_U
 #define LDR_RF_STAGE_U 6     // read forward with staged output: sources loaded per batch (the registers of 8 leave
 #endif                       // one wave per SIMD beside the staging code)
+#ifndef LDR_RF_U_F32
+#define LDR_RF_U_F32 4       // read forward, fp32 updates: sources loaded per batch (fp32 vectors take twice the
+#endif                       // registers: 6 or 8 spilled to scratch)
 #ifndef LDR_RF_MAX_VPT
 #define LDR_RF_MAX_VPT 4     // read forward: most 16-byte vectors per lane in a row
 #endif
@@ -130,9 +133,11 @@ constexpr int WG = 256;                 // lanes per workgroup (4 wave64s)
 constexpr int MAXS = LDR_MAX_SOURCES;
 constexpr int TT_MAX = 32;              // tokens per tile in the tiled kernels
 constexpr int SP = MAXS + 1;            // padded LDS row of per-source scalars
+constexpr int PRO_K = 4;                 // tile prologues: scalar entries per lane whose loads go out together
 
 // The launch settings a build may change, and the ranges the kernels are written for (a value outside them would
 // overflow a tile in LDS, leave rows unwritten or loop without advancing: the build refuses it).
+static_assert(LDR_RF_U_F32 >= 1 && LDR_RF_U_F32 <= 8, "read forward: 1..8 fp32 sources per batch");
 static_assert(LDR_RF_UNROLL >= 1 && LDR_RF_STAGE_U >= 1 && LDR_RF_UNROLL <= 8 && LDR_RF_STAGE_U <= 8,
               "read forward: 1..8 sources per batch");
 static_assert(LDR_RF_STAGE >= 0, "read forward: staging bytes must be >= 0");
@@ -476,6 +481,13 @@ struct Coef {
 __device__ __forceinline__ float coef_cbar(const Coef& c, int64_t tok, int i) {
 #pragma clang fp contract(off)   // the product is rounded on its own, as the caller's scaling is (never fused into a use)
   return i < c.cbar_cols ? c.lam * c.cbar[tok * c.cbar_cols + i] : c.lam;
+}
+
+// x, as a value the compiler cannot see through: index math formed from it inside a tile loop is formed again in
+// each pass instead of hoisted out of the loop, where its registers would stay live through the row stream
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
 }
 
 // per-read constants from the prior: c0, lc = log(max(c0, 1e-8)), M = sum c0 (in source order)
@@ -1429,6 +1441,41 @@ __global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float
   __shared__ float s_c0[MAXS], s_lc[MAXS], s_p0[MAXS], s_M;
   const Rows R(d, tpr, NTH);
   const int tid = (int)threadIdx.x;
+  // A tile's scores, scales and cbar, PRO_K entries per lane at a time: fetch issues a chunk's loads (clamped
+  // in-bounds addresses; none is used before all are issued), commit writes the logits and cbar to LDS -- a memory
+  // round trip per chunk instead of one per entry. Their lane index is opaque, so the index math is formed in each
+  // tile (hoisted out of the tile loop, its registers would stay live through the row stream).
+  const int nt = n * tt;
+  float zv[PRO_K], rv[PRO_K], cv[PRO_K];
+  auto fetch = [&](int64_t t0, int c) {
+    const int lane = opaque(tid) + c;
+#pragma unroll
+    for (int k = 0; k < PRO_K; ++k) {
+      const int idx = min(lane + k * NTH, nt - 1);
+      const int i = idx / tt, t = idx - i * tt;                  // source-major: coalesced over tokens
+      const int64_t tok = min(t0 + t, n_tok - 1);
+      zv[k] = dots[(int64_t)i * dots_stride + tok];
+      rv[k] = src.r[i][tok];
+      const int t2 = idx / n, i2 = idx - t2 * n;                 // token-major: coalesced over [tok][i]
+      cv[k] = coef_cbar(cf, min(t0 + t2, n_tok - 1), i2);
+    }
+  };
+  auto commit = [&](int64_t t0, int c) {
+    const int lane = opaque(tid) + c;
+#pragma unroll
+    for (int k = 0; k < PRO_K; ++k) {
+      const int idx = lane + k * NTH;
+      if (idx < nt) {
+        const int i = idx / tt, t = idx - i * tt;
+        float l = s_lc[i];
+        if (t0 + t < n_tok) l = zv[k] * rv[k] * inv + s_lc[i];
+        s_l[i * (TT_MAX + 1) + t] = l;
+        const int t2 = idx / n, i2 = idx - t2 * n;
+        s_w[t2 * SP + i2] = t0 + t2 < n_tok ? cv[k] : 0.f;
+      }
+    }
+  };
+  const int64_t tiles = (n_tok + tt - 1) / tt;
   load_prior(cf, n, s_c0, s_lc, &s_M);
   const float M = s_M;
   if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
@@ -1448,20 +1495,12 @@ __global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float
       if (i < n) s_p0[i] = p0[m];
     }
   }
-  const int64_t tiles = (n_tok + tt - 1) / tt;
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int64_t t0 = tile * tt;
-    for (int idx = tid; idx < n * tt; idx += NTH) {   // source-major: coalesced over tokens
-      const int i = idx / tt, t = idx - i * tt;
-      const int64_t tok = t0 + t;
-      float l = s_lc[i];
-      if (tok < n_tok) l = dots[(int64_t)i * dots_stride + tok] * src.r[i][tok] * inv + s_lc[i];
-      s_l[i * (TT_MAX + 1) + t] = l;
-    }
-    for (int idx = tid; idx < n * tt; idx += NTH) {   // token-major: coalesced over [tok][i]
-      const int t = idx / n, i = idx - t * n;
-      const int64_t tok = t0 + t;
-      s_w[t * SP + i] = tok < n_tok ? coef_cbar(cf, tok, i) : 0.f;
+#pragma unroll 1
+    for (int c = 0; c < nt; c += PRO_K * NTH) {
+      fetch(t0, c);
+      commit(t0, c);
     }
     __syncthreads();
     {
@@ -1493,7 +1532,7 @@ __global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float
       if (tok >= n_tok) break;
       const float* wrow = &s_w[rr * SP];
       const int64_t roff = tok * (int64_t)d;
-      constexpr int U = STAGE ? LDR_RF_STAGE_U : LDR_RF_UNROLL;
+      constexpr int U = std::is_same<T, float>::value ? LDR_RF_U_F32 : STAGE ? LDR_RF_STAGE_U : LDR_RF_UNROLL;
       using Raw = typename IO<T>::Raw;
       float acc[VPT][8];
 #pragma unroll
@@ -1802,6 +1841,46 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
   float* s_w = lds + 5 * TT_MAX * SP;
   const Rows R(d, tpr);
   const int tid = (int)threadIdx.x;
+  // A tile's per-token scalars, PRO_K entries per lane at a time: fetch issues a chunk's loads (clamped in-bounds
+  // addresses; none is used before all are issued), commit writes them to LDS -- a memory round trip per chunk
+  // instead of one per entry (the lane index opaque, as in the read forward).
+  const int nt = n * tt;
+  float pv[PRO_K], gv[PRO_K], wv[PRO_K], rv[PRO_K], zv[PRO_K];
+  auto fetch = [&](int64_t t0, int c) {
+    const int lane = opaque(tid) + c;
+#pragma unroll
+    for (int k = 0; k < PRO_K; ++k) {
+      const int idx = min(lane + k * WG, nt - 1);
+      const int t = idx / n, i = idx - t * n;                    // token-major: [tok][i]
+      const int64_t tok = min(t0 + t, n_tok - 1);
+      pv[k] = prob[tok * n + i];
+      gv[k] = gt ? gt[tok * n + i] : 0.f;
+      wv[k] = tcp[tok * n + i] - coef_cbar(cf, tok, i);
+      const int i2 = idx / tt, t2 = idx - i2 * tt;               // source-major: scales and raw scores
+      const int64_t tok2 = min(t0 + t2, n_tok - 1);
+      rv[k] = src.r[i2][tok2];
+      zv[k] = dots[i2 * dots_stride + tok2];
+    }
+  };
+  auto commit = [&](int64_t t0, int c) {
+    const int lane = opaque(tid) + c;
+#pragma unroll
+    for (int k = 0; k < PRO_K; ++k) {
+      const int idx = lane + k * WG;
+      if (idx < nt) {
+        const int t = idx / n, i = idx - t * n;
+        const bool ok = t0 + t < n_tok;
+        s_p[t * SP + i] = ok ? pv[k] : 0.f;
+        s_gt[t * SP + i] = ok ? gv[k] : 0.f;
+        s_w[t * SP + i] = ok ? wv[k] : 0.f;
+        const int i2 = idx / tt, t2 = idx - i2 * tt;
+        const bool ok2 = t0 + t2 < n_tok;
+        s_r[t2 * SP + i2] = ok2 ? rv[k] : 1.f;
+        s_dz[t2 * SP + i2] = ok2 ? zv[k] : 0.f;                  // q . v_i until the epilogue
+      }
+    }
+  };
+  const int64_t tiles = (n_tok + tt - 1) / tt;
   load_prior(cf, n, s_c0, s_lc, &s_M);
   const float M = s_M;
   float dqa[VPT][8];
@@ -1809,27 +1888,12 @@ __global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restr
   for (int v = 0; v < VPT; ++v)
 #pragma unroll
     for (int k = 0; k < 8; ++k) dqa[v][k] = 0.f;
-  const int64_t tiles = (n_tok + tt - 1) / tt;
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int64_t t0 = tile * tt;
-    for (int idx = tid; idx < n * tt; idx += WG) {   // token-major scalars
-      const int t = idx / n, i = idx - t * n;
-      const int64_t tok = t0 + t;
-      float p = 0.f, gtv = 0.f, w = 0.f;
-      if (tok < n_tok) {
-        p = prob[tok * n + i];
-        if (gt) gtv = gt[tok * n + i];
-        w = tcp[tok * n + i] - coef_cbar(cf, tok, i);
-      }
-      s_p[t * SP + i] = p;
-      s_gt[t * SP + i] = gtv;
-      s_w[t * SP + i] = w;
-    }
-    for (int idx = tid; idx < n * tt; idx += WG) {   // source-major: scales and raw scores
-      const int i = idx / tt, t = idx - i * tt;
-      const int64_t tok = t0 + t;
-      s_r[t * SP + i] = tok < n_tok ? src.r[i][tok] : 1.f;
-      s_dz[t * SP + i] = tok < n_tok ? dots[i * dots_stride + tok] : 0.f;   // q . v_i until the epilogue
+#pragma unroll 1
+    for (int c = 0; c < nt; c += PRO_K * WG) {
+      fetch(t0, c);
+      commit(t0, c);
     }
     __syncthreads();
     const int rows_per_slot = (tt + R.rpw - 1) / R.rpw;
