@@ -68,6 +68,9 @@
 #ifndef LDR_AS_MAX_VPT_F32
 #define LDR_AS_MAX_VPT_F32 4   // update gradient, fp32 updates: one wave per row of 2048 (bf16 and fp16: two)
 #endif
+#ifndef LDR_AS_RB_F32
+#define LDR_AS_RB_F32 2        // update gradient, fp32 rows of 3-4 vectors per lane: token rows per lane
+#endif
 #ifndef LDR_AS_JB_F32
 #define LDR_AS_JB_F32 2        // update gradient, fp32 updates: reads whose rows are loaded together
 #endif
@@ -2187,7 +2190,7 @@ __global__ __launch_bounds__(WG) void k_bwd2_list(PtrTab dv, int n, int accum, c
 // stacked layout: the finished gradient of one update from every read that held it, plus its scale's term
 // ---------------------------------------------------------------------------------------------------------------
 // token rows per lane, sharing each query load (fewer when the lane holds 3+ vectors of a row: registers)
-constexpr int as_rb(int vpt) { return vpt >= 3 ? 2 : LDR_AS_RB; }
+constexpr int as_rb(int vpt, bool f32 = false) { return vpt >= 3 ? (f32 ? LDR_AS_RB_F32 : 2) : LDR_AS_RB; }
 // reads per batch of loads: fp32 rows two (c4 fp32: the update gradients 16.0 -> 14.8 ms per pass, with one wave per
 // row; either setting takes bf16's from 6.4 to 7.0-7.8 ms)
 template <typename T> constexpr int as_jb() { return std::is_same<T, float>::value ? LDR_AS_JB_F32 : LDR_AS_JB; }
@@ -2202,7 +2205,7 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
                                                     const T* __restrict__ add, float add_beta,
                                                     T* __restrict__ dv, T* __restrict__ dv_neg, int64_t n_tok, int d,
                                                     int tpr) {
-  constexpr int AS_RB = as_rb(VPT);
+  constexpr int AS_RB = as_rb(VPT, std::is_same<T, float>::value);
   const Rows R(d, tpr);
   const int64_t rows_per_tile = (int64_t)R.rpw * AS_RB;
   const int64_t tiles = (n_tok + rows_per_tile - 1) / rows_per_tile;
@@ -3186,7 +3189,7 @@ int ldr_dv_assemble(const uint64_t* g, const uint64_t* wz, const uint64_t* q, in
   if (e == LDR_E_SHAPE && !LDR_AS_VPT) e = row_layout(d, &vpt, &tpr, 4, false, 0, true);   // rows past 3 x 256 x 8
   if (e) return e;
   if (n_tok == 0) return LDR_OK;
-  const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * as_rb(vpt)), LDR_AS_GRID);
+  const unsigned grid = grid_of(cdiv(n_tok, (WG / tpr) * as_rb(vpt, dtype == LDR_F32)), LDR_AS_GRID);
   hipStream_t st = static_cast<hipStream_t>(stream);
   // the added gradient is often the last read's output gradient itself (the proposal of that read is this write's
   // h): then its rows are read once
