@@ -1815,8 +1815,11 @@ void k_read_online(SrcTab src, int n, const float* __restrict__ q, float* __rest
 constexpr int B1_GRID = LDR_B1_GRID;
 constexpr int B1_MAX_VPT = LDR_B1_MAX_VPT;
 
+// two waves per SIMD (two workgroups per CU): the fp32 rows' instantiations need it said (else 254 registers and 16
+// accumulation registers, one workgroup per CU; with it 256 and 60 bytes of scratch: 14.07 -> 14.01 ms per pass at
+// config 4); the 16-bit ones fit it anyway
 template <typename T, int VPT, int C>
-__global__ __launch_bounds__(WG) void k_bwd1(SrcTab src, int n, const T* __restrict__ g, const float* __restrict__ gt,
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_bwd1(SrcTab src, int n, const T* __restrict__ g, const float* __restrict__ gt,
                                              const float* __restrict__ prob, const float* __restrict__ dots,
                                              int64_t dots_stride, const float* __restrict__ tcp, Coef cf, float inv,
                                              float* __restrict__ dcbar, int dcbar_cols, PtrTab dr, int dr_accum,
