@@ -2967,10 +2967,14 @@ int ldr_read_fwd(const uint64_t* src_v, const uint64_t* src_r, int64_t n, const 
   const int64_t row_bytes = d * elt_bytes(dtype);
   // 512-lane workgroups with 32-token tiles whose output (at most 128 KiB) is written as one burst, one workgroup
   // per CU, whenever the tile's rows fit and the read has enough sources to repay the launch's higher fixed cost;
-  // else 256-lane workgroups, 16-token tiles, 64 KiB bursts when they fit
-  const bool big = LDR_RF_BIG && (n + 2) * row_bytes >= LDR_RF_BIG_MIN_ROW_BYTES && RF_BIG_LANES / tpr <= RF_BIG_TT &&
-                   RF_BIG_TT * row_bytes <= RF_BIG_STAGE;
-  int tt = big ? RF_BIG_TT : rf_tile(tpr);
+  // rows of 4-8 KiB (fp32 rows of 2048) take 16-token tiles there, a token's softmax still over 32 lanes as in the
+  // 256-lane launch's 8-token tiles for such rows (the same bits; fp32 headline read forward 15.15 -> 14.26 ms per
+  // pass); else 256-lane workgroups, 16-token tiles, 64 KiB bursts when they fit
+  int big_tt = RF_BIG_TT;
+  if (LDR_RF_HALF_TT && big_tt * row_bytes > RF_BIG_STAGE) big_tt /= 2;
+  const bool big = LDR_RF_BIG && (n + 2) * row_bytes >= LDR_RF_BIG_MIN_ROW_BYTES && RF_BIG_LANES / tpr <= big_tt &&
+                   big_tt * row_bytes <= RF_BIG_STAGE;
+  int tt = big ? big_tt : rf_tile(tpr);
   // rows too long for a tile's output to fit the staging space (fp32 rows of 2048, bf16 rows of 3072 and more): half
   // the tokens per tile, while that still gives every row slot a row, so the output still goes out in bursts
   if (LDR_RF_HALF_TT && !big && RF_STAGE_BYTES > 0 && tt * row_bytes > RF_STAGE_BYTES &&

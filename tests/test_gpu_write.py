@@ -116,15 +116,18 @@ def test_whole_row_write_is_the_matrix_core_write_bitwise(d, nq, T, dtype):
         assert ((s1[:nq].double() - ref).abs().max() / ref.pow(2).mean().sqrt()).item() <= 1e-5
 
 
-@pytest.mark.parametrize("d,n", [(2048, 5), (2048, 32), (1024, 12), (1024, 20), (768, 17), (768, 40), (1536, 8)])
+@pytest.mark.parametrize("dtype,d,n", [("bf16", 2048, 5), ("bf16", 2048, 32), ("bf16", 1024, 12), ("bf16", 1024, 20),
+                                       ("bf16", 768, 17), ("bf16", 768, 40), ("bf16", 1536, 8), ("fp32", 2048, 5),
+                                       ("fp32", 2048, 31), ("bf16", 3072, 9)])
 @pytest.mark.parametrize("T", [1, 77, 1000, 4099])
 @pytest.mark.parametrize("blend", [False, True])
-def test_read_forward_launch_shapes_agree_bitwise(d, n, T, blend):
-    """ldr_read_fwd in its two launch shapes -- 512-lane workgroups with 32-token tiles (the product library, for reads
-    of at least 7 rows of 4 KiB per token) and 256-lane workgroups with 16-token tiles (the fixture library built with
-    the alternative kernel shapes) -- on the same inputs: out, tc, p and next_prior bitwise equal (each row sums its
-    sources in the same order, and the softmax spreads a token over 16 lanes in both), with and without the
-    iteration-end blend, over ragged token counts."""
+def test_read_forward_launch_shapes_agree_bitwise(dtype, d, n, T, blend):
+    """ldr_read_fwd in its two launch shapes -- 512-lane workgroups (the product library, for reads of at least
+    28 KiB of rows per token) with 32-token tiles, or 16-token tiles for rows of 4-8 KiB (fp32 rows of 2048, bf16 rows
+    of 3072), and 256-lane workgroups with 16-token tiles, 8-token ones for rows of 4-8 KiB (the fixture library built
+    with the alternative kernel shapes) -- on the same inputs: out, tc, p and next_prior bitwise equal (each row sums
+    its sources in the same order, and the softmax spreads a token over the same lanes in both: 16, or 32 for rows of
+    4-8 KiB), with and without the iteration-end blend, over ragged token counts."""
     import ctypes
     from loopback_amd import _lib as L
     from loopback_amd import build as B
@@ -132,26 +135,27 @@ def test_read_forward_launch_shapes_agree_bitwise(d, n, T, blend):
     res, args = L.SIGNATURES["ldr_read_fwd"]
     fns = [L.LIB.ldr_read_fwd, other.ldr_read_fwd]
     fns[1].restype, fns[1].argtypes = res, args
+    dt, code = (torch.float32, L.F32) if dtype == "fp32" else (torch.bfloat16, L.BF16)
     gen = torch.Generator().manual_seed(d + 13 * n + T + int(blend))
-    V = [(torch.randn(T, d, generator=gen) * (0.5 + 0.05 * i)).to(torch.bfloat16).to(DEV) for i in range(n)]
+    V = [(torch.randn(T, d, generator=gen) * (0.5 + 0.05 * i)).to(dt).to(DEV) for i in range(n)]
     R = [(torch.rand(T, generator=gen) + 0.5).to(DEV) for _ in range(n)]
     dots = (torch.randn(n, T, generator=gen) * 3.0).to(DEV)
-    base = torch.randn(T, d, generator=gen).to(torch.bfloat16).to(DEV)
-    h0 = torch.randn(T, d, generator=gen).to(torch.bfloat16).to(DEV)
+    base = torch.randn(T, d, generator=gen).to(dt).to(DEV)
+    h0 = torch.randn(T, d, generator=gen).to(dt).to(DEV)
     cbar = (torch.rand(T, n, generator=gen) + 0.1).to(DEV)
     c0 = (torch.rand(n, generator=gen) + 0.1).to(DEV)
     vp = L.u64_array([v.data_ptr() for v in V])
     rp = L.u64_array([r.data_ptr() for r in R])
     st = torch.cuda.current_stream().cuda_stream
-    print(f"case read shapes d{d} n{n} T{T} blend={blend}", flush=True)
+    print(f"case read shapes {dtype} d{d} n{n} T{T} blend={blend}", flush=True)
     outs = []
     for fn in fns:
-        out = torch.empty(T, d, dtype=torch.bfloat16, device=DEV)
+        out = torch.empty(T, d, dtype=dt, device=DEV)
         tc, p = torch.empty(T, n, device=DEV), torch.empty(T, n, device=DEV)
         nxt = torch.empty(n, device=DEV)
         L.check(fn(vp, rp, n, dots.data_ptr(), T, base.data_ptr(), h0.data_ptr() if blend else None, 0.75,
                    cbar.data_ptr(), n, c0.data_ptr(), n, 0.25 if blend else 1.0, d ** -0.5, out.data_ptr(),
-                   tc.data_ptr(), p.data_ptr(), nxt.data_ptr(), T, d, L.BF16, st), "read_fwd")
+                   tc.data_ptr(), p.data_ptr(), nxt.data_ptr(), T, d, code, st), "read_fwd")
         torch.cuda.synchronize()
         outs.append((out.cpu(), tc.cpu(), p.cpu(), nxt.cpu()))
     for a, b in zip(*outs):
