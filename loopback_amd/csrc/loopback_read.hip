@@ -107,6 +107,9 @@
 #ifndef LDR_RF_GRID
 #define LDR_RF_GRID 512      // read forward: workgroups (2 per CU: all resident, each takes token tiles in turn)
 #endif
+#ifndef LDR_ON_PD_VPT4
+#define LDR_ON_PD_VPT4 1     // one-pass online read at 4 vectors per lane: sources in flight per row (2 spilled 36-120
+#endif                       // bytes to scratch: c4 online read bf16 7.38 -> 7.05 ms, fp32 15.88 -> 15.08 ms per pass)
 #ifndef LDR_ON_GRID
 #define LDR_ON_GRID 512      // one-pass online read: workgroups (2 per CU: all resident, each takes rows in turn)
 #endif
@@ -158,7 +161,7 @@ static_assert(LDR_AS_MAX_VPT_F32 >= 1 && LDR_AS_MAX_VPT_F32 <= 4, "vectors per l
 static_assert(LDR_B1_C >= 0 && LDR_B1_C <= 8, "backward pass 1: 0 (by vectors per lane) or 1..8 sources per chunk");
 static_assert(LDR_B1_GD64 == 0 || LDR_B1_GD64 == 1, "backward pass 1: LDR_B1_GD64 is 0 or 1");
 static_assert(LDR_B1_KEEP_LAST == 0 || LDR_B1_KEEP_LAST == 1, "backward pass 1: LDR_B1_KEEP_LAST is 0 or 1");
-static_assert(LDR_ON_PD >= 1 && LDR_ON_WAVES >= 1, "online read: at least one source in flight, one wave per SIMD");
+static_assert(LDR_ON_PD >= 1 && LDR_ON_PD_VPT4 >= 1 && LDR_ON_WAVES >= 1, "online read: at least one source in flight, one wave per SIMD");
 static_assert(LDR_AS_GRID >= 1 && LDR_RF_GRID >= 1 && LDR_ON_GRID >= 1 && LDR_B1_GRID >= 1 && LDR_RF_BIG_GRID >= 1,
               "grids: >= 1 workgroup");
 
@@ -2705,7 +2708,9 @@ int fill_src(SrcTab& s, const uint64_t* v, const uint64_t* r, int64_t n, int64_t
 
 template <int VPT> struct Chunk { static constexpr int C = VPT == 1 ? 8 : 4; };
 // one-pass online read: sources in flight per row (enough bytes in flight to cover the HBM latency)
-template <int VPT> struct OnlineDepth { static constexpr int PD = VPT <= 2 ? 2 * LDR_ON_PD : LDR_ON_PD; };
+template <int VPT> struct OnlineDepth {
+  static constexpr int PD = VPT <= 2 ? 2 * LDR_ON_PD : VPT >= 4 ? LDR_ON_PD_VPT4 : LDR_ON_PD;
+};
 // backward pass 1: sources per row reduction (one LDS exchange per chunk when a row spans two waves)
 template <int VPT> struct B1Chunk { static constexpr int C = LDR_B1_C > 0 ? LDR_B1_C : (VPT == 1 ? 8 : VPT == 2 ? 4 : 1); };
 
