@@ -4,7 +4,7 @@ reference read) in fp64 on the same inputs, run on the GPU beside the HIP chain 
 the CPU's time. Every token and every gradient is compared: the final state, dL/dh0, every dL/dD_s and dL/dquery,
 each within the fp32 bar of the target, max-abs error <= 1e-5 x RMS of the exact value. Both score modes (stored at
 the write / formed by the read), both glue settings (the caller's torch glue around FusedDattnReadStk, as the
-reference trainer calls it, and the glue in the kernels). At this size the reads run the 512-lane launch with 8-token
+reference trainer calls it, and the glue in the kernels). At this size the reads run the 512-lane launch with 16-token
 tiles (fp32 rows of 8 KiB) and every grid-capped kernel takes several tiles per workgroup.
 
 The fp32 oracle chain (the literal reference read in fp32, also on the GPU) is measured beside it and printed, so a
