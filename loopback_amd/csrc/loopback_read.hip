@@ -654,6 +654,15 @@ __global__ __launch_bounds__(WG) void k_rstd_bwd_any(const T* __restrict__ x, co
 // chunk of up to 64 query rows, and 256 lanes form the 32 x nq dot products (lane = token + 32 * query group).
 // ---------------------------------------------------------------------------------------------------------------
 
+// The write kernels load h -- the block's output the caller has just written, which the read that follows takes
+// as its base -- non-temporally: the read forward after it runs 6.62 -> 6.40 ms per pass at config 4 and the write
+// itself 1.28 -> 1.24; fp32: the read forward 14.22 -> 13.80 ms (x loaded so too made the write slower and the read
+// no faster)
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+  const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(t[0], t[1], t[2], t[3]);
+}
+
 template <typename T>
 __global__ __launch_bounds__(WG) void k_write_dots(const T* __restrict__ h, const T* __restrict__ x,
                                                    T* __restrict__ v, float* __restrict__ r,
@@ -884,7 +893,7 @@ __global__ __launch_bounds__(WG) void k_write_mfma(const T* __restrict__ h, cons
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const int cc = col + WM_HS * hf < d ? col + WM_HS * hf : 0;
-        hr[mb][hf] = *reinterpret_cast<const uint4*>(h + roff[mb] + cc);
+        hr[mb][hf] = ld_nt16(h + roff[mb] + cc);
         xr[mb][hf] = *reinterpret_cast<const uint4*>(x + roff[mb] + cc);
       }
   };
@@ -1035,7 +1044,7 @@ __global__ __launch_bounds__(WG) void k_write_rows(const T* __restrict__ h, cons
     const int col = st * KS + lr * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      hr[i] = *reinterpret_cast<const uint4*>(h + rof[i] + col);
+      hr[i] = ld_nt16(h + rof[i] + col);   // non-temporal: see ld_nt16
       xr[i] = *reinterpret_cast<const uint4*>(x + rof[i] + col);
     }
   };
@@ -1218,7 +1227,7 @@ __global__ __launch_bounds__(WG) void k_write_mfma32(const float* __restrict__ h
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         const int cc = col + WM_HS * hf < d ? col + WM_HS * hf : 0;
-        hr[mb][hf] = IO<float>::raw(h + roff[mb] + cc);
+        hr[mb][hf] = IO<float>::raw_str(h + roff[mb] + cc);   // non-temporal, as the 16-bit writes' h
         xr[mb][hf] = IO<float>::raw(x + roff[mb] + cc);
       }
   };
