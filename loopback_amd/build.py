@@ -24,10 +24,11 @@ SRC = os.path.join(HERE, "csrc", "loopback_read.hip")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libloopback_read.so")
 # A test fixture: the same source built with the alternative kernel shapes -- the write in the matrix cores' layout
-# for every width (LDR_WM_ROWS=0), the read forward in 256-lane workgroups for every read (LDR_RF_BIG=0) -- so the
+# for every width and dtype (LDR_WM_ROWS=0, LDR_W32_ROWS=0), the read forward in 256-lane workgroups for every read
+# (LDR_RF_BIG=0) -- so the
 # GPU tests can check that the shapes the product library picks give the same bits. Nothing else loads it.
 TEST_LIB_ALT = os.path.join(HERE, "libloopback_read_alt_shapes.so")
-ALT_DEFINES = ["LDR_WM_ROWS=0", "LDR_RF_BIG=0"]
+ALT_DEFINES = ["LDR_WM_ROWS=0", "LDR_W32_ROWS=0", "LDR_RF_BIG=0"]
 # A test program: the C ABI used from C alone (tests/c_abi/abi_smoke.c), linked against the product library.
 ABI_SMOKE_SRC = os.path.join(ROOT, "tests", "c_abi", "abi_smoke.c")
 ABI_SMOKE = os.path.join(ROOT, "tests", "c_abi", "abi_smoke")

@@ -98,6 +98,9 @@
 #ifndef LDR_WM_ROWS
 #define LDR_WM_ROWS 1        // write: rows streamed whole (d a multiple of 256), else in the matrix cores' layout
 #endif
+#ifndef LDR_W32_ROWS
+#define LDR_W32_ROWS 1       // fp32 write: rows streamed whole (d a multiple of 256), else in the matrix cores' layout
+#endif
 #ifndef LDR_NT
 #define LDR_NT 1             // non-temporal loads for the streamed sources
 #endif
@@ -1316,6 +1319,153 @@ __global__ __launch_bounds__(WG) void k_write_mfma32(const float* __restrict__ h
         if (tok + i < n_tok) dst[i] = sum[i];
     }
   }
+}
+
+// The fp32 write with whole rows (d a multiple of 256). Per 256-column step each wave moves 8 token rows of h and x,
+// a lane two 16-byte pieces of a row 128 columns apart, so each load instruction covers 512 consecutive bytes of
+// two rows (k_write_mfma32's layout strides 32 bytes between lanes); V is stored row-major from there and put in an
+// LDS tile, from which each wave takes its 64-column chunk of the step in k_write_mfma32's layout. The chunks per
+// wave and the order of every sum are k_write_mfma32's, so V, R and the scores are its bits.
+template <int NB>   // NB 16-query blocks scored (from block qt.b0); NB = 0: no scores
+__global__ __launch_bounds__(WG) void k_write_rows32(const float* __restrict__ h, const float* __restrict__ x,
+                                                     float* __restrict__ v, float* __restrict__ r, QTile qt,
+                                                     float* __restrict__ dots, int64_t n_tok, int d,
+                                                     int64_t dots_jstride, float eps) {
+  constexpr int NBA = NB > 0 ? NB : 1;
+  constexpr int KS = 4 * WM_KC;   // columns per step
+  __shared__ f32x4_t s_part[4][W32_MB][NBA][64];
+  __shared__ float s_ss[4][W32_MB][16];
+  __shared__ float4 s_a[W32_TT][KS / 4 + 1];   // the step's V tile (a 16-byte pad per row)
+  const int tid = (int)threadIdx.x, w = tid >> 6, l = tid & 63, row = l & 15, quad = l >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * W32_TT;
+  f32x4_t acc[W32_MB][NBA];
+#pragma unroll
+  for (int mb = 0; mb < W32_MB; ++mb)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[mb][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[W32_MB];
+#pragma unroll
+  for (int mb = 0; mb < W32_MB; ++mb) ss[mb] = 0.f;
+  // this lane's rows in the streaming layout: 8 w + 2 i + (l / 32), i < 4; float4 columns l % 32 and 32 + l % 32
+  constexpr int RI = W32_TT / 8;
+  const int lr = l & 31, lh = l >> 5;
+  int64_t rof[RI];
+  bool rok[RI];
+#pragma unroll
+  for (int i = 0; i < RI; ++i) {
+    const int64_t tok = t0 + 8 * w + 2 * i + lh;
+    rok[i] = tok < n_tok;
+    rof[i] = (rok[i] ? tok : n_tok - 1) * (int64_t)d;
+  }
+  auto load_rows = [&](int st, uint4 (&hr)[RI][2], uint4 (&xr)[RI][2]) {
+    const int col = st * KS + lr * 4;
+#pragma unroll
+    for (int i = 0; i < RI; ++i)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        hr[i][hh] = ld_nt16(h + rof[i] + col + 128 * hh);   // non-temporal: see ld_nt16
+        xr[i][hh] = *reinterpret_cast<const uint4*>(x + rof[i] + col + 128 * hh);
+      }
+  };
+  const int nsteps = d / KS;
+  uint4 hb[RI][2], xb[RI][2];
+  load_rows(0, hb, xb);
+  for (int st = 0; st < nsteps; ++st) {
+    const int c = 4 * st + w;   // this wave's chunk of the step
+    uint4 qv[3][NBA][2];        // its query parts (cache-resident)
+#pragma unroll
+    for (int p = 0; p < 3 * (NB > 0); ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          qv[p][b][hf] = qt.qt[((((int64_t)c * qt.nbq + qt.b0 + b) * 3 + p) * 2 + hf) * 64 + l];
+    uint4 hc[RI][2], xc[RI][2];   // this step's rows; the buffer now takes the next step's
+#pragma unroll
+    for (int i = 0; i < RI; ++i)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) { hc[i][hh] = hb[i][hh]; xc[i][hh] = xb[i][hh]; }
+    if (st + 1 < nsteps) load_rows(st + 1, hb, xb);   // uniform branch
+#pragma unroll
+    for (int i = 0; i < RI; ++i)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const float4 hv = *reinterpret_cast<const float4*>(&hc[i][hh]);
+        const float4 xv = *reinterpret_cast<const float4*>(&xc[i][hh]);
+        const float4 vv = rok[i] ? make_float4(hv.x - xv.x, hv.y - xv.y, hv.z - xv.z, hv.w - xv.w)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        // non-temporal: the read that follows streams V[s] with its other sources
+        if (rok[i])
+          __builtin_nontemporal_store(u32x4{__float_as_uint(vv.x), __float_as_uint(vv.y), __float_as_uint(vv.z),
+                                            __float_as_uint(vv.w)},
+                                      reinterpret_cast<u32x4*>(v + rof[i] + st * KS + lr * 4 + 128 * hh));
+        s_a[8 * w + 2 * i + lh][lr + 32 * hh] = vv;
+      }
+    __syncthreads();
+    uint4 va[W32_MB][2][3];
+#pragma unroll
+    for (int mb = 0; mb < W32_MB; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int u4 = 16 * w + 2 * quad + 8 * hf;   // k_write_mfma32's columns 8 quad + 32 hf of chunk c
+        const float4 a = s_a[16 * mb + row][u4], b = s_a[16 * mb + row][u4 + 1];
+        const float vv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss[mb] = __builtin_fmaf(vv[k], vv[k], ss[mb]);   // k_rstd_chunks' order
+        split3(vv, va[mb][hf]);
+      }
+    __syncthreads();   // the tile is read before the next step overwrites it
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int mb = 0; mb < W32_MB; ++mb)   // a_i q_j, i + j <= 2, in k_write_mfma32's order
+#pragma unroll
+          for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j + i < 3; ++j)
+              acc[mb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va[mb][hf][i]), as_bf16x8(qv[j][b][hf]),
+                                                                   acc[mb][b], 0, 0, 0);
+  }
+#pragma unroll
+  for (int mb = 0; mb < W32_MB; ++mb) {
+    ss[mb] += __shfl_xor(ss[mb], 16, 64);
+    ss[mb] += __shfl_xor(ss[mb], 32, 64);
+    if (quad == 0) s_ss[w][mb][row] = ss[mb];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) s_part[w][mb][b][l] = acc[mb][b];
+  }
+  __syncthreads();
+  if (tid < 16 * W32_MB) {
+    const int mb = tid >> 4, rr = tid & 15;
+    const float tot = ((s_ss[0][mb][rr] + s_ss[1][mb][rr]) + s_ss[2][mb][rr]) + s_ss[3][mb][rr];
+    const int64_t tok = t0 + tid;
+    if (tok < n_tok) r[tok] = rsqrtf(tot / (float)d + eps);
+  }
+  if constexpr (NB > 0) {   // the scores (NB = 0 writes none)
+    for (int e = tid; e < W32_MB * NB * 64; e += WG) {
+      const int mb = e / (NB * 64), rem = e - mb * NB * 64, b = rem >> 6, ll = rem & 63;
+      const f32x4_t sum = ((s_part[0][mb][b][ll] + s_part[1][mb][b][ll]) + s_part[2][mb][b][ll]) + s_part[3][mb][b][ll];
+      const int jj = 16 * (qt.b0 + b) + (ll & 15);   // the query; dots points at query j_lo's slice
+      if (jj < qt.j_lo || jj >= qt.nq) continue;
+      const int64_t tok = t0 + 16 * mb + 4 * (ll >> 4);
+      float* dst = dots + (int64_t)(jj - qt.j_lo) * dots_jstride + tok;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (tok + i < n_tok) dst[i] = sum[i];
+    }
+  }
+}
+
+// the fp32 write kernel: rows streamed whole when d is whole 256-column steps (LDR_W32_ROWS), else the matrix
+// cores' layout; both give the same bits
+template <int NB>
+auto write32_kernel(bool rows) {
+  if constexpr (LDR_W32_ROWS) {
+    if (rows) return &k_write_rows32<NB>;
+  }
+  return &k_write_mfma32<NB>;
 }
 
 // the write kernel for bf16 updates: rows streamed whole when d is whole 256-column steps (and the build keeps
@@ -2879,18 +3029,18 @@ int ldr_write_dots(const void* h, const void* x, void* v_out, float* r_out, cons
     const float* hf = static_cast<const float*>(h);
     const float* xf = static_cast<const float*>(x);
     float* vf = static_cast<float*>(v_out);
+    const bool rows = d % (4 * WM_KC) == 0;   // rows streamed whole when d is whole steps
+#define LDR_W32_LAUNCH(NBV)                                                                                   \
+  hipLaunchKernelGGL((write32_kernel<NBV>(rows)), dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok, \
+                     (int)d, dots_jstride, eps)
     switch (nb) {
-      case 0: hipLaunchKernelGGL(k_write_mfma32<0>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
-                                 (int)d, dots_jstride, eps); break;
-      case 1: hipLaunchKernelGGL(k_write_mfma32<1>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
-                                 (int)d, dots_jstride, eps); break;
-      case 2: hipLaunchKernelGGL(k_write_mfma32<2>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
-                                 (int)d, dots_jstride, eps); break;
-      case 3: hipLaunchKernelGGL(k_write_mfma32<3>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
-                                 (int)d, dots_jstride, eps); break;
-      default: hipLaunchKernelGGL(k_write_mfma32<4>, dim3(grid), dim3(WG), 0, st, hf, xf, vf, r_out, qtl, dots, n_tok,
-                                  (int)d, dots_jstride, eps); break;
+      case 0: LDR_W32_LAUNCH(0); break;
+      case 1: LDR_W32_LAUNCH(1); break;
+      case 2: LDR_W32_LAUNCH(2); break;
+      case 3: LDR_W32_LAUNCH(3); break;
+      default: LDR_W32_LAUNCH(4); break;
     }
+#undef LDR_W32_LAUNCH
   } else if (!valu) {   // matrix-core scores from the operand table of the nq queries (bf16 and fp16 updates)
     const unsigned grid = (unsigned)cdiv(n_tok, WM_TT);
     const int nbq = (int)query_blocks(nq), b0 = (int)(j_lo / 16);

@@ -73,15 +73,16 @@ def test_blend_sum_bitwise(dtype, m, T, d, per_read):
 @pytest.mark.parametrize("d", [256, 2048, 8192])
 @pytest.mark.parametrize("nq", [0, 1, 16, 17, 32, 40, 63])
 @pytest.mark.parametrize("T", [1, 77, 333])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_whole_row_write_is_the_matrix_core_write_bitwise(d, nq, T, dtype):
     """k_write_rows (rows streamed whole, the write for widths that are multiples of 256) against k_write_mfma (the
-    matrix cores' layout), bf16 and fp16 updates, on the same inputs through the C ABI, scoring the last nq of 64
+    matrix cores' layout), bf16 and fp16 updates, and k_write_rows32 against k_write_mfma32 for fp32 updates
+    (three bf16 parts per value), on the same inputs through the C ABI, scoring the last nq of 64
     queries (so the first 16-query block scored starts inside the table at every nq not a multiple of 16): V, R and
     the scores bitwise
     equal (the same chunks per wave, operands and order of every sum), the scores within 1e-5 x RMS of an fp64
-    product. k_write_mfma comes from the test fixture library built with the alternative kernel shapes
-    (LDR_WM_ROWS=0; loopback_amd.build builds it beside the product library)."""
+    product. k_write_mfma and k_write_mfma32 come from the test fixture library built with the alternative kernel
+    shapes (LDR_WM_ROWS=0, LDR_W32_ROWS=0; loopback_amd.build builds it beside the product library)."""
     import ctypes
     from loopback_amd import _lib as L
     from loopback_amd import build as B
