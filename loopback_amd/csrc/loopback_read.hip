@@ -492,6 +492,24 @@ __device__ __forceinline__ float coef_cbar(const Coef& c, int64_t tok, int i) {
   return i < c.cbar_cols ? c.lam * c.cbar[tok * c.cbar_cols + i] : c.lam;
 }
 
+// coef_cbar in two halves, for the tile prologues, which issue all their loads before the first is used: the load,
+// always issued at an in-bounds address (its column clamped; `spare`, any readable float, when there is no cbar
+// column), and the value formed from it. A load under a per-lane condition is waited for where the two paths meet
+// (the other path writes its register), one memory round trip per call.
+__device__ __forceinline__ float cbar_load(const Coef& c, int64_t tok, int i, const float* spare) {
+  const float* p = c.cbar_cols > 0 ? c.cbar + (tok * c.cbar_cols + min(i, c.cbar_cols - 1)) : spare;
+  return *p;
+}
+// a scale row's address kept in LDS, as a global-memory pointer: loaded from LDS, a plain pointer is generic and
+// its loads flat ones, which the compiler waits for with the LDS reads
+typedef const __attribute__((address_space(1))) float* gptr_f32;
+__device__ __forceinline__ gptr_f32 as_global(const float* p) { return (gptr_f32)p; }
+
+__device__ __forceinline__ float cbar_value(const Coef& c, float loaded, int i) {
+#pragma clang fp contract(off)   // as coef_cbar
+  return i < c.cbar_cols ? c.lam * loaded : c.lam;
+}
+
 // x, as a value the compiler cannot see through: index math formed from it inside a tile loop is formed again in
 // each pass instead of hoisted out of the loop, where its registers would stay live through the row stream
 __device__ __forceinline__ int opaque(int x) {
@@ -1604,12 +1622,15 @@ __global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float
   float* s_l = s_big;
   __shared__ float s_w[TT_MAX * SP];           // cbar, then the weights [t][i]
   __shared__ float s_c0[MAXS], s_lc[MAXS], s_p0[MAXS], s_M;
+  __shared__ gptr_f32 s_rp[MAXS];   // the sources' scale rows (see fetch)
   const Rows R(d, tpr, NTH);
   const int tid = (int)threadIdx.x;
   // A tile's scores, scales and cbar, PRO_K entries per lane at a time: fetch issues a chunk's loads (clamped
   // in-bounds addresses; none is used before all are issued), commit writes the logits and cbar to LDS -- a memory
   // round trip per chunk instead of one per entry. Their lane index is opaque, so the index math is formed in each
-  // tile (hoisted out of the tile loop, its registers would stay live through the row stream).
+  // tile (hoisted out of the tile loop, its registers would stay live through the row stream). A lane's scale
+  // addresses come from LDS: read from the kernel's argument table at a per-lane index, each would be a memory
+  // round trip of its own before its load.
   const int nt = n * tt;
   float zv[PRO_K], rv[PRO_K], cv[PRO_K];
   auto fetch = [&](int64_t t0, int c) {
@@ -1620,9 +1641,9 @@ __global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float
       const int i = idx / tt, t = idx - i * tt;                  // source-major: coalesced over tokens
       const int64_t tok = min(t0 + t, n_tok - 1);
       zv[k] = dots[(int64_t)i * dots_stride + tok];
-      rv[k] = src.r[i][tok];
+      rv[k] = s_rp[i][tok];
       const int t2 = idx / n, i2 = idx - t2 * n;                 // token-major: coalesced over [tok][i]
-      cv[k] = coef_cbar(cf, min(t0 + t2, n_tok - 1), i2);
+      cv[k] = cbar_load(cf, min(t0 + t2, n_tok - 1), i2, dots);
     }
   };
   auto commit = [&](int64_t t0, int c) {
@@ -1636,11 +1657,12 @@ __global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float
         if (t0 + t < n_tok) l = zv[k] * rv[k] * inv + s_lc[i];
         s_l[i * (TT_MAX + 1) + t] = l;
         const int t2 = idx / n, i2 = idx - t2 * n;
-        s_w[t2 * SP + i2] = t0 + t2 < n_tok ? cv[k] : 0.f;
+        s_w[t2 * SP + i2] = t0 + t2 < n_tok ? cbar_value(cf, cv[k], i2) : 0.f;
       }
     }
   };
   const int64_t tiles = (n_tok + tt - 1) / tt;
+  if (tid < n) s_rp[tid] = as_global(src.r[tid]);   // visible after load_prior's barriers
   load_prior(cf, n, s_c0, s_lc, &s_M);
   const float M = s_M;
   if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
@@ -1801,11 +1823,13 @@ void k_read_online(SrcTab src, int n, const float* __restrict__ q, float* __rest
   __shared__ float s_c0[MAXS], s_lc[MAXS], s_p0[MAXS], s_M;
   __shared__ __align__(16) float s_q[64 * 4 * 8];   // the query, zero past d (rows of <= 64 lanes x 4 vectors)
   __shared__ int s_qnz;
+  __shared__ gptr_f32 s_rp[MAXS];   // the sources' scale rows, as in the read forward's prologue
   using Raw = typename IO<T>::Raw;
   const Rows R(d, tpr);
   const int tid = (int)threadIdx.x;
   if (tid == 0) s_qnz = 0;
-  load_prior(cf, n, s_c0, s_lc, &s_M);   // barriers inside: s_qnz is cleared before anyone sets it
+  if (tid < n) s_rp[tid] = as_global(src.r[tid]);
+  load_prior(cf, n, s_c0, s_lc, &s_M);   // barriers inside: s_qnz is cleared before anyone sets it, s_rp is seen
   const float M = s_M;
   if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
   bool nz = false;
@@ -1842,9 +1866,10 @@ void k_read_online(SrcTab src, int n, const float* __restrict__ q, float* __rest
     const int64_t tk = valid ? tok : n_tok - 1;   // rows past the end recompute the last token, store nothing
     const int64_t roff = tk * (int64_t)d;
     for (int i = R.lr; i < n; i += tpr) {           // the row's per-source scalars, spread over its lanes
-      const float cb = coef_cbar(cf, tk, i);
+      const float cb = cbar_value(cf, cbar_load(cf, tk, i, q), i);   // both loads out before either is used
+      const float rv = s_rp[i][tk];
       wt[i] = qz ? s_c0[i] - cb : (s_c0[i] - cb) - M * s_p0[i];
-      rsc[i] = src.r[i][tk];
+      rsc[i] = rv;
     }
     auto load_src = [&](int i, Raw (&rw)[VPT]) {
 #pragma unroll
@@ -2000,6 +2025,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
   typedef typename std::conditional<GD64, double, float>::type Acc;
   __shared__ float lds[6 * TT_MAX * SP];
   __shared__ float s_sacc[TT_MAX], s_c0[MAXS], s_lc[MAXS], s_M;
+  __shared__ gptr_f32 s_rp[MAXS];   // the sources' scale rows, as in the read forward's prologue
   __shared__ Acc red[4 * C];
   float* s_p = lds;
   float* s_r = lds + 1 * TT_MAX * SP;
@@ -2013,7 +2039,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
   // addresses; none is used before all are issued), commit writes them to LDS -- a memory round trip per chunk
   // instead of one per entry (the lane index opaque, as in the read forward).
   const int nt = n * tt;
-  float pv[PRO_K], gv[PRO_K], wv[PRO_K], rv[PRO_K], zv[PRO_K];
+  float pv[PRO_K], gv[PRO_K], wv[PRO_K], cv[PRO_K], rv[PRO_K], zv[PRO_K];
+  const float* gtp = gt ? gt : prob;   // without gt: prob's entries loaded and not used (a load under no condition)
   auto fetch = [&](int64_t t0, int c) {
     const int lane = opaque(tid) + c;
 #pragma unroll
@@ -2022,11 +2049,12 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
       const int t = idx / n, i = idx - t * n;                    // token-major: [tok][i]
       const int64_t tok = min(t0 + t, n_tok - 1);
       pv[k] = prob[tok * n + i];
-      gv[k] = gt ? gt[tok * n + i] : 0.f;
-      wv[k] = tcp[tok * n + i] - coef_cbar(cf, tok, i);
+      gv[k] = gtp[tok * n + i];
+      wv[k] = tcp[tok * n + i];
+      cv[k] = cbar_load(cf, tok, i, tcp);
       const int i2 = idx / tt, t2 = idx - i2 * tt;               // source-major: scales and raw scores
       const int64_t tok2 = min(t0 + t2, n_tok - 1);
-      rv[k] = src.r[i2][tok2];
+      rv[k] = s_rp[i2][tok2];
       zv[k] = dots[i2 * dots_stride + tok2];
     }
   };
@@ -2039,8 +2067,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
         const int t = idx / n, i = idx - t * n;
         const bool ok = t0 + t < n_tok;
         s_p[t * SP + i] = ok ? pv[k] : 0.f;
-        s_gt[t * SP + i] = ok ? gv[k] : 0.f;
-        s_w[t * SP + i] = ok ? wv[k] : 0.f;
+        s_gt[t * SP + i] = ok && gt ? gv[k] : 0.f;
+        s_w[t * SP + i] = ok ? wv[k] - cbar_value(cf, cv[k], i) : 0.f;
         const int i2 = idx / tt, t2 = idx - i2 * tt;
         const bool ok2 = t0 + t2 < n_tok;
         s_r[t2 * SP + i2] = ok2 ? rv[k] : 1.f;
@@ -2049,6 +2077,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
     }
   };
   const int64_t tiles = (n_tok + tt - 1) / tt;
+  if (tid < n) s_rp[tid] = as_global(src.r[tid]);   // visible after load_prior's barriers
   load_prior(cf, n, s_c0, s_lc, &s_M);
   const float M = s_M;
   float dqa[VPT][8];
@@ -2056,26 +2085,46 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
   for (int v = 0; v < VPT; ++v)
 #pragma unroll
     for (int k = 0; k < 8; ++k) dqa[v][k] = 0.f;
+  const int nfull = (n - LDR_B1_KEEP_LAST) - (n - LDR_B1_KEEP_LAST) % C;   // sources in whole chunks
+  const int rows_per_slot = (tt + R.rpw - 1) / R.rpw;
+  typename IO<T>::Raw gq[VPT];     // the row's g, kept packed (fewer registers), unpacked where used
+  typename IO<T>::Raw cur[C][VPT];  // the row's chunk of sources being reduced
+  auto load_chunk = [&](int64_t roff, int i0, typename IO<T>::Raw (&rw)[C][VPT]) {
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) rw[c][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0 + c]) + roff + R.off(v));
+  };
+  // a row's first loads: its g and its first chunk of sources
+  auto start_row = [&](int64_t t0, int rk) {
+    const int64_t tok = t0 + R.rs + rk * R.rpw;
+    const int64_t roff = (tok < n_tok ? tok : n_tok - 1) * (int64_t)d;
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+      gq[v] = IO<T>::raw(g + roff + R.off(v));   // just written by the caller: cached, not streamed
+      if (!R.act(v)) gq[v] = IO<T>::zero();
+    }
+    if (nfull > 0) load_chunk(roff, 0, cur);
+  };
   for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int64_t t0 = tile * tt;
+    // the tile's first row is requested after the prologue's first loads and before they are waited for (waiting
+    // for older loads does not wait for younger ones), so the prologue's round trip overlaps the row stream's start
+    fetch(t0, 0);
+    start_row(t0, 0);
+    commit(t0, 0);
 #pragma unroll 1
-    for (int c = 0; c < nt; c += PRO_K * WG) {
+    for (int c = PRO_K * WG; c < nt; c += PRO_K * WG) {
       fetch(t0, c);
       commit(t0, c);
     }
     __syncthreads();
-    const int rows_per_slot = (tt + R.rpw - 1) / R.rpw;
     for (int rk = 0; rk < rows_per_slot; ++rk) {   // uniform trip count: row_sum may hold barriers
       const int rr = R.rs + rk * R.rpw;            // < tt: tt is a multiple of rpw
       const int64_t tok = t0 + rr;
       const bool valid = tok < n_tok;
       const int64_t roff = (valid ? tok : n_tok - 1) * (int64_t)d;
-      typename IO<T>::Raw gq[VPT];   // g kept packed (fewer registers), unpacked where used
-#pragma unroll
-      for (int v = 0; v < VPT; ++v) {
-        gq[v] = IO<T>::raw(g + roff + R.off(v));   // just written by the caller: cached, not streamed
-        if (!R.act(v)) gq[v] = IO<T>::zero();
-      }
+      if (rk > 0) start_row(t0, rk);
       if ((g_prop || g_h0) && valid) {   // the blend's gradients: beta g to h0, g - beta g to the proposal
 #pragma clang fp contract(off)   // a product and a difference, each rounded as autograd rounds them (no fma)
 #pragma unroll
@@ -2142,19 +2191,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
         else
           row_sum(pd, tpr, red);
       };
-      auto load_chunk = [&](int i0, typename IO<T>::Raw (&rw)[C][VPT]) {
-#pragma unroll
-        for (int c = 0; c < C; ++c)
-#pragma unroll
-          for (int v = 0; v < VPT; ++v) rw[c][v] = IO<T>::raw_nt(static_cast<const T*>(src.v[i0 + c]) + roff + R.off(v));
-      };
       int i0 = 0;
-      const int nfull = (n - LDR_B1_KEEP_LAST) - (n - LDR_B1_KEEP_LAST) % C;
-      typename IO<T>::Raw cur[C][VPT];
-      if (nfull > 0) load_chunk(0, cur);
       for (; i0 < nfull; i0 += C) {   // the next chunk's loads in flight while this one is reduced
         typename IO<T>::Raw nxt[C][VPT];
-        if (i0 + C < nfull) load_chunk(i0 + C, nxt);
+        if (i0 + C < nfull) load_chunk(roff, i0 + C, nxt);
         Acc pd[C];
 #pragma unroll
         for (int c = 0; c < C; ++c) pd[c] = dotc(cur[c]);
