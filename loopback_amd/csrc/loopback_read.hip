@@ -2493,20 +2493,52 @@ __global__ __launch_bounds__(WG) void k_dv_assemble(AsmTab tab, int m, const T* 
       for (int v = 0; v < VPT; ++v) load_f32x8(tab.q[m - 1] + R.off(v), qv[v]);
       take_row(last, sc, qv);
     }
+    // the tile's last loads, all requested before the first is used (the scales and their gradients and, for 16-bit
+    // rows, the updates' rows and the added gradient's rows): per token row in turn they were two memory round trips
+    // each (c4: the update gradients 6.44 -> 6.29 ms per pass). fp32 rows, and rows of 3 or more vectors per lane,
+    // load per token row still: their registers would cost some instantiations a wave per SIMD (the fp32 update
+    // gradients 14.41 -> 14.66 ms with only the scales' loads taken first).
+    constexpr bool EPI_ROWS = !std::is_same<T, float>::value && VPT <= 2;
+    constexpr int ER = EPI_ROWS ? AS_RB : 1;
+    float rs[ER], grs[ER];
+    typename IO<T>::Raw er[ER][VPT], ar[ER][VPT];
+    if constexpr (EPI_ROWS) {
+      const float* grp = gr ? gr : r;   // without gr: r's entries loaded again and not used
+#pragma unroll
+      for (int k = 0; k < ER; ++k) {
+        rs[k] = r[tokc[k]];
+        grs[k] = grp[tokc[k]];
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) er[k][v] = IO<T>::raw(vsrc + roff[k] + R.off(v));
+      }
+      if (!ADD_LAST && add) {
+#pragma unroll
+        for (int k = 0; k < ER; ++k)
+#pragma unroll
+          for (int v = 0; v < VPT; ++v) ar[k][v] = IO<T>::raw(add + roff[k] + R.off(v));
+      }
+    }
 #pragma unroll
     for (int k = 0; k < AS_RB; ++k) {
-      const float rv = r[tokc[k]];
-      const float c = gr ? gr[tokc[k]] * (-rv * rv * rv) / (float)d : 0.f;
+      const int ke = EPI_ROWS ? k : 0;
+      const float rv = EPI_ROWS ? rs[ke] : r[tokc[k]];
+      const float c = gr ? (EPI_ROWS ? grs[ke] : gr[tokc[k]]) * (-rv * rv * rv) / (float)d : 0.f;
       float e[VPT][8], a[VPT][8];
 #pragma unroll
-      for (int v = 0; v < VPT; ++v) IO<T>::load(vsrc + roff[k] + R.off(v), e[v]);
+      for (int v = 0; v < VPT; ++v) {
+        if constexpr (EPI_ROWS) IO<T>::unpack(er[ke][v], e[v]);
+        else IO<T>::load(vsrc + roff[k] + R.off(v), e[v]);
+      }
       if (add) {   // a gradient of the write's h from elsewhere, added as autograd would add it
         if (ADD_LAST) {   // the rows already in registers
 #pragma unroll
           for (int v = 0; v < VPT; ++v) IO<T>::unpack(last[k][v], a[v]);
         } else {
 #pragma unroll
-          for (int v = 0; v < VPT; ++v) IO<T>::load(add + roff[k] + R.off(v), a[v]);
+          for (int v = 0; v < VPT; ++v) {
+            if constexpr (EPI_ROWS) IO<T>::unpack(ar[ke][v], a[v]);
+            else IO<T>::load(add + roff[k] + R.off(v), a[v]);
+          }
         }
         if (add_beta != 0.f) {   // add is the output gradient g of an iteration-end blend: its proposal's share
 #pragma clang fp contract(off)
