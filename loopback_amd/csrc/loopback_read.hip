@@ -1833,8 +1833,13 @@ void k_read_online(SrcTab src, int n, const float* __restrict__ q, float* __rest
   const float M = s_M;
   if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
   bool nz = false;
-  for (int k = tid; k < 64 * 4 * 8; k += WG) {
-    const float x = k < d ? q[k] : 0.f;
+  float qk[64 * 4 * 8 / WG];   // every load out before the first is used (at a clamped column, the value then zeroed)
+#pragma unroll
+  for (int j = 0; j < 64 * 4 * 8 / WG; ++j) qk[j] = q[min(tid + j * WG, d - 1)];
+#pragma unroll
+  for (int j = 0; j < 64 * 4 * 8 / WG; ++j) {
+    const int k = tid + j * WG;
+    const float x = k < d ? qk[j] : 0.f;
     s_q[k] = x;
     nz |= x != 0.f;
   }
@@ -1865,23 +1870,28 @@ void k_read_online(SrcTab src, int n, const float* __restrict__ q, float* __rest
     const bool valid = tok < n_tok;
     const int64_t tk = valid ? tok : n_tok - 1;   // rows past the end recompute the last token, store nothing
     const int64_t roff = tk * (int64_t)d;
+    auto load_src = [&](int i, Raw (&rw)[VPT]) {
+#pragma unroll
+      for (int v = 0; v < VPT; ++v) rw[v] = IO<T>::raw_str(static_cast<const T*>(src.v[i]) + roff + R.off(v));
+    };
+    // the row's first sources and its base are requested before its scalars, so one memory round trip brings all
+    // three (the scalars first were two: theirs, then the rows')
+    Raw buf[PD][VPT];   // a ring of PD sources in flight: source i lives in buf[i % PD]
+#pragma unroll
+    for (int j = 0; j < PD; ++j)
+      if (j < n) load_src(j, buf[j]);
+    Raw braw[VPT];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) braw[v] = IO<T>::raw(base + roff + R.off(v));
     for (int i = R.lr; i < n; i += tpr) {           // the row's per-source scalars, spread over its lanes
       const float cb = cbar_value(cf, cbar_load(cf, tk, i, q), i);   // both loads out before either is used
       const float rv = s_rp[i][tk];
       wt[i] = qz ? s_c0[i] - cb : (s_c0[i] - cb) - M * s_p0[i];
       rsc[i] = rv;
     }
-    auto load_src = [&](int i, Raw (&rw)[VPT]) {
-#pragma unroll
-      for (int v = 0; v < VPT; ++v) rw[v] = IO<T>::raw_str(static_cast<const T*>(src.v[i]) + roff + R.off(v));
-    };
-    Raw buf[PD][VPT];   // a ring of PD sources in flight: source i lives in buf[i % PD]
-#pragma unroll
-    for (int j = 0; j < PD; ++j)
-      if (j < n) load_src(j, buf[j]);
     float acc[VPT][8], P[VPT][8];
 #pragma unroll
-    for (int v = 0; v < VPT; ++v) IO<T>::load(base + roff + R.off(v), acc[v]);
+    for (int v = 0; v < VPT; ++v) IO<T>::unpack(braw[v], acc[v]);
     if (BLEND) {   // iteration end: base = proposal + beta (h0 - proposal), each step rounded as the caller's ops
 #pragma clang fp contract(off)   // three separately rounded operations, as torch runs them (no fused multiply-add)
 #pragma unroll
