@@ -306,3 +306,70 @@ def test_any_shape_refuses_graph_capture():
             with torch.cuda.graph(graph, stream=side):
                 cell.combine(prop, h0, xs, coeffs, prior, 0, n - 1)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d", [256, 8192])
+def test_one_source_without_coefficient_columns(dtype, d):
+    """A read of one source with no stored cbar or prior column (cbar_cols = c0_cols = 0: the newest column implied,
+    lam) against the same read given those columns explicitly as ones (lam x 1 = lam), through the C ABI: the read
+    forward (both scores paths; d = 8192 takes the 512-lane launch), backward pass 1 and every scalar bitwise equal.
+    The kernels load cbar at a clamped address before its column is tested; with no column they load another
+    operand's first element instead and use lam."""
+    from loopback_amd import _lib as L
+    from loopback_amd import fused_dattn as FD
+    lib = L.LIB
+    T, n = 300, 1
+    dt = lib_dtype(dtype)
+    g_ = torch.Generator().manual_seed(d + 5)
+    V = [torch.randn(T, d, generator=g_).to(dtype).to(DEV)]
+    R = [FD.rstd(V[0], 1e-6).reshape(T)]
+    q = (torch.randn(d, generator=g_) * 0.4).to(DEV)
+    base = torch.randn(T, d, generator=g_).to(dtype).to(DEV)
+    h0 = torch.randn(T, d, generator=g_).to(dtype).to(DEV)
+    g = torch.randn(T, d, generator=g_).to(dtype).to(DEV)
+    gt = torch.randn(T, n, generator=g_).to(DEV)
+    ones_t, ones_1 = torch.ones(T, 1, device=DEV), torch.ones(1, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    inv, lam = 1.0 / d ** 0.5, 0.75
+    vh, rh = _u64(L, (v.data_ptr() for v in V)), _u64(L, (r.data_ptr() for r in R))
+    print(f"case one source, no coefficient columns {dtype} d{d}", flush=True)
+
+    def check(code):
+        assert code == 0, lib.ldr_strerror(code)
+
+    res = {}
+    for cols in (0, 1):
+        # with no column the pointers are another tensor's (any readable address): nothing may be read from them
+        cbar = ones_t if cols else gt
+        c0 = ones_1 if cols else gt
+        outs = []
+        dots = torch.empty(n, T, device=DEV)
+        for online in (True, False):
+            out, tc, p, nxt = (torch.empty_like(base), torch.empty(T, n, device=DEV), torch.empty(T, n, device=DEV),
+                               torch.empty(n, device=DEV))
+            tail = (base.data_ptr(), h0.data_ptr(), 0.75, cbar.data_ptr(), cols, c0.data_ptr(), cols, lam, inv,
+                    out.data_ptr(), tc.data_ptr(), p.data_ptr(), nxt.data_ptr(), T, d, dt, st)
+            if online:
+                check(lib.ldr_read_fwd_online(vh, rh, n, q.data_ptr(), dots.data_ptr(), T, *tail))
+            else:
+                check(lib.ldr_read_fwd(vh, rh, n, dots.data_ptr(), T, *tail))
+            outs += [out, tc, p, nxt]
+        _, tc, p, _ = outs[4:]
+        dcbar = torch.empty(T, n, device=DEV)
+        dr = torch.zeros(n, T, device=DEV)
+        wz = torch.empty(n, T, 2, device=DEV)
+        parts = max(1, L.bwd1_parts(T, d))
+        dq_part = torch.empty(parts, d, device=DEV)
+        gp, gh = torch.empty_like(g), torch.empty_like(g)
+        check(lib.ldr_read_bwd1(vh, rh, n, g.data_ptr(), gt.data_ptr(), p.data_ptr(), dots.data_ptr(), T,
+                                tc.data_ptr(), cbar.data_ptr(), cols, c0.data_ptr(), cols, lam, inv, dcbar.data_ptr(),
+                                0, _u64(L, (dr[i].data_ptr() for i in range(n))), 0, wz.data_ptr(), T,
+                                dq_part.data_ptr(), d, gp.data_ptr(), gh.data_ptr(), 0.75, T, d, dt, st))
+        dq = torch.empty(d, device=DEV)
+        check(lib.ldr_reduce_rows(dq_part.data_ptr(), parts, d, dq.data_ptr(), st))
+        torch.cuda.synchronize()
+        res[cols] = outs + [dots, dr, wz, dq, gp, gh]
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+    assert torch.isfinite(res[0][0].float()).all() and res[0][2].eq(1.0).all() and res[0][6].eq(1.0).all()   # p = 1
