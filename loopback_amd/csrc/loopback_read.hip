@@ -517,13 +517,25 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
-// per-read constants from the prior: c0, lc = log(max(c0, 1e-8)), M = sum c0 (in source order)
-__device__ __forceinline__ void load_prior(const Coef& c, int n, float* s_c0, float* s_lc, float* s_M) {
+// per-read constants from the prior: c0, lc = log(max(c0, 1e-8)), M = sum c0 (in source order); and the sources'
+// scale-row addresses into s_rp as global-memory pointers (a lane's scale loads read them from LDS). The prior's
+// entry (at a clamped address; `spare`, any readable float, when there is no prior column) and the address are
+// requested together, before either is used: one memory round trip.
+__device__ __forceinline__ void load_prior(const Coef& c, int n, float* s_c0, float* s_lc, float* s_M,
+                                           const SrcTab& src, gptr_f32* s_rp, const float* spare) {
   const int t = (int)threadIdx.x;
   if (t < n) {
-    const float v = t < c.c0_cols ? c.lam * c.c0[t] : c.lam;
+    const float* p = c.c0_cols > 0 ? c.c0 + min(t, c.c0_cols - 1) : spare;
+    const float raw = *p;
+    const float* rp = src.r[t];
+    float v;
+    {
+#pragma clang fp contract(off)   // the product rounded on its own, as the caller's scaling is
+      v = t < c.c0_cols ? c.lam * raw : c.lam;
+    }
     s_c0[t] = v;
     s_lc[t] = logf(fmaxf(v, 1e-8f));
+    s_rp[t] = as_global(rp);
   }
   __syncthreads();
   if (t == 0) {
@@ -1662,8 +1674,7 @@ __global__ __launch_bounds__(NTH) void k_read_fwd(SrcTab src, int n, const float
     }
   };
   const int64_t tiles = (n_tok + tt - 1) / tt;
-  if (tid < n) s_rp[tid] = as_global(src.r[tid]);   // visible after load_prior's barriers
-  load_prior(cf, n, s_c0, s_lc, &s_M);
+  load_prior(cf, n, s_c0, s_lc, &s_M, src, s_rp, dots);
   const float M = s_M;
   if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
   const int lpt = NTH / tt;   // lanes per token in the softmax
@@ -1828,8 +1839,7 @@ void k_read_online(SrcTab src, int n, const float* __restrict__ q, float* __rest
   const Rows R(d, tpr);
   const int tid = (int)threadIdx.x;
   if (tid == 0) s_qnz = 0;
-  if (tid < n) s_rp[tid] = as_global(src.r[tid]);
-  load_prior(cf, n, s_c0, s_lc, &s_M);   // barriers inside: s_qnz is cleared before anyone sets it, s_rp is seen
+  load_prior(cf, n, s_c0, s_lc, &s_M, src, s_rp, q);   // barriers inside: s_qnz is cleared before anyone sets it
   const float M = s_M;
   if (next_prior && blockIdx.x == 0 && tid < n) next_prior[tid] = s_c0[tid];
   bool nz = false;
@@ -2087,8 +2097,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
     }
   };
   const int64_t tiles = (n_tok + tt - 1) / tt;
-  if (tid < n) s_rp[tid] = as_global(src.r[tid]);   // visible after load_prior's barriers
-  load_prior(cf, n, s_c0, s_lc, &s_M);
+  load_prior(cf, n, s_c0, s_lc, &s_M, src, s_rp, tcp);
   const float M = s_M;
   float dqa[VPT][8];
 #pragma unroll
