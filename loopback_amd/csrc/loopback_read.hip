@@ -503,7 +503,9 @@ __device__ __forceinline__ float cbar_load(const Coef& c, int64_t tok, int i, co
 // a scale row's address kept in LDS, as a global-memory pointer: loaded from LDS, a plain pointer is generic and
 // its loads flat ones, which the compiler waits for with the LDS reads
 typedef const __attribute__((address_space(1))) float* gptr_f32;
+typedef __attribute__((address_space(1))) float* gptr_f32w;
 __device__ __forceinline__ gptr_f32 as_global(const float* p) { return (gptr_f32)p; }
+__device__ __forceinline__ gptr_f32w as_global(float* p) { return (gptr_f32w)p; }
 
 __device__ __forceinline__ float cbar_value(const Coef& c, float loaded, int i) {
 #pragma clang fp contract(off)   // as coef_cbar
@@ -522,12 +524,14 @@ __device__ __forceinline__ int opaque(int x) {
 // entry (at a clamped address; `spare`, any readable float, when there is no prior column) and the address are
 // requested together, before either is used: one memory round trip.
 __device__ __forceinline__ void load_prior(const Coef& c, int n, float* s_c0, float* s_lc, float* s_M,
-                                           const SrcTab& src, gptr_f32* s_rp, const float* spare) {
+                                           const SrcTab& src, gptr_f32* s_rp, const float* spare,
+                                           const PtrTab* drt = nullptr, gptr_f32w* s_drp = nullptr) {
   const int t = (int)threadIdx.x;
   if (t < n) {
     const float* p = c.c0_cols > 0 ? c.c0 + min(t, c.c0_cols - 1) : spare;
     const float raw = *p;
     const float* rp = src.r[t];
+    if (drt) s_drp[t] = as_global(static_cast<float*>(drt->p[t]));   // (backward pass 1: the dr rows too)
     float v;
     {
 #pragma clang fp contract(off)   // the product rounded on its own, as the caller's scaling is
@@ -556,9 +560,9 @@ constexpr int WR_TT = 32, WR_KC = 128, WR_KP = WR_KC + 4, WR_MQ = 8;
 // (which store it beside the update) or by these kernels (the list layout's rstd, the stacked layout when the write
 // did not store it) -- so both layouts read with bitwise equal scales, and so bitwise equal outputs.
 //
-// Every dtype: the order of the matrix-core writes (k_write_mfma, k_write_rows, k_write_mfma32). Columns go in
-// 64-column chunks, chunk c to slot w = c mod 4; inside a chunk, quad q takes columns [8q, 8q + 8) and
-// [32 + 8q, 40 + 8q). Partial (w, q) is the fused multiply-add sum over its chunks in order, its two column groups
+// Every dtype: the order of the matrix-core writes (k_write_mfma, k_write_rows, k_write_mfma32, k_write_rows32).
+// Columns go in 64-column chunks, chunk c to slot w = c mod 4; inside a chunk, quad q takes columns [8q, 8q + 8)
+// and [32 + 8q, 40 + 8q). Partial (w, q) is the fused multiply-add sum over its chunks in order, its two column groups
 // in order, and their elements in order. Then W_w = (p_w0 + p_w1) + (p_w2 + p_w3), and
 // sum = ((W_0 + W_1) + W_2) + W_3.
 // Here a row takes 16 lanes (lane 4 w + q holds partial (w, q)), 4 rows per wave.
@@ -2046,6 +2050,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
   __shared__ float lds[6 * TT_MAX * SP];
   __shared__ float s_sacc[TT_MAX], s_c0[MAXS], s_lc[MAXS], s_M;
   __shared__ gptr_f32 s_rp[MAXS];   // the sources' scale rows, as in the read forward's prologue
+  __shared__ gptr_f32w s_drp[MAXS]; // the sources' dr rows (the same: no argument-table read per entry)
   __shared__ Acc red[4 * C];
   float* s_p = lds;
   float* s_r = lds + 1 * TT_MAX * SP;
@@ -2097,7 +2102,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
     }
   };
   const int64_t tiles = (n_tok + tt - 1) / tt;
-  load_prior(cf, n, s_c0, s_lc, &s_M, src, s_rp, tcp);
+  load_prior(cf, n, s_c0, s_lc, &s_M, src, s_rp, tcp, &dr, s_drp);
   const float M = s_M;
   float dqa[VPT][8];
 #pragma unroll
@@ -2270,7 +2275,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(2))) void k_
       const int i = idx / tt, t = idx - i * tt;
       const int64_t tok = t0 + t;
       if (tok < n_tok) {
-        float* dri = static_cast<float*>(dr.p[i]);
+        const gptr_f32w dri = s_drp[i];
         const float drv = s_dz[t * SP + i];
         dri[tok] = dr_accum ? dri[tok] + drv : drv;
         const float dz = s_gd[t * SP + i];
